@@ -1,0 +1,150 @@
+/*
+ * mround_hip.h -- C ABI of libmround_hip.so, the MI355X (gfx950) kernels of
+ * the SignRound v2 tuning path.
+ *
+ * The reference has no FFI: its hot path is a set of Python operator
+ * functions evaluated by MLX. Each entry point below replaces one of them and
+ * cites it. The Python package mround_amd binds these through ctypes
+ * (mround_amd/kernels/__init__.py) under the reference's own function names.
+ *
+ * Conventions shared by every entry point:
+ *   - All array arguments are device pointers owned by the caller; nothing
+ *     here allocates device memory. Reductions take a caller-provided
+ *     workspace whose size the matching *_workspace_bytes() query returns.
+ *   - Every call enqueues work on `stream` (a hipStream_t, NULL = default
+ *     stream) and returns without synchronising.
+ *   - The return value is MR_OK, MR_EINVAL (bad shape or argument, checked on
+ *     the host before anything is launched) or MR_EHIP - hipError_t for a HIP
+ *     runtime error. mr_last_error() gives the message for the calling thread.
+ *   - Weights are row-major (rows = out_features, cols = in_features).
+ *     Quantization groups run along cols. With group_size == -1 a whole row
+ *     is one group. Per-weight learnable perturbations (v) and codes use the
+ *     reference's grouped layout (rows, n_groups, group_size), which pads the
+ *     last group with zeros when cols % group_size != 0; per-group
+ *     quantities (alpha, beta, scale, zero point) are (rows, n_groups).
+ *   - `mode` is MR_ASYM (unsigned codes, learned zero point), MR_SYM (signed
+ *     codes, signed scale) or MR_SYM_SEARCHED (signed codes, scale =
+ *     init_scale * beta).
+ */
+#ifndef MROUND_HIP_H
+#define MROUND_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MR_OK = 0, MR_EINVAL = -22, MR_EHIP = -1000 };
+enum { MR_F32 = 0, MR_BF16 = 1, MR_F16 = 2 };
+enum { MR_ASYM = 0, MR_SYM = 1, MR_SYM_SEARCHED = 2 };
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mr_last_error(void);
+/* ABI version of this library. */
+int mr_abi_version(void);
+
+/*
+ * Fake-quantize forward: quantize and dequantize in one pass, optionally also
+ * returning the integer codes and the per-group scale and zero point.
+ * Replaces mround/core/quantizer.py:287-347 (fake_quantize) and 350-398
+ * (quantize_codes); oracle mround/reference/quantize.py:249-319.
+ *   w          (rows, cols) in w_dtype (MR_F32 / MR_BF16 / MR_F16)
+ *   v, alpha, beta  fp32 learnables, or all NULL for round-to-nearest
+ *   init_scale fp32 (rows, n_groups), required iff mode == MR_SYM_SEARCHED
+ *   wq_out     (rows, cols) in wq_dtype, or NULL
+ *   codes_out  (rows, n_groups, group_size) bytes (uint8 asym, int8 sym), or NULL
+ *   scale_out, zp_out  fp32 (rows, n_groups), or NULL (zp only for MR_ASYM)
+ */
+int mr_fq_forward(const void* w, int w_dtype, const float* v, const float* alpha,
+                  const float* beta, const float* init_scale, int64_t rows, int64_t cols,
+                  int group_size, int bits, int mode, float eps, void* wq_out, int wq_dtype,
+                  void* codes_out, float* scale_out, float* zp_out, void* stream);
+
+/*
+ * Straight-through backward fused with the sign-SGD step and the projection.
+ * Replaces the MLX autodiff of fake_quantize (oracle
+ * mround/reference/quantize.py:399-522), SignSGD.apply
+ * (mround/core/signsgd.py:125-145) and project_params
+ * (mround/core/quantizer.py:430-446), for one layer:
+ *   g        dL/dW' (rows, cols) in g_dtype
+ *   update   1: v, alpha, beta <- clip(p - lr * sign(dL/dp), bounds), in place
+ *            0: parameters untouched
+ *   grad_*_out  optional fp32 outputs of dL/dv (grouped), dL/dalpha, dL/dbeta;
+ *               when update == 0 at least one must be non-NULL.
+ * The gradients are taken at the parameters as they were on entry.
+ */
+int mr_fq_backward_signsgd(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                           const float* init_scale, const void* g, int g_dtype, int64_t rows,
+                           int64_t cols, int group_size, int bits, int mode, float eps,
+                           int update, float lr, float coef_lo, float coef_hi, float v_bound,
+                           float* grad_v_out, float* grad_alpha_out, float* grad_beta_out,
+                           void* stream);
+
+/*
+ * Pack one-byte codes into MLX uint32 words, element 0 in the least
+ * significant bits; widths 3/5/6/7 use the cross-word bitstream.
+ * Replaces mround/formats/packing.py:119-163 (pack_codes); oracle
+ * mround/reference/packing.py:73-122.
+ *   codes        (rows, cols) bytes; read as int8 when codes_signed, else uint8
+ *   code_offset  added to every code first (2^(bits-1) for symmetric codes)
+ *   range_out    optional device int32[2]: {min, max} of the offset codes;
+ *                the caller raises if they leave [0, 2^bits - 1].
+ */
+int mr_pack_codes(const void* codes, int codes_signed, int code_offset, int64_t rows,
+                  int64_t cols, int bits, uint32_t* packed_out, int32_t* range_out,
+                  void* stream);
+
+/* Words per row, or MR_EINVAL (mround/formats/packing.py:84-116). */
+int64_t mr_packed_width(int64_t cols, int bits);
+
+/* Inverse of mr_pack_codes (mround/formats/packing.py:166-206). */
+int mr_unpack_codes(const uint32_t* packed, int64_t rows, int64_t cols, int bits,
+                    uint8_t* codes_out, void* stream);
+
+/*
+ * MLX affine metadata from scale and zero point:
+ * scales = out(scale), biases = out(-scales * out(zp)), zp = 2^(bits-1)
+ * when zp == NULL (symmetric). Replaces mround/formats/mlx_export.py:159-195.
+ */
+int mr_to_affine(const float* scale, const float* zp, int64_t n_groups, int bits,
+                 int out_dtype, void* scales_out, void* biases_out, void* stream);
+
+/*
+ * Block reconstruction losses with dL/dpred written in the same pass.
+ * Replaces mround/core/losses.py:42-130 (reconstruction_loss,
+ * outlier_suppressed_loss, outlier_threshold, piece_loss).
+ *   loss = sum(r_kept^2) / denom, r = pred - target (fp32), grad = 2 r_kept / denom
+ * mr_loss_mse keeps every element. mr_loss_outlier keeps |r| < threshold,
+ * where threshold is the k-th largest |r| over the n elements (exact radix
+ * select on the float bit pattern; every element tied at the threshold is
+ * excluded), unless threshold_in is non-NULL. loss_out and threshold_out are
+ * device scalars; grad_out may be NULL.
+ */
+size_t mr_loss_workspace_bytes(int64_t n);
+int mr_loss_mse(const float* pred, const float* target, int64_t n, int64_t denom,
+                float* loss_out, float* grad_out, void* workspace, void* stream);
+int mr_loss_outlier(const float* pred, const float* target, int64_t n, int64_t k, int64_t denom,
+                    const float* threshold_in, float* threshold_out, float* loss_out,
+                    float* grad_out, void* workspace, void* stream);
+
+/*
+ * DeltaLoss accumulation: scores_out[i] += sum |g * (rtn_i(W) - W)| for each
+ * width bits_list[i] (round-to-nearest at that width, fp32 terms, fp64 sum).
+ * Replaces the per-batch term of mround/pipeline/scoring.py:238-266;
+ * oracle mround/planner/sensitivity.py:190-229. At most 8 widths.
+ */
+size_t mr_delta_loss_workspace_bytes(int64_t rows, int64_t cols, int n_bits);
+int mr_delta_loss(const void* w, int w_dtype, const float* g, int64_t rows, int64_t cols,
+                  int group_size, const int* bits_list, int n_bits, int mode, float eps,
+                  double* scores_out, void* workspace, void* stream);
+
+/* Plain device copy of `bytes` bytes, used to calibrate traffic counters. */
+int mr_copy_bytes(const void* src, void* dst, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MROUND_HIP_H */

@@ -1,0 +1,160 @@
+// Shared helpers for the libmround_hip kernels (gfx950).
+//
+// Element conversions are written out on bit patterns so that their rounding
+// is explicit: bf16 and fp16 widen exactly, and narrowing rounds to nearest,
+// ties to even, which is what torch and MLX do.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/mround_hip.h"
+
+namespace mr {
+
+// Error plumbing: a thread-local message and status codes (mr_common.hip).
+int fail(int code, const char* fmt, ...);
+int hip_fail(hipError_t err, const char* what);
+void clear_error();
+
+#define MR_LAUNCH_CHECK(what)                                        \
+  do {                                                               \
+    hipError_t e_ = hipGetLastError();                               \
+    if (e_ != hipSuccess) return ::mr::hip_fail(e_, what);           \
+  } while (0)
+
+inline bool valid_dtype(int dt) { return dt == MR_F32 || dt == MR_BF16 || dt == MR_F16; }
+inline int dtype_bytes(int dt) { return dt == MR_F32 ? 4 : 2; }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* p, int64_t i) {
+  if constexpr (DT == MR_F32) {
+    return static_cast<const float*>(p)[i];
+  } else if constexpr (DT == MR_BF16) {
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  } else {
+    return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store_elem(void* p, int64_t i, float x) {
+  if constexpr (DT == MR_F32) {
+    static_cast<float*>(p)[i] = x;
+  } else if constexpr (DT == MR_BF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(x);
+  } else {
+    static_cast<uint16_t*>(p)[i] = f32_to_f16(x);
+  }
+}
+
+// 16-byte streaming accesses. Data read or written exactly once per pass goes
+// through these nontemporal forms, which keep it from displacing reused lines
+// in the caches; measured faster than plain accesses on the fake-quant passes.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld16_stream(const void* p) {
+  u32x4_t r = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(r.x, r.y, r.z, r.w);
+}
+
+__device__ __forceinline__ void st16_stream(void* p, uint4 v) {
+  u32x4_t r = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(r, reinterpret_cast<u32x4_t*>(p));
+}
+
+// Eight consecutive elements starting at element index i (i % 8 == 0 and the
+// base pointer 16-byte aligned): one 16-byte load for 2-byte types, two for fp32.
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, int64_t i, float (&out)[8]) {
+  if constexpr (DT == MR_F32) {
+    const float* q = static_cast<const float*>(p) + i;
+    uint4 a = ld16_stream(q), b = ld16_stream(q + 4);
+    out[0] = __uint_as_float(a.x); out[1] = __uint_as_float(a.y);
+    out[2] = __uint_as_float(a.z); out[3] = __uint_as_float(a.w);
+    out[4] = __uint_as_float(b.x); out[5] = __uint_as_float(b.y);
+    out[6] = __uint_as_float(b.z); out[7] = __uint_as_float(b.w);
+  } else {
+    uint4 r = ld16_stream(static_cast<const uint16_t*>(p) + i);
+    uint32_t words[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint16_t lo = static_cast<uint16_t>(words[k] & 0xffffu);
+      uint16_t hi = static_cast<uint16_t>(words[k] >> 16);
+      if constexpr (DT == MR_BF16) {
+        out[2 * k] = bf16_to_f32(lo);
+        out[2 * k + 1] = bf16_to_f32(hi);
+      } else {
+        out[2 * k] = f16_to_f32(lo);
+        out[2 * k + 1] = f16_to_f32(hi);
+      }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(void* p, int64_t i, const float (&x)[8]) {
+  if constexpr (DT == MR_F32) {
+    float* q = static_cast<float*>(p) + i;
+    st16_stream(q, make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                              __float_as_uint(x[3])));
+    st16_stream(q + 4, make_uint4(__float_as_uint(x[4]), __float_as_uint(x[5]),
+                                  __float_as_uint(x[6]), __float_as_uint(x[7])));
+  } else {
+    uint32_t words[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint16_t lo, hi;
+      if constexpr (DT == MR_BF16) {
+        lo = f32_to_bf16(x[2 * k]);
+        hi = f32_to_bf16(x[2 * k + 1]);
+      } else {
+        lo = f32_to_f16(x[2 * k]);
+        hi = f32_to_f16(x[2 * k + 1]);
+      }
+      words[k] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+    st16_stream(static_cast<uint16_t*>(p) + i, make_uint4(words[0], words[1], words[2], words[3]));
+  }
+}
+
+__device__ __forceinline__ void load8_f32(const float* p, int64_t i, float (&out)[8]) {
+  load8<MR_F32>(p, i, out);
+}
+
+__device__ __forceinline__ void store8_f32(float* p, int64_t i, const float (&x)[8]) {
+  store8<MR_F32>(p, i, x);
+}
+
+// sign(x) as numpy/MLX define it: -1, 0 or +1 (NaN propagates).
+__device__ __forceinline__ float signf(float x) {
+  return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x * 0.0f);
+}
+
+__device__ __forceinline__ float clampf(float x, float lo, float hi) {
+  return fminf(fmaxf(x, lo), hi);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace mr

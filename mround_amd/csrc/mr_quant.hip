@@ -1,0 +1,665 @@
+// Fake quantization (forward) and its straight-through backward fused with the
+// sign-SGD step, for gfx950.
+//
+// Arithmetic follows the reference's float32 operation order exactly
+// (mround/reference/quantize.py:156-319 forward, 370-522 backward; the
+// round-to-nearest shortcut of mround/core/quantizer.py:269-284): IEEE
+// division (never a reciprocal multiply), round half to even (rintf), no
+// contraction into fused multiply-adds (this file is built with
+// -ffp-contract=off). Codes and reconstructions are therefore bit-identical to
+// a float32 evaluation of the reference's formulas; only the per-group sums of
+// the backward differ, by summation order.
+//
+// Two launch shapes:
+//   fast    each lane owns 8 consecutive weights; a group of gs weights spans
+//           gs/8 adjacent lanes (a power of two <= 64) and its min/max and
+//           gradient sums are xor-butterfly reductions over those lanes, so
+//           every lane of the group ends with bit-identical group values.
+//           One wave streams 8 * 64 weights with 16-byte loads: W, v and the
+//           outputs are read and written exactly once (HBM-bound).
+//   generic one wave per group, strided over the group; covers per-channel
+//           groups, padded last groups and fp16 inputs.
+#include <cmath>
+
+#include "mr_common.h"
+
+namespace mr {
+namespace {
+
+constexpr int kBlock = 256;
+
+struct Group {
+  float s;         // scale (signed under the symmetric modes)
+  float zp;        // zero point (asymmetric)
+  float wmax_raw;  // max(max(W_g), 0)
+  float wmin_raw;  // min(min(W_g), 0)
+  float wmin;      // wmin_raw * beta
+  float base;      // searched scale
+  bool pos_dom;    // symmetric: the positive extreme dominates
+};
+
+__device__ __forceinline__ float clamp_magnitude(float s, float eps) {
+  float sg = signf(s);
+  sg = (sg == 0.0f) ? 1.0f : sg;
+  return sg * fmaxf(fabsf(s), eps);
+}
+
+// Per-group scale and zero point: mround/reference/quantize.py:156-246.
+template <int MODE>
+__device__ __forceinline__ Group group_params(float mx, float mn, float a, float b, float base,
+                                              float maxq, float eps) {
+  Group p;
+  p.base = base;
+  p.zp = 0.0f;
+  p.pos_dom = false;
+  p.wmax_raw = fmaxf(mx, 0.0f);
+  p.wmin_raw = fminf(mn, 0.0f);
+  if constexpr (MODE == MR_SYM_SEARCHED) {
+    p.wmin = 0.0f;
+    p.s = clamp_magnitude(base * b, eps);
+  } else {
+    float wmax = p.wmax_raw * a;
+    p.wmin = p.wmin_raw * b;
+    if constexpr (MODE == MR_ASYM) {
+      p.s = fmaxf((wmax - p.wmin) / maxq, eps);
+      p.zp = rintf(-p.wmin / p.s);
+    } else {
+      float pos_mag = wmax;
+      float neg_mag = -p.wmin;
+      p.pos_dom = pos_mag >= neg_mag;
+      float dominant = p.pos_dom ? pos_mag : neg_mag;
+      float signed_ = p.pos_dom ? -dominant : dominant;
+      p.s = clamp_magnitude(signed_ / maxq, eps);
+    }
+  }
+  return p;
+}
+
+// One weight: code (before narrowing), clamp mask, reconstruction.
+template <int MODE, bool HAS_V>
+__device__ __forceinline__ float quant_one(float w, float v, const Group& p, float qmin, float qmax,
+                                           float& code, float& inside) {
+  float x = w / p.s;
+  if constexpr (HAS_V) x = x + v;
+  float raw = rintf(x);
+  if constexpr (MODE == MR_ASYM) raw = raw + p.zp;
+  inside = (raw >= qmin && raw <= qmax) ? 1.0f : 0.0f;
+  code = clampf(raw, qmin, qmax);
+  if constexpr (MODE == MR_ASYM) return p.s * (code - p.zp);
+  return p.s * code;
+}
+
+__device__ __forceinline__ float group_max(float x, int tpg) {
+  for (int off = tpg >> 1; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, tpg));
+  return x;
+}
+__device__ __forceinline__ float group_min(float x, int tpg) {
+  for (int off = tpg >> 1; off > 0; off >>= 1) x = fminf(x, __shfl_xor(x, off, tpg));
+  return x;
+}
+__device__ __forceinline__ float group_sum(float x, int tpg) {
+  for (int off = tpg >> 1; off > 0; off >>= 1) x = x + __shfl_xor(x, off, tpg);
+  return x;
+}
+// Compile-time-width butterflies: xor partners below 32 lanes come from
+// ds_swizzle in bit mode (lane ^ OFF within each 32-lane half, no address
+// arithmetic); only the 32-lane step needs a permute.
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float x) {
+  if constexpr (OFF < 32) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1f | (OFF << 10)));
+  } else {
+    return __shfl_xor(x, OFF, 64);
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float bfly_max(float x) {
+  if constexpr (OFF >= 1) return bfly_max<OFF / 2>(fmaxf(x, xor_lane<OFF>(x)));
+  return x;
+}
+template <int OFF>
+__device__ __forceinline__ float bfly_min(float x) {
+  if constexpr (OFF >= 1) return bfly_min<OFF / 2>(fminf(x, xor_lane<OFF>(x)));
+  return x;
+}
+template <int OFF>
+__device__ __forceinline__ float bfly_sum(float x) {
+  if constexpr (OFF >= 1) return bfly_sum<OFF / 2>(x + xor_lane<OFF>(x));
+  return x;
+}
+// TPG > 0: width known at compile time; TPG == 0: runtime width `tpg`.
+template <int TPG>
+__device__ __forceinline__ float gmax(float x, int tpg) {
+  if constexpr (TPG > 0) return bfly_max<TPG / 2>(x);
+  return group_max(x, tpg);
+}
+template <int TPG>
+__device__ __forceinline__ float gmin(float x, int tpg) {
+  if constexpr (TPG > 0) return bfly_min<TPG / 2>(x);
+  return group_min(x, tpg);
+}
+template <int TPG>
+__device__ __forceinline__ float gsum(float x, int tpg) {
+  if constexpr (TPG > 0) return bfly_sum<TPG / 2>(x);
+  return group_sum(x, tpg);
+}
+
+__device__ __forceinline__ float wave_max(float x) { return group_max(x, 64); }
+__device__ __forceinline__ float wave_min(float x) { return group_min(x, 64); }
+__device__ __forceinline__ float wave_sum(float x) { return group_sum(x, 64); }
+
+// ---------------------------------------------------------------- forward --
+
+template <int WT, int OT, int MODE, bool HAS_V, int TPG>
+__global__ __launch_bounds__(kBlock) void fq_fwd_fast(
+    const void* __restrict__ w, const float* __restrict__ v, const float* __restrict__ alpha,
+    const float* __restrict__ beta, const float* __restrict__ init_scale, void* __restrict__ wq,
+    uint8_t* __restrict__ codes, float* __restrict__ scale_out, float* __restrict__ zp_out,
+    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps) {
+  int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const bool active = chunk < n_chunks;
+  // Inactive lanes form whole groups (n_chunks % tpg == 0); they stay for the
+  // shuffles on a valid address and store nothing.
+  if (!active) chunk = n_chunks - 1;
+  const int64_t grp = chunk >> tpg_shift;
+  const int64_t e = chunk * 8;
+
+  float x[8];
+  load8<WT>(w, e, x);
+  float mx = x[0], mn = x[0];
+#pragma unroll
+  for (int k = 1; k < 8; ++k) {
+    mx = fmaxf(mx, x[k]);
+    mn = fminf(mn, x[k]);
+  }
+  if constexpr (MODE != MR_SYM_SEARCHED) {
+    mx = gmax<TPG>(mx, tpg);
+    mn = gmin<TPG>(mn, tpg);
+  }
+  float a = 1.0f, b = 1.0f, base = 0.0f;
+  if constexpr (HAS_V) {
+    a = alpha[grp];
+    b = beta[grp];
+  }
+  if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+
+  float vv[8];
+  if constexpr (HAS_V) {
+    load8_f32(v, e, vv);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) vv[k] = 0.0f;
+  }
+  float q[8], c[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float in;
+    q[k] = quant_one<MODE, HAS_V>(x[k], vv[k], p, qmin, qmax, c[k], in);
+  }
+  if (!active) return;
+  if (wq) store8<OT>(wq, e, q);
+  if (codes) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo |= (static_cast<uint32_t>(static_cast<int>(c[k])) & 0xffu) << (8 * k);
+      hi |= (static_cast<uint32_t>(static_cast<int>(c[k + 4])) & 0xffu) << (8 * k);
+    }
+    *reinterpret_cast<uint2*>(codes + e) = make_uint2(lo, hi);
+  }
+  if ((chunk & (tpg - 1)) == 0) {
+    if (scale_out) scale_out[grp] = p.s;
+    if (zp_out) zp_out[grp] = p.zp;
+  }
+}
+
+__device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
+  if (dt == MR_F32) return load_elem<MR_F32>(p, i);
+  if (dt == MR_BF16) return load_elem<MR_BF16>(p, i);
+  return load_elem<MR_F16>(p, i);
+}
+__device__ __forceinline__ void store_any(void* p, int dt, int64_t i, float x) {
+  if (dt == MR_F32) store_elem<MR_F32>(p, i, x);
+  else if (dt == MR_BF16) store_elem<MR_BF16>(p, i, x);
+  else store_elem<MR_F16>(p, i, x);
+}
+
+// One wave per group; v and codes use the padded grouped layout (stride gs).
+template <int MODE, bool HAS_V>
+__global__ __launch_bounds__(kBlock) void fq_fwd_generic(
+    const void* __restrict__ w, int wt, const float* __restrict__ v,
+    const float* __restrict__ alpha, const float* __restrict__ beta,
+    const float* __restrict__ init_scale, void* __restrict__ wq, int ot,
+    uint8_t* __restrict__ codes, float* __restrict__ scale_out, float* __restrict__ zp_out,
+    int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float qmin, float qmax,
+    float eps) {
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  if (grp >= rows * ng) return;  // uniform across the wave
+  const int64_t r = grp / ng;
+  const int64_t c0 = (grp % ng) * gs;
+  float mx = 0.0f, mn = 0.0f;  // padding zeros and the forced zero coincide
+  if constexpr (MODE != MR_SYM_SEARCHED) {
+    for (int t = lane; t < gs; t += 64) {
+      int64_t c = c0 + t;
+      float x = c < cols ? load_any(w, wt, r * cols + c) : 0.0f;
+      mx = fmaxf(mx, x);
+      mn = fminf(mn, x);
+    }
+    mx = wave_max(mx);
+    mn = wave_min(mn);
+  }
+  float a = 1.0f, b = 1.0f, base = 0.0f;
+  if constexpr (HAS_V) {
+    a = alpha[grp];
+    b = beta[grp];
+  }
+  if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+  for (int t = lane; t < gs; t += 64) {
+    int64_t c = c0 + t;
+    float x = c < cols ? load_any(w, wt, r * cols + c) : 0.0f;
+    float vv = 0.0f;
+    if constexpr (HAS_V) vv = v[grp * gs + t];
+    float code, in;
+    float q = quant_one<MODE, HAS_V>(x, vv, p, qmin, qmax, code, in);
+    if (wq && c < cols) store_any(wq, ot, r * cols + c, q);
+    if (codes) codes[grp * gs + t] = static_cast<uint8_t>(static_cast<int>(code) & 0xff);
+  }
+  if (lane == 0) {
+    if (scale_out) scale_out[grp] = p.s;
+    if (zp_out) zp_out[grp] = p.zp;
+  }
+}
+
+// --------------------------------------------------------------- backward --
+
+// Per-element backward terms: mround/reference/quantize.py:464-520.
+//
+// The reference writes d(qdq)/ds for the asymmetric mode as
+//   (c - zp) + s * (inside * (-w/s^2 + wmin/s^2) - wmin/s^2),
+// which is (c - zp) - w/s inside the clamp and (c - zp) - wmin/s outside it;
+// for the symmetric modes it is c - inside * w / s. Both are evaluated here
+// from t = w/s, the quotient the rounding already needs, and the per-group
+// wmin/s, so the backward costs one division per weight like the forward.
+// grad_v = g * s * inside is formed exactly as the reference forms it; only
+// the summands of the per-group sums are rounded differently.
+template <int MODE>
+struct BwdTerms {
+  float gv, ts, td;
+};
+
+template <int MODE>
+__device__ __forceinline__ BwdTerms<MODE> bwd_one(float x, float vv, float g, const Group& p,
+                                                  float wmin_over_s, float qmin, float qmax) {
+  const float t = x / p.s;
+  float raw = rintf(t + vv);
+  if constexpr (MODE == MR_ASYM) raw = raw + p.zp;
+  const bool in = raw >= qmin && raw <= qmax;
+  const float inside = in ? 1.0f : 0.0f;
+  const float code = clampf(raw, qmin, qmax);
+  BwdTerms<MODE> r;
+  r.gv = g * p.s * inside;
+  if constexpr (MODE == MR_ASYM) {
+    const float dq = (code - p.zp) - (in ? t : wmin_over_s);
+    r.ts = g * dq;
+    r.td = g * (1.0f - inside) * p.wmin_raw;
+  } else {
+    const float dq = code - (in ? t : 0.0f);
+    r.ts = g * dq;
+    r.td = 0.0f;
+  }
+  return r;
+}
+
+// dL/dalpha, dL/dbeta from the group sums: mround/reference/quantize.py:388-396,
+// 480-487, 506-520.
+template <int MODE>
+__device__ __forceinline__ void coef_grads(const Group& p, float sum_s, float sum_d, float maxq,
+                                           float& ga, float& gb) {
+  if constexpr (MODE == MR_ASYM) {
+    ga = sum_s * (p.wmax_raw / maxq);
+    gb = sum_s * (-p.wmin_raw / maxq) + sum_d;
+  } else if constexpr (MODE == MR_SYM) {
+    float da = p.pos_dom ? -p.wmax_raw / maxq : 0.0f;
+    float db = p.pos_dom ? 0.0f : -p.wmin_raw / maxq;
+    ga = sum_s * da;
+    gb = sum_s * db;
+  } else {
+    ga = 0.0f;
+    gb = sum_s * p.base;
+  }
+}
+
+struct StepArgs {
+  float lr, lo, hi, vb;
+};
+
+template <int WT, int GT, int MODE, bool UPDATE, int TPG>
+__global__ __launch_bounds__(kBlock) void fq_bwd_fast(
+    const void* __restrict__ w, float* __restrict__ v, float* __restrict__ alpha,
+    float* __restrict__ beta, const float* __restrict__ init_scale, const void* __restrict__ g,
+    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps,
+    StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
+    float* __restrict__ gb_out) {
+  int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const bool active = chunk < n_chunks;
+  if (!active) chunk = n_chunks - 1;
+  const int64_t grp = chunk >> tpg_shift;
+  const int64_t e = chunk * 8;
+
+  float x[8], vv[8], gg[8];
+  load8<WT>(w, e, x);
+  load8_f32(v, e, vv);
+  load8<GT>(g, e, gg);
+  float mx = x[0], mn = x[0];
+#pragma unroll
+  for (int k = 1; k < 8; ++k) {
+    mx = fmaxf(mx, x[k]);
+    mn = fminf(mn, x[k]);
+  }
+  if constexpr (MODE != MR_SYM_SEARCHED) {
+    mx = gmax<TPG>(mx, tpg);
+    mn = gmin<TPG>(mn, tpg);
+  }
+  const float a = alpha[grp];
+  const float b = beta[grp];
+  float base = 0.0f;
+  if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+  const float wmin_over_s = p.wmin / p.s;
+
+  float sum_s = 0.0f, sum_d = 0.0f;
+  float gv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    BwdTerms<MODE> t = bwd_one<MODE>(x[k], vv[k], gg[k], p, wmin_over_s, qmin, qmax);
+    gv[k] = t.gv;
+    sum_s = sum_s + t.ts;
+    if constexpr (MODE == MR_ASYM) sum_d = sum_d + t.td;
+  }
+  sum_s = gsum<TPG>(sum_s, tpg);
+  if constexpr (MODE == MR_ASYM) sum_d = gsum<TPG>(sum_d, tpg);
+  float ga, gb;
+  coef_grads<MODE>(p, sum_s, sum_d, maxq, ga, gb);
+
+  if (!active) return;
+  if (gv_out) store8_f32(gv_out, e, gv);
+  const bool leader = (chunk & (tpg - 1)) == 0;
+  if (leader) {
+    if (ga_out) ga_out[grp] = ga;
+    if (gb_out) gb_out[grp] = gb;
+  }
+  if constexpr (UPDATE) {
+    float nv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) nv[k] = clampf(vv[k] - st.lr * signf(gv[k]), -st.vb, st.vb);
+    store8_f32(v, e, nv);
+    if (leader) {
+      alpha[grp] = clampf(a - st.lr * signf(ga), st.lo, st.hi);
+      beta[grp] = clampf(b - st.lr * signf(gb), st.lo, st.hi);
+    }
+  }
+}
+
+template <int MODE, bool UPDATE>
+__global__ __launch_bounds__(kBlock) void fq_bwd_generic(
+    const void* __restrict__ w, int wt, float* __restrict__ v, float* __restrict__ alpha,
+    float* __restrict__ beta, const float* __restrict__ init_scale, const void* __restrict__ g,
+    int gt, int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float qmin, float qmax,
+    float eps, StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
+    float* __restrict__ gb_out) {
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  if (grp >= rows * ng) return;
+  const int64_t r = grp / ng;
+  const int64_t c0 = (grp % ng) * gs;
+  float mx = 0.0f, mn = 0.0f;
+  if constexpr (MODE != MR_SYM_SEARCHED) {
+    for (int t = lane; t < gs; t += 64) {
+      int64_t c = c0 + t;
+      float x = c < cols ? load_any(w, wt, r * cols + c) : 0.0f;
+      mx = fmaxf(mx, x);
+      mn = fminf(mn, x);
+    }
+    mx = wave_max(mx);
+    mn = wave_min(mn);
+  }
+  const float a = alpha[grp];
+  const float b = beta[grp];
+  float base = 0.0f;
+  if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+  const float wmin_over_s = p.wmin / p.s;
+  float sum_s = 0.0f, sum_d = 0.0f;
+  for (int t = lane; t < gs; t += 64) {
+    int64_t c = c0 + t;
+    bool real = c < cols;
+    float x = real ? load_any(w, wt, r * cols + c) : 0.0f;
+    float gg = real ? load_any(g, gt, r * cols + c) : 0.0f;
+    float vv = v[grp * gs + t];
+    BwdTerms<MODE> tm = bwd_one<MODE>(x, vv, gg, p, wmin_over_s, qmin, qmax);
+    sum_s = sum_s + tm.ts;
+    if constexpr (MODE == MR_ASYM) sum_d = sum_d + tm.td;
+    if (gv_out) gv_out[grp * gs + t] = tm.gv;
+    if constexpr (UPDATE) v[grp * gs + t] = clampf(vv - st.lr * signf(tm.gv), -st.vb, st.vb);
+  }
+  sum_s = wave_sum(sum_s);
+  if constexpr (MODE == MR_ASYM) sum_d = wave_sum(sum_d);
+  float ga, gb;
+  coef_grads<MODE>(p, sum_s, sum_d, maxq, ga, gb);
+  if (lane == 0) {
+    if (ga_out) ga_out[grp] = ga;
+    if (gb_out) gb_out[grp] = gb;
+    if constexpr (UPDATE) {
+      alpha[grp] = clampf(a - st.lr * signf(ga), st.lo, st.hi);
+      beta[grp] = clampf(b - st.lr * signf(gb), st.lo, st.hi);
+    }
+  }
+}
+
+// ------------------------------------------------------------ host side --
+
+struct Shape {
+  int64_t rows, cols, ng, n_groups;
+  int gs, tpg, tpg_shift;
+  bool fast;
+  float maxq, qmin, qmax;
+};
+
+int check_common(const char* fn, const void* w, int w_dtype, int64_t rows, int64_t cols,
+                 int group_size, int bits, int mode, const float* init_scale, Shape& sh) {
+  if (!w && rows > 0 && cols > 0) return fail(MR_EINVAL, "%s: weight pointer is null", fn);
+  if (!valid_dtype(w_dtype)) return fail(MR_EINVAL, "%s: unknown weight dtype %d", fn, w_dtype);
+  if (rows < 0 || cols < 0) return fail(MR_EINVAL, "%s: negative shape", fn);
+  if (bits < 2 || bits > 8) return fail(MR_EINVAL, "%s: bits must be in [2, 8], got %d", fn, bits);
+  if (mode != MR_ASYM && mode != MR_SYM && mode != MR_SYM_SEARCHED)
+    return fail(MR_EINVAL, "%s: unknown mode %d", fn, mode);
+  if (group_size != -1 && group_size <= 0)
+    return fail(MR_EINVAL, "%s: group_size must be positive or -1, got %d", fn, group_size);
+  if ((mode == MR_SYM_SEARCHED) != (init_scale != nullptr) && rows > 0 && cols > 0)
+    return fail(MR_EINVAL, "%s: init_scale is required by, and only by, the searched mode", fn);
+  sh.rows = rows;
+  sh.cols = cols;
+  int64_t gs = group_size == -1 ? cols : group_size;
+  if (gs > (int64_t{1} << 30)) return fail(MR_EINVAL, "%s: group too large", fn);
+  sh.gs = static_cast<int>(gs);
+  sh.ng = (group_size == -1) ? 1 : (cols + gs - 1) / gs;
+  sh.n_groups = rows * sh.ng;
+  int tpg = sh.gs / 8;
+  bool pow2 = tpg > 0 && (tpg & (tpg - 1)) == 0 && tpg <= 64;
+  sh.tpg = tpg;
+  sh.tpg_shift = 0;
+  while (pow2 && (1 << sh.tpg_shift) < tpg) ++sh.tpg_shift;
+  sh.fast = (sh.gs % 8 == 0) && pow2 && gs > 0 && (cols % gs == 0);
+  if (mode == MR_ASYM) {
+    sh.maxq = static_cast<float>((1 << bits) - 1);
+    sh.qmin = 0.0f;
+    sh.qmax = sh.maxq;
+  } else {
+    sh.maxq = static_cast<float>(1 << (bits - 1));
+    sh.qmin = -sh.maxq;
+    sh.qmax = sh.maxq - 1.0f;
+  }
+  return MR_OK;
+}
+
+template <int MODE, bool HAS_V>
+int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const float* alpha,
+               const float* beta, const float* init_scale, void* wq, int ot, uint8_t* codes,
+               float* scale_out, float* zp_out, float eps, hipStream_t stream) {
+  const bool fast_types = (wt == MR_F32 || wt == MR_BF16) && (!wq || ot == MR_F32 || ot == MR_BF16);
+  const bool fast_align = aligned16(w) && (!HAS_V || aligned16(v)) && (!wq || aligned16(wq)) &&
+                          (!codes || (reinterpret_cast<uintptr_t>(codes) & 7u) == 0);
+  if (sh.fast && fast_types && fast_align) {
+    const int64_t n_chunks = sh.rows * sh.cols / 8;
+    const int64_t blocks = (n_chunks + kBlock - 1) / kBlock;
+    if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_fq_forward: tensor too large");
+#define MR_FWD_FAST_T(WT_, OT_, T_)                                                        \
+  hipLaunchKernelGGL((fq_fwd_fast<WT_, OT_, MODE, HAS_V, T_>),                             \
+                     dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, w, v, alpha, \
+                     beta, init_scale, wq, codes, scale_out, zp_out, n_chunks, sh.tpg,       \
+                     sh.tpg_shift, sh.maxq, sh.qmin, sh.qmax, eps)
+#define MR_FWD_FAST(WT_, OT_)                                               \
+  do {                                                                      \
+    if (sh.tpg == 8) MR_FWD_FAST_T(WT_, OT_, 8);                            \
+    else if (sh.tpg == 4) MR_FWD_FAST_T(WT_, OT_, 4);                       \
+    else if (sh.tpg == 16) MR_FWD_FAST_T(WT_, OT_, 16);                     \
+    else MR_FWD_FAST_T(WT_, OT_, 0);                                        \
+  } while (0)
+    const int o = wq ? ot : MR_F32;
+    if (wt == MR_BF16 && o == MR_BF16) MR_FWD_FAST(MR_BF16, MR_BF16);
+    else if (wt == MR_BF16) MR_FWD_FAST(MR_BF16, MR_F32);
+    else if (o == MR_BF16) MR_FWD_FAST(MR_F32, MR_BF16);
+    else MR_FWD_FAST(MR_F32, MR_F32);
+#undef MR_FWD_FAST_T
+#undef MR_FWD_FAST
+  } else {
+    const int64_t blocks = (sh.n_groups + 3) / 4;
+    if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_fq_forward: tensor too large");
+    hipLaunchKernelGGL((fq_fwd_generic<MODE, HAS_V>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), 0, stream, w, wt, v, alpha, beta, init_scale, wq, ot, codes,
+                       scale_out, zp_out, sh.rows, sh.cols, sh.gs, sh.ng, sh.maxq, sh.qmin,
+                       sh.qmax, eps);
+  }
+  MR_LAUNCH_CHECK("mr_fq_forward");
+  return MR_OK;
+}
+
+template <int MODE, bool UPDATE>
+int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, float* beta,
+               const float* init_scale, const void* g, int gt, float eps, StepArgs st,
+               float* gv_out, float* ga_out, float* gb_out, hipStream_t stream) {
+  const bool fast_types = (wt == MR_F32 || wt == MR_BF16) && (gt == MR_F32 || gt == MR_BF16);
+  const bool fast_align = aligned16(w) && aligned16(v) && aligned16(g) && (!gv_out || aligned16(gv_out));
+  if (sh.fast && fast_types && fast_align) {
+    const int64_t n_chunks = sh.rows * sh.cols / 8;
+    const int64_t blocks = (n_chunks + kBlock - 1) / kBlock;
+    if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_fq_backward_signsgd: tensor too large");
+#define MR_BWD_FAST_T(WT_, GT_, T_)                                                         \
+  hipLaunchKernelGGL((fq_bwd_fast<WT_, GT_, MODE, UPDATE, T_>),                             \
+                     dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, w, v, alpha, \
+                     beta, init_scale, g, n_chunks, sh.tpg, sh.tpg_shift, sh.maxq, sh.qmin,   \
+                     sh.qmax, eps, st, gv_out, ga_out, gb_out)
+#define MR_BWD_FAST(WT_, GT_)                                               \
+  do {                                                                      \
+    if (sh.tpg == 8) MR_BWD_FAST_T(WT_, GT_, 8);                            \
+    else if (sh.tpg == 4) MR_BWD_FAST_T(WT_, GT_, 4);                       \
+    else if (sh.tpg == 16) MR_BWD_FAST_T(WT_, GT_, 16);                     \
+    else MR_BWD_FAST_T(WT_, GT_, 0);                                        \
+  } while (0)
+    if (wt == MR_BF16 && gt == MR_F32) MR_BWD_FAST(MR_BF16, MR_F32);
+    else if (wt == MR_BF16) MR_BWD_FAST(MR_BF16, MR_BF16);
+    else if (gt == MR_F32) MR_BWD_FAST(MR_F32, MR_F32);
+    else MR_BWD_FAST(MR_F32, MR_BF16);
+#undef MR_BWD_FAST_T
+#undef MR_BWD_FAST
+  } else {
+    const int64_t blocks = (sh.n_groups + 3) / 4;
+    if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_fq_backward_signsgd: tensor too large");
+    hipLaunchKernelGGL((fq_bwd_generic<MODE, UPDATE>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), 0, stream, w, wt, v, alpha, beta, init_scale, g, gt, sh.rows,
+                       sh.cols, sh.gs, sh.ng, sh.maxq, sh.qmin, sh.qmax, eps, st, gv_out, ga_out,
+                       gb_out);
+  }
+  MR_LAUNCH_CHECK("mr_fq_backward_signsgd");
+  return MR_OK;
+}
+
+}  // namespace
+}  // namespace mr
+
+extern "C" {
+
+int mr_fq_forward(const void* w, int w_dtype, const float* v, const float* alpha,
+                  const float* beta, const float* init_scale, int64_t rows, int64_t cols,
+                  int group_size, int bits, int mode, float eps, void* wq_out, int wq_dtype,
+                  void* codes_out, float* scale_out, float* zp_out, void* stream) {
+  using namespace mr;
+  clear_error();
+  Shape sh;
+  int rc = check_common("mr_fq_forward", w, w_dtype, rows, cols, group_size, bits, mode,
+                        init_scale, sh);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return MR_OK;
+  const bool any_v = v || alpha || beta;
+  if (any_v && !(v && alpha && beta))
+    return fail(MR_EINVAL, "mr_fq_forward: v, alpha and beta are given together or not at all");
+  if (!wq_out && !codes_out && !scale_out && !zp_out)
+    return fail(MR_EINVAL, "mr_fq_forward: no output requested");
+  if (wq_out && !valid_dtype(wq_dtype))
+    return fail(MR_EINVAL, "mr_fq_forward: unknown output dtype %d", wq_dtype);
+  if (zp_out && mode != MR_ASYM)
+    return fail(MR_EINVAL, "mr_fq_forward: a zero point exists only in the asymmetric mode");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* codes = static_cast<uint8_t*>(codes_out);
+#define MR_FWD(MODE_)                                                                     \
+  return any_v ? launch_fwd<MODE_, true>(sh, w, w_dtype, v, alpha, beta, init_scale, wq_out, \
+                                         wq_dtype, codes, scale_out, zp_out, eps, s)       \
+               : launch_fwd<MODE_, false>(sh, w, w_dtype, v, alpha, beta, init_scale, wq_out, \
+                                          wq_dtype, codes, scale_out, zp_out, eps, s)
+  if (mode == MR_ASYM) MR_FWD(MR_ASYM);
+  if (mode == MR_SYM) MR_FWD(MR_SYM);
+  MR_FWD(MR_SYM_SEARCHED);
+#undef MR_FWD
+}
+
+int mr_fq_backward_signsgd(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                           const float* init_scale, const void* g, int g_dtype, int64_t rows,
+                           int64_t cols, int group_size, int bits, int mode, float eps,
+                           int update, float lr, float coef_lo, float coef_hi, float v_bound,
+                           float* grad_v_out, float* grad_alpha_out, float* grad_beta_out,
+                           void* stream) {
+  using namespace mr;
+  clear_error();
+  Shape sh;
+  int rc = check_common("mr_fq_backward_signsgd", w, w_dtype, rows, cols, group_size, bits, mode,
+                        init_scale, sh);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return MR_OK;
+  if (!v || !alpha || !beta)
+    return fail(MR_EINVAL, "mr_fq_backward_signsgd: v, alpha and beta are required");
+  if (!g) return fail(MR_EINVAL, "mr_fq_backward_signsgd: gradient pointer is null");
+  if (!valid_dtype(g_dtype))
+    return fail(MR_EINVAL, "mr_fq_backward_signsgd: unknown gradient dtype %d", g_dtype);
+  if (!update && !grad_v_out && !grad_alpha_out && !grad_beta_out)
+    return fail(MR_EINVAL, "mr_fq_backward_signsgd: nothing to do (no update, no gradient output)");
+  if (update && !(coef_lo <= coef_hi && v_bound >= 0.0f))
+    return fail(MR_EINVAL, "mr_fq_backward_signsgd: bad bounds");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  StepArgs st{lr, coef_lo, coef_hi, v_bound};
+#define MR_BWD(MODE_)                                                                       \
+  return update ? launch_bwd<MODE_, true>(sh, w, w_dtype, v, alpha, beta, init_scale, g,     \
+                                          g_dtype, eps, st, grad_v_out, grad_alpha_out,      \
+                                          grad_beta_out, s)                                  \
+                : launch_bwd<MODE_, false>(sh, w, w_dtype, v, alpha, beta, init_scale, g,    \
+                                           g_dtype, eps, st, grad_v_out, grad_alpha_out,     \
+                                           grad_beta_out, s)
+  if (mode == MR_ASYM) MR_BWD(MR_ASYM);
+  if (mode == MR_SYM) MR_BWD(MR_SYM);
+  MR_BWD(MR_SYM_SEARCHED);
+#undef MR_BWD
+}
+
+}  // extern "C"

@@ -1,0 +1,252 @@
+"""ctypes binding of ``libmround_hip.so`` -- the package's only compute path.
+
+The reference leaves ``mround/kernels/`` empty as the designated home for
+accelerated operators called from ``core`` and ``formats``
+(``mround/kernels/__init__.py:3-8``, ``mround/formats/packing.py:28-30``).
+Here it is the binding of the HIP library declared in ``include/mround_hip.h``.
+
+Every wrapper takes torch tensors that already live on a ROCm device,
+passes raw device pointers and the current HIP stream, and raises
+:class:`~mround_amd.exceptions.KernelError` when the library refuses a call.
+If the library is missing, :class:`~mround_amd.exceptions.KernelUnavailableError`
+is raised; nothing falls back to another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+from mround_amd.exceptions import KernelError, KernelUnavailableError
+
+__all__ = [
+    "MODE",
+    "copy_bytes",
+    "delta_loss",
+    "dtype_code",
+    "fq_backward_signsgd",
+    "fq_forward",
+    "lib",
+    "lib_path",
+    "loss_mse",
+    "loss_outlier",
+    "loss_workspace",
+    "pack_codes",
+    "packed_width",
+    "to_affine",
+    "unpack_codes",
+]
+
+_PKG = Path(__file__).resolve().parent.parent
+_LIB_PATH = _PKG / "_lib" / "libmround_hip.so"
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+MR_OK, MR_EINVAL = 0, -22
+MODE = {"asym": 0, "sym": 1, "searched": 2}
+_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_D = ctypes.c_double
+
+_SIGNATURES = {
+    "mr_last_error": (ctypes.c_char_p, []),
+    "mr_abi_version": (_I, []),
+    "mr_fq_forward": (_I, [_P, _I, _P, _P, _P, _P, _L, _L, _I, _I, _I, _F, _P, _I, _P, _P, _P, _P]),
+    "mr_fq_backward_signsgd": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F, _I, _F,
+                                    _F, _F, _F, _P, _P, _P, _P]),
+    "mr_pack_codes": (_I, [_P, _I, _I, _L, _L, _I, _P, _P, _P]),
+    "mr_packed_width": (_L, [_L, _I]),
+    "mr_unpack_codes": (_I, [_P, _L, _L, _I, _P, _P]),
+    "mr_to_affine": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
+    "mr_loss_workspace_bytes": (ctypes.c_size_t, [_L]),
+    "mr_loss_mse": (_I, [_P, _P, _L, _L, _P, _P, _P, _P]),
+    "mr_loss_outlier": (_I, [_P, _P, _L, _L, _L, _P, _P, _P, _P, _P, _P]),
+    "mr_delta_loss_workspace_bytes": (ctypes.c_size_t, [_L, _L, _I]),
+    "mr_delta_loss": (_I, [_P, _I, _P, _L, _L, _I, _P, _I, _I, _F, _P, _P, _P]),
+    "mr_copy_bytes": (_I, [_P, _P, ctypes.c_size_t, _P]),
+}
+
+
+def lib_path() -> Path:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises :class:`KernelUnavailableError` if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not _LIB_PATH.exists():
+                raise KernelUnavailableError(
+                    f"{_LIB_PATH} is missing: build it with `python -m mround_amd.build` "
+                    "(hipcc --offload-arch=gfx950); there is no CPU fallback"
+                )
+            try:
+                handle = ctypes.CDLL(str(_LIB_PATH))
+            except OSError as exc:
+                raise KernelUnavailableError(f"cannot load {_LIB_PATH}: {exc}") from exc
+            for name, (restype, argtypes) in _SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _lib = handle
+    return _lib
+
+
+def _check(rc: int, name: str) -> None:
+    if rc != MR_OK:
+        msg = lib().mr_last_error().decode(errors="replace")
+        raise KernelError(f"{name} failed ({rc}): {msg}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise KernelError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise KernelError("tensors passed to the HIP library must live on a ROCm device")
+    if not t.is_contiguous():
+        raise KernelError("tensors passed to the HIP library must be contiguous")
+    return t.data_ptr()
+
+
+def _f32(t: torch.Tensor | None, name: str) -> torch.Tensor | None:
+    if t is not None and t.dtype != torch.float32:
+        raise KernelError(f"{name} must be float32, got {t.dtype}")
+    return t
+
+
+# ---------------------------------------------------------------- quantizer --
+
+def fq_forward(weight, v, alpha, beta, *, bits, group_size, mode, eps, init_scale=None,
+               wq_out=None, codes_out=None, scale_out=None, zp_out=None) -> None:
+    """``mr_fq_forward``: fills whichever outputs are given."""
+    rows, cols = weight.shape
+    rc = lib().mr_fq_forward(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(v, "v")), _ptr(_f32(alpha, "alpha")),
+        _ptr(_f32(beta, "beta")), _ptr(_f32(init_scale, "init_scale")), rows, cols, group_size,
+        bits, MODE[mode], eps, _ptr(wq_out), dtype_code(wq_out.dtype) if wq_out is not None else 0,
+        _ptr(codes_out), _ptr(_f32(scale_out, "scale")), _ptr(_f32(zp_out, "zero_point")),
+        _stream(weight))
+    _check(rc, "mr_fq_forward")
+
+
+def fq_backward_signsgd(weight, v, alpha, beta, grad_wq, *, bits, group_size, mode, eps,
+                        update, lr=0.0, coef_lo=0.0, coef_hi=0.0, v_bound=0.5, init_scale=None,
+                        grad_v_out=None, grad_alpha_out=None, grad_beta_out=None) -> None:
+    """``mr_fq_backward_signsgd``: gradients and/or the fused sign step."""
+    rows, cols = weight.shape
+    rc = lib().mr_fq_backward_signsgd(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(v, "v")), _ptr(_f32(alpha, "alpha")),
+        _ptr(_f32(beta, "beta")), _ptr(_f32(init_scale, "init_scale")), _ptr(grad_wq),
+        dtype_code(grad_wq.dtype), rows, cols, group_size, bits, MODE[mode], eps, int(update), lr,
+        coef_lo, coef_hi, v_bound, _ptr(grad_v_out), _ptr(grad_alpha_out), _ptr(grad_beta_out),
+        _stream(weight))
+    _check(rc, "mr_fq_backward_signsgd")
+
+
+# ------------------------------------------------------------------ packing --
+
+def packed_width(cols: int, bits: int) -> int:
+    w = lib().mr_packed_width(cols, bits)
+    if w < 0:
+        raise ValueError(lib().mr_last_error().decode())
+    return int(w)
+
+
+def pack_codes(codes, bits: int, *, signed: bool, offset: int, packed_out, range_out=None) -> None:
+    rows, cols = codes.shape
+    rc = lib().mr_pack_codes(_ptr(codes), int(signed), offset, rows, cols, bits, _ptr(packed_out),
+                             _ptr(range_out), _stream(codes))
+    _check(rc, "mr_pack_codes")
+
+
+def unpack_codes(packed, rows: int, cols: int, bits: int, codes_out) -> None:
+    rc = lib().mr_unpack_codes(_ptr(packed), rows, cols, bits, _ptr(codes_out), _stream(packed))
+    _check(rc, "mr_unpack_codes")
+
+
+def to_affine(scale, zero_point, bits: int, scales_out, biases_out) -> None:
+    rc = lib().mr_to_affine(_ptr(_f32(scale, "scale")), _ptr(_f32(zero_point, "zero_point")),
+                            scale.numel(), bits, dtype_code(scales_out.dtype), _ptr(scales_out),
+                            _ptr(biases_out), _stream(scale))
+    _check(rc, "mr_to_affine")
+
+
+# ------------------------------------------------------------------- losses --
+
+_workspaces: dict[tuple[int, str], torch.Tensor] = {}
+
+
+def loss_workspace(device: torch.device, n: int) -> torch.Tensor:
+    """A cached workspace for the loss kernels on ``device``."""
+    nbytes = int(lib().mr_loss_workspace_bytes(n))
+    key = (device.index or 0, "loss")
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def loss_mse(pred, target, *, denom, loss_out, grad_out=None, workspace=None) -> None:
+    n = pred.numel()
+    ws = workspace if workspace is not None else loss_workspace(pred.device, n)
+    rc = lib().mr_loss_mse(_ptr(_f32(pred, "pred")), _ptr(_f32(target, "target")), n, denom,
+                           _ptr(loss_out), _ptr(grad_out), _ptr(ws), _stream(pred))
+    _check(rc, "mr_loss_mse")
+
+
+def loss_outlier(pred, target, *, k, denom, loss_out, threshold_in=None, threshold_out=None,
+                 grad_out=None, workspace=None) -> None:
+    n = pred.numel()
+    ws = workspace if workspace is not None else loss_workspace(pred.device, n)
+    rc = lib().mr_loss_outlier(_ptr(_f32(pred, "pred")), _ptr(_f32(target, "target")), n, k, denom,
+                               _ptr(threshold_in), _ptr(threshold_out), _ptr(loss_out),
+                               _ptr(grad_out), _ptr(ws), _stream(pred))
+    _check(rc, "mr_loss_outlier")
+
+
+# ------------------------------------------------------------- sensitivity --
+
+def delta_loss(weight, grad, *, group_size, bits_list, mode, eps, scores_out, workspace=None) -> None:
+    rows, cols = weight.shape
+    n_bits = len(bits_list)
+    arr = (ctypes.c_int * n_bits)(*bits_list)
+    nbytes = int(lib().mr_delta_loss_workspace_bytes(rows, cols, n_bits))
+    if workspace is None:
+        key = (weight.device.index or 0, "delta")
+        workspace = _workspaces.get(key)
+        if workspace is None or workspace.numel() < nbytes:
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
+            _workspaces[key] = workspace
+    if scores_out.dtype != torch.float64:
+        raise KernelError("scores_out must be float64")
+    rc = lib().mr_delta_loss(_ptr(weight), dtype_code(weight.dtype), _ptr(_f32(grad, "grad")), rows,
+                             cols, group_size, arr, n_bits, MODE[mode], eps, _ptr(scores_out),
+                             _ptr(workspace), _stream(weight))
+    _check(rc, "mr_delta_loss")
+
+
+def copy_bytes(src, dst, nbytes: int) -> None:
+    rc = lib().mr_copy_bytes(_ptr(src), _ptr(dst), nbytes, _stream(src))
+    _check(rc, "mr_copy_bytes")

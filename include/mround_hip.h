@@ -63,6 +63,19 @@ int mr_fq_forward(const void* w, int w_dtype, const float* v, const float* alpha
                   void* codes_out, float* scale_out, float* zp_out, void* stream);
 
 /*
+ * Row placement of wq_out (forward) or of g (backward) inside a larger
+ * row-major buffer with the same number of columns: weight row r lives at
+ * row (r / block) * stride + offset + r % block. block == 0 is the identity.
+ * It lets several layers' W' land in one GEMM operand (q/k/v stacked:
+ * block = rows, offset = first row; gate/up interleaved by 32: block = 32,
+ * stride = 64, offset 0 or 32) and their gradients be read back from it.
+ */
+int mr_fq_forward_mapped(const void* w, int w_dtype, const float* v, const float* alpha,
+                         const float* beta, const float* init_scale, int64_t rows, int64_t cols,
+                         int group_size, int bits, int mode, float eps, void* wq_out, int wq_dtype,
+                         int64_t row_block, int64_t row_stride, int64_t row_offset, void* stream);
+
+/*
  * Straight-through backward fused with the sign-SGD step and the projection.
  * Replaces the MLX autodiff of fake_quantize (oracle
  * mround/reference/quantize.py:399-522), SignSGD.apply
@@ -81,6 +94,14 @@ int mr_fq_backward_signsgd(const void* w, int w_dtype, float* v, float* alpha, f
                            int update, float lr, float coef_lo, float coef_hi, float v_bound,
                            float* grad_v_out, float* grad_alpha_out, float* grad_beta_out,
                            void* stream);
+
+/* The fused step with g read through the row placement of mr_fq_forward_mapped. */
+int mr_fq_backward_signsgd_mapped(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                                  const float* init_scale, const void* g, int g_dtype,
+                                  int64_t rows, int64_t cols, int group_size, int bits, int mode,
+                                  float eps, float lr, float coef_lo, float coef_hi, float v_bound,
+                                  int64_t row_block, int64_t row_stride, int64_t row_offset,
+                                  void* stream);
 
 /*
  * Pack one-byte codes into MLX uint32 words, element 0 in the least
@@ -139,6 +160,35 @@ size_t mr_delta_loss_workspace_bytes(int64_t rows, int64_t cols, int n_bits);
 int mr_delta_loss(const void* w, int w_dtype, const float* g, int64_t rows, int64_t cols,
                   int group_size, const int* bits_list, int n_bits, int mode, float eps,
                   double* scores_out, void* workspace, void* stream);
+
+/*
+ * bf16 GEMM on the MFMA cores, fp32 accumulation:
+ *   C[m, n] = sum_k A(m, k) B(n, k) (+ bias[n]) (+ resid[m, n])
+ * layout MR_NT: A = X [M, K], B = W [N, K]  (forward, y = x W^T)
+ *        MR_NN: A = dY [M, K], B = W [K, N] (input gradient, dx = dy W)
+ *        MR_TN: A = dY [K, M], B = X [K, N] (weight gradient, dW = dy^T x)
+ * All row-major with leading dimensions lda/ldb/ldc/ldr in elements; M, N
+ * multiples of 8, K a multiple of 32, operands 16-byte aligned. C is fp32 or
+ * bf16; with resid (fp32) C is fp32. Replaces the matmul of the reference's
+ * tunable linear, `x @ weight.T` (mround/pipeline/runner.py:364-368), and the
+ * two products MLX autodiff forms for its backward.
+ */
+enum { MR_NT = 0, MR_NN = 1, MR_TN = 2 };
+int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+            const void* B, int64_t ldb, void* C, int c_dtype, int64_t ldc, const float* bias,
+            const float* resid, int64_t ldr, void* stream);
+
+/*
+ * SwiGLU projection pair in one product: act = silu(x Wg^T) * (x Wu^T), bf16
+ * [M, N], from the row-interleaved weight Wgu [2N, K] (rows 64b .. 64b+31 are
+ * gate rows 32b .. 32b+31, rows 64b+32 .. 64b+63 the matching up rows; the
+ * fake-quant forward writes this layout directly). Optionally also the bf16
+ * gate and up values, gu [M, 2N], interleaved the same way by column.
+ * Replaces the mlp's gate/up linears and `nn.silu(g) * u` of the mlx-lm
+ * block reached at mround/pipeline/blocks.py:605.
+ */
+int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* Wgu,
+                   int64_t ldw, void* act, int64_t ldact, void* gu, int64_t ldgu, void* stream);
 
 /* Plain device copy of `bytes` bytes, used to calibrate traffic counters. */
 int mr_copy_bytes(const void* src, void* dst, size_t bytes, void* stream);

@@ -1,0 +1,419 @@
+// bf16 GEMMs on the MFMA cores of gfx950, fp32 accumulation.
+//
+// C[M, N] = sum_k A(m, k) * B(n, k), with each operand stored either K-major
+// (row-major with k contiguous: activations X[t, k], weights W[n, k]) or
+// MN-major (k is the row index: dY[t, n] used as A(n, t) for dW = dY^T X, and
+// W[k, n] used as B(n, k) for dX = dY W). The three products of a linear
+// layer's forward and backward are therefore one kernel:
+//   forward  Y  = X  W^T   A = X  (K-major)  B = W  (K-major)
+//   input    dX = dY W     A = dY (K-major)  B = W  (MN-major)
+//   weight   dW = dY^T X   A = dY (MN-major) B = X  (MN-major)
+//
+// Tiling: a block of 256 threads (4 waves of 64, 2 x 2) owns a BM x BN tile
+// of C; each wave owns (BM/2) x (BN/2) as a grid of 32 x 32 accumulators fed by
+// v_mfma_f32_32x32x16_bf16 (lane l: A row l%32, B column l%32, k half l/32;
+// accumulator register r: row (r/4)*8 + (l/32)*4 + r%4, column l%32). Both
+// operands are staged in LDS K-major (row = m or n, 32 k per row, padded), so
+// every MFMA operand is one 16-byte LDS read. MN-major tiles are transposed
+// in registers (4 k x 8 mn blocks, v_perm_b32) on their way into LDS. The k
+// loop is double-buffered in LDS with the next tile's global loads in flight
+// during the current tile's MFMAs.
+//
+// Blocks are renumbered so that each XCD (blocks are dealt to the 8 XCDs
+// round-robin) receives a contiguous run of tiles, grouped along M so that a
+// run shares B panels in that XCD's L2.
+#include <type_traits>
+
+#include "mr_common.h"
+
+namespace mr {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int BK = 64;
+// LDS tiles are K-major rows of 64 bf16 (128 bytes, 8 chunks of 16 bytes)
+// with no padding; chunk c of row r is stored at position c ^ (r & 7). Eight
+// consecutive rows read at one k chunk (the MFMA operand reads of 8 lanes)
+// then cover 8 distinct positions, i.e. all 32 banks once, and the 8 chunks
+// of one row written together are a permutation of the row: no conflicts.
+constexpr int ROW_BYTES = BK * 2;
+
+enum Epi : int {
+  EPI_STORE = 0,   // C = acc (+ bias[n])
+  EPI_RESID = 1,   // C = resid[m, n] + acc (+ bias[n]), fp32
+  EPI_SWIGLU = 2,  // act = silu(g) * u from row-interleaved gate/up weights
+};
+
+struct GemmParams {
+  int M, N, K;
+  const uint16_t* A;
+  int64_t lda;
+  const uint16_t* B;
+  int64_t ldb;
+  int n_out;           // SWIGLU: columns of act (B has 2 * n_out interleaved rows)
+  void* C;
+  int64_t ldc;
+  const float* bias;
+  const float* resid;
+  int64_t ldr;
+  uint16_t* gu;        // SWIGLU: gate/up copy, [M, 2 * n_out] bf16, interleaved like B
+  int64_t ldgu;
+  int grid_m, grid_n;
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+
+__device__ __forceinline__ uint4 ldg16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * ROW_BYTES + ((chunk ^ (row & 7)) << 4); }
+
+// ---- K-major operand: global -> LDS directly (global_load_lds, 16 B/lane) --
+//
+// One wave instruction moves 64 chunks = 8 rows; lane l covers row 8q + l/8
+// and LDS position l % 8, i.e. global chunk (l % 8) ^ (l / 8). Rows past the
+// valid range are clamped to the last valid row: they only feed accumulator
+// rows or columns that are never stored.
+template <int ROWS>
+struct KMajorDirect {
+  static constexpr int INSTR = ROWS * 8 / 64 / 4;  // instructions per wave
+  __device__ __forceinline__ static void issue(const uint16_t* base, int64_t ld, int row0,
+                                               int rows_valid, int k0, uint8_t* lds) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int sub = lane >> 3;
+    const int chunk = (lane & 7) ^ sub;
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      const int q = i * 4 + wave;
+      const int row = q * 8 + sub;
+      const int g = min(row0 + row, rows_valid - 1);
+      const uint16_t* src = base + static_cast<int64_t>(g) * ld + k0 + chunk * 8;
+      __builtin_amdgcn_global_load_lds((const gbl_void_t*)src,
+                                       (lds_void_t*)(lds + q * 8 * ROW_BYTES), 16, 0, 0);
+    }
+  }
+};
+
+// ---- MN-major operand: element (row, k) at base[k * ld + row] -------------
+//
+// Each thread moves an 8 k x 8 row block: eight 16-byte loads along the row
+// index (one per k), transposed in registers (v_perm_b32 pairs of bf16) into
+// eight 16-byte LDS writes of 8 consecutive k. The k chunk is the fastest
+// lane index, so the 8 lanes of one write cycle fill one row.
+template <int ROWS>
+struct MNMajorLoader {
+  static constexpr int KB = BK / 8;
+  static constexpr int BLOCKS = KB * (ROWS / 8);
+  static constexpr int PER_THREAD = (BLOCKS + kThreads - 1) / kThreads;
+  uint4 r[PER_THREAD][8];
+
+  __device__ __forceinline__ void load(const uint16_t* base, int64_t ld, int row0, int rows_valid,
+                                       int k0) {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int b = min(static_cast<int>(threadIdx.x) + i * kThreads, BLOCKS - 1);
+      const int kb = b % KB;
+      const int rb = min(row0 + (b / KB) * 8, rows_valid - 8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        r[i][j] = ldg16(base + static_cast<int64_t>(k0 + kb * 8 + j) * ld + rb);
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int b = threadIdx.x + i * kThreads;
+      if (b >= BLOCKS) continue;
+      const int kb = b % KB;
+      const int rb = (b / KB) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const int c = e >> 1;
+        uint32_t d[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = (&r[i][2 * q].x)[c];
+          const uint32_t hi = (&r[i][2 * q + 1].x)[c];
+          d[q] = __builtin_amdgcn_perm(hi, lo, sel);  // (k = 2q, 2q + 1) of row rb + e
+        }
+        *reinterpret_cast<uint4*>(lds + swz(rb + e, kb)) = make_uint4(d[0], d[1], d[2], d[3]);
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  // Two LDS stages as four distinct arrays, indexed only with compile-time
+  // stage numbers (the k loop below is unrolled by two), so that the waits
+  // for the direct-to-LDS loads into one stage are not placed in front of the
+  // operand reads of the other.
+  __shared__ __attribute__((aligned(1024))) uint8_t As0[BM * ROW_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t As1[BM * ROW_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t Bs0[BN * ROW_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t Bs1[BN * ROW_BYTES];
+
+  // XCD-aware renumbering, then grouped order along M.
+  const int nblk = p.grid_m * p.grid_n;
+  int bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 8;
+  const int per_group = GROUP_M * p.grid_n;
+  const int group = bid / per_group;
+  const int first_m = group * GROUP_M;
+  const int gm = min(p.grid_m - first_m, GROUP_M);
+  const int bm = first_m + (bid % per_group) % gm;
+  const int bn = (bid % per_group) / gm;
+  const int m0 = bm * BM;
+  const int n0 = bn * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  MNMajorLoader<BM> la;
+  MNMajorLoader<BN> lb;
+  (void)la;
+  (void)lb;
+
+  // Global loads of tile kt: direct ones land in the given LDS stage;
+  // register ones wait in la/lb until stage_regs().
+  auto issue_loads = [&](int kt, uint8_t* as_dst, uint8_t* bs_dst) {
+    const int k0 = kt * BK;
+    if constexpr (A_KMAJOR) KMajorDirect<BM>::issue(p.A, p.lda, m0, p.M, k0, as_dst);
+    else la.load(p.A, p.lda, m0, p.M, k0);
+    if constexpr (B_KMAJOR) KMajorDirect<BN>::issue(p.B, p.ldb, n0, p.N, k0, bs_dst);
+    else lb.load(p.B, p.ldb, n0, p.N, k0);
+  };
+  auto stage_regs = [&](uint8_t* as_dst, uint8_t* bs_dst) {
+    if constexpr (!A_KMAJOR) la.store(as_dst);
+    if constexpr (!B_KMAJOR) lb.store(bs_dst);
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+
+  // MFMAs over one LDS stage, with the operands of the next k16 step read
+  // while the current step's MFMAs run.
+  auto compute = [&](const uint8_t* as, const uint8_t* bs) {
+    bf16x8 af[2][TM], bfr[2][TN];
+    auto read_frags = [&](int kk, int slot) {
+      const int chunk = kk * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WM + i * 32 + (lane & 31);
+        af[slot][i] = *reinterpret_cast<const bf16x8*>(as + swz(row, chunk));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wn * WN + j * 32 + (lane & 31);
+        bfr[slot][j] = *reinterpret_cast<const bf16x8*>(bs + swz(row, chunk));
+      }
+    };
+    read_frags(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int cur = kk & 1;
+      if (kk + 1 < BK / 16) read_frags(kk + 1, cur ^ 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0,
+                                                              0, 0);
+    }
+  };
+
+  // One pipeline step: compute on stage (cur_a, cur_b) while tile kt + 1
+  // moves into the other stage, then a barrier.
+  auto step = [&](int kt, int KT, const uint8_t* cur_a, const uint8_t* cur_b, uint8_t* nxt_a,
+                  uint8_t* nxt_b) {
+    if (kt + 1 < KT) issue_loads(kt + 1, nxt_a, nxt_b);
+    compute(cur_a, cur_b);
+    if (kt + 1 < KT) stage_regs(nxt_a, nxt_b);
+    // The direct loads of the next tile and every read of this one are done
+    // before any wave moves on.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  };
+
+  const int KT = p.K / BK;
+  issue_loads(0, As0, Bs0);
+  stage_regs(As0, Bs0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    step(kt, KT, As0, Bs0, As1, Bs1);
+    step(kt + 1, KT, As1, Bs1, As0, Bs0);
+  }
+  if (kt < KT) step(kt, KT, As0, Bs0, As1, Bs1);
+
+  // ---- epilogue ----
+  const int lrow = (lane >> 5) * 4;
+  const int lcol = lane & 31;
+  if constexpr (EPI == EPI_SWIGLU) {
+    // B rows interleave 32 gate rows and 32 up rows, and a wave's column
+    // range starts on a multiple of 64: tile j = 2q holds gate columns and
+    // j = 2q + 1 the up columns for the same 32 act columns.
+    uint16_t* act = static_cast<uint16_t*>(p.C);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int q = 0; q < TN / 2; ++q) {
+        const int gcol = n0 + wn * WN + 2 * q * 32 + lcol;  // interleaved column of gate
+        const int col = (n0 + wn * WN) / 2 + q * 32 + lcol;  // act column
+        const f32x16 gt = acc[i][2 * q];
+        const f32x16 ut = acc[i][2 * q + 1];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
+          if (row < p.M && col < p.n_out) {
+            const float g = gt[r];
+            const float u = ut[r];
+            act[static_cast<int64_t>(row) * p.ldc + col] = f32_to_bf16(silu(g) * u);
+            if (p.gu) {
+              p.gu[static_cast<int64_t>(row) * p.ldgu + gcol] = f32_to_bf16(g);
+              p.gu[static_cast<int64_t>(row) * p.ldgu + gcol + 32] = f32_to_bf16(u);
+            }
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lcol;
+        const float bias = (p.bias && col < p.N) ? p.bias[col] : 0.0f;
+        const f32x16 t = acc[i][j];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
+          if (row < p.M && col < p.N) {
+            float x = t[r] + bias;
+            if constexpr (EPI == EPI_RESID) x = p.resid[static_cast<int64_t>(row) * p.ldr + col] + x;
+            const int64_t o = static_cast<int64_t>(row) * p.ldc + col;
+            if constexpr (OUT_BF16) static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(x);
+            else static_cast<float*>(p.C)[o] = x;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, bool AK, bool BKM, int EPI, bool OB>
+int launch(GemmParams p, hipStream_t s) {
+  p.grid_m = (p.M + BM - 1) / BM;
+  p.grid_n = (p.N + BN - 1) / BN;
+  const int64_t blocks = static_cast<int64_t>(p.grid_m) * p.grid_n;
+  if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_gemm: problem too large");
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BKM, EPI, OB>),
+                     dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s, p);
+  MR_LAUNCH_CHECK("mr_gemm");
+  return MR_OK;
+}
+
+// Large problems use 256 x 256 tiles; problems that would leave most of the
+// 256 CUs idle use 128 x 128.
+template <bool AK, bool BKM, int EPI, bool OB>
+int dispatch(GemmParams p, hipStream_t s) {
+  const int64_t big = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (big >= 256) return launch<256, 256, AK, BKM, EPI, OB>(p, s);
+  return launch<128, 128, AK, BKM, EPI, OB>(p, s);
+}
+
+bool ok16(const void* p, int64_t ld) {
+  return aligned16(p) && (ld % 8) == 0;
+}
+
+}  // namespace
+}  // namespace mr
+
+extern "C" {
+
+int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+            const void* B, int64_t ldb, void* C, int c_dtype, int64_t ldc, const float* bias,
+            const float* resid, int64_t ldr, void* stream) {
+  using namespace mr;
+  clear_error();
+  if (M < 0 || N < 0 || K < 0) return fail(MR_EINVAL, "mr_gemm: negative size");
+  if (M == 0 || N == 0) return MR_OK;
+  if (!A || !B || !C) return fail(MR_EINVAL, "mr_gemm: null operand");
+  if (M % 8 || N % 8 || K % BK || K == 0)
+    return fail(MR_EINVAL, "mr_gemm: M and N must be multiples of 8 and K a positive multiple of %d "
+                "(M=%lld N=%lld K=%lld)", BK, (long long)M, (long long)N, (long long)K);
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return fail(MR_EINVAL, "mr_gemm: too large");
+  if (!ok16(A, lda) || !ok16(B, ldb))
+    return fail(MR_EINVAL, "mr_gemm: operands must be 16-byte aligned with ld a multiple of 8");
+  if (c_dtype != MR_F32 && c_dtype != MR_BF16) return fail(MR_EINVAL, "mr_gemm: C must be fp32 or bf16");
+  if (resid && c_dtype != MR_F32) return fail(MR_EINVAL, "mr_gemm: the residual form writes fp32");
+  GemmParams p{};
+  p.M = static_cast<int>(M);
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.A = static_cast<const uint16_t*>(A);
+  p.lda = lda;
+  p.B = static_cast<const uint16_t*>(B);
+  p.ldb = ldb;
+  p.C = C;
+  p.ldc = ldc;
+  p.bias = bias;
+  p.resid = resid;
+  p.ldr = ldr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool ob = c_dtype == MR_BF16;
+#define MR_GEMM_CASE(AK, BKM)                                                             \
+  if (resid) return dispatch<AK, BKM, EPI_RESID, false>(p, s);                            \
+  return ob ? dispatch<AK, BKM, EPI_STORE, true>(p, s)                                    \
+            : dispatch<AK, BKM, EPI_STORE, false>(p, s);
+  switch (layout) {
+    case 0: { MR_GEMM_CASE(true, true) }    // NT: Y = X W^T
+    case 1: { MR_GEMM_CASE(true, false) }   // NN: dX = dY W
+    case 2: { MR_GEMM_CASE(false, false) }  // TN: dW = dY^T X
+    default: return fail(MR_EINVAL, "mr_gemm: unknown layout %d", layout);
+  }
+#undef MR_GEMM_CASE
+}
+
+int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* Wgu,
+                   int64_t ldw, void* act, int64_t ldact, void* gu, int64_t ldgu, void* stream) {
+  using namespace mr;
+  clear_error();
+  if (M <= 0 || N <= 0) return MR_OK;
+  if (!X || !Wgu || !act) return fail(MR_EINVAL, "mr_gemm_swiglu: null operand");
+  if (M % 8 || N % 32 || K % BK || K == 0)
+    return fail(MR_EINVAL, "mr_gemm_swiglu: M %% 8, N %% 32 and K %% %d must be 0", BK);
+  if (!ok16(X, ldx) || !ok16(Wgu, ldw))
+    return fail(MR_EINVAL, "mr_gemm_swiglu: operands must be 16-byte aligned");
+  GemmParams p{};
+  p.M = static_cast<int>(M);
+  p.N = static_cast<int>(2 * N);
+  p.n_out = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.A = static_cast<const uint16_t*>(X);
+  p.lda = ldx;
+  p.B = static_cast<const uint16_t*>(Wgu);
+  p.ldb = ldw;
+  p.C = act;
+  p.ldc = ldact;
+  p.gu = static_cast<uint16_t*>(gu);
+  p.ldgu = ldgu;
+  return dispatch<true, true, EPI_SWIGLU, true>(p, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -28,6 +28,24 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// Row placement of the reconstruction (forward) or of the gradient (backward)
+// inside a larger row-major buffer with the same column count: row r lives at
+// (r / blk) * stride + off + r % blk; blk == 0 is the identity.
+struct RowMap {
+  int64_t blk, stride, off;
+  int cpr;  // 8-element chunks per row (fast kernels)
+  __device__ __forceinline__ int64_t row(int64_t r) const {
+    return blk ? (r / blk) * stride + off + r % blk : r;
+  }
+  // Element index of chunk `chunk` (8 elements) under the placement.
+  __device__ __forceinline__ int64_t chunk_elem(int64_t chunk) const {
+    if (!blk) return chunk * 8;
+    const int c32 = static_cast<int>(chunk);
+    const int r = c32 / cpr;
+    return (row(r) * cpr + (c32 - r * cpr)) * 8;
+  }
+};
+
 struct Group {
   float s;         // scale (signed under the symmetric modes)
   float zp;        // zero point (asymmetric)
@@ -155,7 +173,8 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
     const void* __restrict__ w, const float* __restrict__ v, const float* __restrict__ alpha,
     const float* __restrict__ beta, const float* __restrict__ init_scale, void* __restrict__ wq,
     uint8_t* __restrict__ codes, float* __restrict__ scale_out, float* __restrict__ zp_out,
-    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps) {
+    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps,
+    RowMap map) {
   int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const bool active = chunk < n_chunks;
   // Inactive lanes form whole groups (n_chunks % tpg == 0); they stay for the
@@ -198,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
     q[k] = quant_one<MODE, HAS_V>(x[k], vv[k], p, qmin, qmax, c[k], in);
   }
   if (!active) return;
-  if (wq) store8<OT>(wq, e, q);
+  if (wq) store8<OT>(wq, map.chunk_elem(chunk), q);
   if (codes) {
     uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -233,7 +252,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_generic(
     const float* __restrict__ init_scale, void* __restrict__ wq, int ot,
     uint8_t* __restrict__ codes, float* __restrict__ scale_out, float* __restrict__ zp_out,
     int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float qmin, float qmax,
-    float eps) {
+    float eps, RowMap map) {
   const int64_t grp = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   if (grp >= rows * ng) return;  // uniform across the wave
@@ -264,7 +283,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_generic(
     if constexpr (HAS_V) vv = v[grp * gs + t];
     float code, in;
     float q = quant_one<MODE, HAS_V>(x, vv, p, qmin, qmax, code, in);
-    if (wq && c < cols) store_any(wq, ot, r * cols + c, q);
+    if (wq && c < cols) store_any(wq, ot, map.row(r) * cols + c, q);
     if (codes) codes[grp * gs + t] = static_cast<uint8_t>(static_cast<int>(code) & 0xff);
   }
   if (lane == 0) {
@@ -342,7 +361,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
     float* __restrict__ beta, const float* __restrict__ init_scale, const void* __restrict__ g,
     int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps,
     StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
-    float* __restrict__ gb_out) {
+    float* __restrict__ gb_out, RowMap map) {
   int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const bool active = chunk < n_chunks;
   if (!active) chunk = n_chunks - 1;
@@ -352,7 +371,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
   float x[8], vv[8], gg[8];
   load8<WT>(w, e, x);
   load8_f32(v, e, vv);
-  load8<GT>(g, e, gg);
+  load8<GT>(g, map.chunk_elem(chunk), gg);
   float mx = x[0], mn = x[0];
 #pragma unroll
   for (int k = 1; k < 8; ++k) {
@@ -409,7 +428,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
     float* __restrict__ beta, const float* __restrict__ init_scale, const void* __restrict__ g,
     int gt, int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float qmin, float qmax,
     float eps, StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
-    float* __restrict__ gb_out) {
+    float* __restrict__ gb_out, RowMap map) {
   const int64_t grp = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   if (grp >= rows * ng) return;
@@ -437,7 +456,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
     int64_t c = c0 + t;
     bool real = c < cols;
     float x = real ? load_any(w, wt, r * cols + c) : 0.0f;
-    float gg = real ? load_any(g, gt, r * cols + c) : 0.0f;
+    float gg = real ? load_any(g, gt, map.row(r) * cols + c) : 0.0f;
     float vv = v[grp * gs + t];
     BwdTerms<MODE> tm = bwd_one<MODE>(x, vv, gg, p, wmin_over_s, qmin, qmax);
     sum_s = sum_s + tm.ts;
@@ -508,7 +527,8 @@ int check_common(const char* fn, const void* w, int w_dtype, int64_t rows, int64
 template <int MODE, bool HAS_V>
 int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const float* alpha,
                const float* beta, const float* init_scale, void* wq, int ot, uint8_t* codes,
-               float* scale_out, float* zp_out, float eps, hipStream_t stream) {
+               float* scale_out, float* zp_out, float eps, RowMap map, hipStream_t stream) {
+  map.cpr = static_cast<int>(sh.cols / 8);
   const bool fast_types = (wt == MR_F32 || wt == MR_BF16) && (!wq || ot == MR_F32 || ot == MR_BF16);
   const bool fast_align = aligned16(w) && (!HAS_V || aligned16(v)) && (!wq || aligned16(wq)) &&
                           (!codes || (reinterpret_cast<uintptr_t>(codes) & 7u) == 0);
@@ -520,7 +540,7 @@ int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const flo
   hipLaunchKernelGGL((fq_fwd_fast<WT_, OT_, MODE, HAS_V, T_>),                             \
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, w, v, alpha, \
                      beta, init_scale, wq, codes, scale_out, zp_out, n_chunks, sh.tpg,       \
-                     sh.tpg_shift, sh.maxq, sh.qmin, sh.qmax, eps)
+                     sh.tpg_shift, sh.maxq, sh.qmin, sh.qmax, eps, map)
 #define MR_FWD_FAST(WT_, OT_)                                               \
   do {                                                                      \
     if (sh.tpg == 8) MR_FWD_FAST_T(WT_, OT_, 8);                            \
@@ -541,7 +561,7 @@ int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const flo
     hipLaunchKernelGGL((fq_fwd_generic<MODE, HAS_V>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kBlock), 0, stream, w, wt, v, alpha, beta, init_scale, wq, ot, codes,
                        scale_out, zp_out, sh.rows, sh.cols, sh.gs, sh.ng, sh.maxq, sh.qmin,
-                       sh.qmax, eps);
+                       sh.qmax, eps, map);
   }
   MR_LAUNCH_CHECK("mr_fq_forward");
   return MR_OK;
@@ -550,7 +570,8 @@ int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const flo
 template <int MODE, bool UPDATE>
 int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, float* beta,
                const float* init_scale, const void* g, int gt, float eps, StepArgs st,
-               float* gv_out, float* ga_out, float* gb_out, hipStream_t stream) {
+               float* gv_out, float* ga_out, float* gb_out, RowMap map, hipStream_t stream) {
+  map.cpr = static_cast<int>(sh.cols / 8);
   const bool fast_types = (wt == MR_F32 || wt == MR_BF16) && (gt == MR_F32 || gt == MR_BF16);
   const bool fast_align = aligned16(w) && aligned16(v) && aligned16(g) && (!gv_out || aligned16(gv_out));
   if (sh.fast && fast_types && fast_align) {
@@ -561,7 +582,7 @@ int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, f
   hipLaunchKernelGGL((fq_bwd_fast<WT_, GT_, MODE, UPDATE, T_>),                             \
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, w, v, alpha, \
                      beta, init_scale, g, n_chunks, sh.tpg, sh.tpg_shift, sh.maxq, sh.qmin,   \
-                     sh.qmax, eps, st, gv_out, ga_out, gb_out)
+                     sh.qmax, eps, st, gv_out, ga_out, gb_out, map)
 #define MR_BWD_FAST(WT_, GT_)                                               \
   do {                                                                      \
     if (sh.tpg == 8) MR_BWD_FAST_T(WT_, GT_, 8);                            \
@@ -581,7 +602,7 @@ int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, f
     hipLaunchKernelGGL((fq_bwd_generic<MODE, UPDATE>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kBlock), 0, stream, w, wt, v, alpha, beta, init_scale, g, gt, sh.rows,
                        sh.cols, sh.gs, sh.ng, sh.maxq, sh.qmin, sh.qmax, eps, st, gv_out, ga_out,
-                       gb_out);
+                       gb_out, map);
   }
   MR_LAUNCH_CHECK("mr_fq_backward_signsgd");
   return MR_OK;
@@ -592,37 +613,97 @@ int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, f
 
 extern "C" {
 
-int mr_fq_forward(const void* w, int w_dtype, const float* v, const float* alpha,
-                  const float* beta, const float* init_scale, int64_t rows, int64_t cols,
-                  int group_size, int bits, int mode, float eps, void* wq_out, int wq_dtype,
-                  void* codes_out, float* scale_out, float* zp_out, void* stream) {
+static int fq_forward_impl(const char* fn, const void* w, int w_dtype, const float* v,
+                           const float* alpha, const float* beta, const float* init_scale,
+                           int64_t rows, int64_t cols, int group_size, int bits, int mode, float eps,
+                           void* wq_out, int wq_dtype, void* codes_out, float* scale_out,
+                           float* zp_out, mr::RowMap map, void* stream) {
   using namespace mr;
   clear_error();
   Shape sh;
-  int rc = check_common("mr_fq_forward", w, w_dtype, rows, cols, group_size, bits, mode,
-                        init_scale, sh);
+  int rc = check_common(fn, w, w_dtype, rows, cols, group_size, bits, mode, init_scale, sh);
   if (rc) return rc;
   if (rows == 0 || cols == 0) return MR_OK;
   const bool any_v = v || alpha || beta;
   if (any_v && !(v && alpha && beta))
-    return fail(MR_EINVAL, "mr_fq_forward: v, alpha and beta are given together or not at all");
+    return fail(MR_EINVAL, "%s: v, alpha and beta are given together or not at all", fn);
   if (!wq_out && !codes_out && !scale_out && !zp_out)
-    return fail(MR_EINVAL, "mr_fq_forward: no output requested");
+    return fail(MR_EINVAL, "%s: no output requested", fn);
   if (wq_out && !valid_dtype(wq_dtype))
-    return fail(MR_EINVAL, "mr_fq_forward: unknown output dtype %d", wq_dtype);
+    return fail(MR_EINVAL, "%s: unknown output dtype %d", fn, wq_dtype);
   if (zp_out && mode != MR_ASYM)
-    return fail(MR_EINVAL, "mr_fq_forward: a zero point exists only in the asymmetric mode");
+    return fail(MR_EINVAL, "%s: a zero point exists only in the asymmetric mode", fn);
+  if (map.blk < 0 || map.stride < 0 || map.off < 0)
+    return fail(MR_EINVAL, "%s: negative row placement", fn);
+  if (map.blk && rows * cols / 8 > 0x7fffffffLL)
+    return fail(MR_EINVAL, "%s: placed tensor too large", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* codes = static_cast<uint8_t*>(codes_out);
 #define MR_FWD(MODE_)                                                                     \
   return any_v ? launch_fwd<MODE_, true>(sh, w, w_dtype, v, alpha, beta, init_scale, wq_out, \
-                                         wq_dtype, codes, scale_out, zp_out, eps, s)       \
+                                         wq_dtype, codes, scale_out, zp_out, eps, map, s)  \
                : launch_fwd<MODE_, false>(sh, w, w_dtype, v, alpha, beta, init_scale, wq_out, \
-                                          wq_dtype, codes, scale_out, zp_out, eps, s)
+                                          wq_dtype, codes, scale_out, zp_out, eps, map, s)
   if (mode == MR_ASYM) MR_FWD(MR_ASYM);
   if (mode == MR_SYM) MR_FWD(MR_SYM);
   MR_FWD(MR_SYM_SEARCHED);
 #undef MR_FWD
+}
+
+int mr_fq_forward(const void* w, int w_dtype, const float* v, const float* alpha,
+                  const float* beta, const float* init_scale, int64_t rows, int64_t cols,
+                  int group_size, int bits, int mode, float eps, void* wq_out, int wq_dtype,
+                  void* codes_out, float* scale_out, float* zp_out, void* stream) {
+  return fq_forward_impl("mr_fq_forward", w, w_dtype, v, alpha, beta, init_scale, rows, cols,
+                         group_size, bits, mode, eps, wq_out, wq_dtype, codes_out, scale_out, zp_out,
+                         mr::RowMap{0, 0, 0, 0}, stream);
+}
+
+int mr_fq_forward_mapped(const void* w, int w_dtype, const float* v, const float* alpha,
+                         const float* beta, const float* init_scale, int64_t rows, int64_t cols,
+                         int group_size, int bits, int mode, float eps, void* wq_out, int wq_dtype,
+                         int64_t row_block, int64_t row_stride, int64_t row_offset, void* stream) {
+  if (!wq_out) return mr::fail(MR_EINVAL, "mr_fq_forward_mapped: no output");
+  return fq_forward_impl("mr_fq_forward_mapped", w, w_dtype, v, alpha, beta, init_scale, rows,
+                         cols, group_size, bits, mode, eps, wq_out, wq_dtype, nullptr, nullptr,
+                         nullptr, mr::RowMap{row_block, row_stride, row_offset, 0}, stream);
+}
+
+static int fq_backward_impl(const char* fn, const void* w, int w_dtype, float* v, float* alpha,
+                            float* beta, const float* init_scale, const void* g, int g_dtype,
+                            int64_t rows, int64_t cols, int group_size, int bits, int mode,
+                            float eps, int update, float lr, float coef_lo, float coef_hi,
+                            float v_bound, float* grad_v_out, float* grad_alpha_out,
+                            float* grad_beta_out, mr::RowMap map, void* stream) {
+  using namespace mr;
+  clear_error();
+  Shape sh;
+  int rc = check_common(fn, w, w_dtype, rows, cols, group_size, bits, mode, init_scale, sh);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return MR_OK;
+  if (!v || !alpha || !beta) return fail(MR_EINVAL, "%s: v, alpha and beta are required", fn);
+  if (!g) return fail(MR_EINVAL, "%s: gradient pointer is null", fn);
+  if (!valid_dtype(g_dtype)) return fail(MR_EINVAL, "%s: unknown gradient dtype %d", fn, g_dtype);
+  if (!update && !grad_v_out && !grad_alpha_out && !grad_beta_out)
+    return fail(MR_EINVAL, "%s: nothing to do (no update, no gradient output)", fn);
+  if (update && !(coef_lo <= coef_hi && v_bound >= 0.0f)) return fail(MR_EINVAL, "%s: bad bounds", fn);
+  if (map.blk < 0 || map.stride < 0 || map.off < 0)
+    return fail(MR_EINVAL, "%s: negative row placement", fn);
+  if (map.blk && rows * cols / 8 > 0x7fffffffLL)
+    return fail(MR_EINVAL, "%s: placed tensor too large", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  StepArgs st{lr, coef_lo, coef_hi, v_bound};
+#define MR_BWD(MODE_)                                                                       \
+  return update ? launch_bwd<MODE_, true>(sh, w, w_dtype, v, alpha, beta, init_scale, g,     \
+                                          g_dtype, eps, st, grad_v_out, grad_alpha_out,      \
+                                          grad_beta_out, map, s)                             \
+                : launch_bwd<MODE_, false>(sh, w, w_dtype, v, alpha, beta, init_scale, g,    \
+                                           g_dtype, eps, st, grad_v_out, grad_alpha_out,     \
+                                           grad_beta_out, map, s)
+  if (mode == MR_ASYM) MR_BWD(MR_ASYM);
+  if (mode == MR_SYM) MR_BWD(MR_SYM);
+  MR_BWD(MR_SYM_SEARCHED);
+#undef MR_BWD
 }
 
 int mr_fq_backward_signsgd(const void* w, int w_dtype, float* v, float* alpha, float* beta,
@@ -631,35 +712,22 @@ int mr_fq_backward_signsgd(const void* w, int w_dtype, float* v, float* alpha, f
                            int update, float lr, float coef_lo, float coef_hi, float v_bound,
                            float* grad_v_out, float* grad_alpha_out, float* grad_beta_out,
                            void* stream) {
-  using namespace mr;
-  clear_error();
-  Shape sh;
-  int rc = check_common("mr_fq_backward_signsgd", w, w_dtype, rows, cols, group_size, bits, mode,
-                        init_scale, sh);
-  if (rc) return rc;
-  if (rows == 0 || cols == 0) return MR_OK;
-  if (!v || !alpha || !beta)
-    return fail(MR_EINVAL, "mr_fq_backward_signsgd: v, alpha and beta are required");
-  if (!g) return fail(MR_EINVAL, "mr_fq_backward_signsgd: gradient pointer is null");
-  if (!valid_dtype(g_dtype))
-    return fail(MR_EINVAL, "mr_fq_backward_signsgd: unknown gradient dtype %d", g_dtype);
-  if (!update && !grad_v_out && !grad_alpha_out && !grad_beta_out)
-    return fail(MR_EINVAL, "mr_fq_backward_signsgd: nothing to do (no update, no gradient output)");
-  if (update && !(coef_lo <= coef_hi && v_bound >= 0.0f))
-    return fail(MR_EINVAL, "mr_fq_backward_signsgd: bad bounds");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  StepArgs st{lr, coef_lo, coef_hi, v_bound};
-#define MR_BWD(MODE_)                                                                       \
-  return update ? launch_bwd<MODE_, true>(sh, w, w_dtype, v, alpha, beta, init_scale, g,     \
-                                          g_dtype, eps, st, grad_v_out, grad_alpha_out,      \
-                                          grad_beta_out, s)                                  \
-                : launch_bwd<MODE_, false>(sh, w, w_dtype, v, alpha, beta, init_scale, g,    \
-                                           g_dtype, eps, st, grad_v_out, grad_alpha_out,     \
-                                           grad_beta_out, s)
-  if (mode == MR_ASYM) MR_BWD(MR_ASYM);
-  if (mode == MR_SYM) MR_BWD(MR_SYM);
-  MR_BWD(MR_SYM_SEARCHED);
-#undef MR_BWD
+  return fq_backward_impl("mr_fq_backward_signsgd", w, w_dtype, v, alpha, beta, init_scale, g,
+                          g_dtype, rows, cols, group_size, bits, mode, eps, update, lr, coef_lo,
+                          coef_hi, v_bound, grad_v_out, grad_alpha_out, grad_beta_out,
+                          mr::RowMap{0, 0, 0, 0}, stream);
+}
+
+int mr_fq_backward_signsgd_mapped(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                                  const float* init_scale, const void* g, int g_dtype,
+                                  int64_t rows, int64_t cols, int group_size, int bits, int mode,
+                                  float eps, float lr, float coef_lo, float coef_hi, float v_bound,
+                                  int64_t row_block, int64_t row_stride, int64_t row_offset,
+                                  void* stream) {
+  return fq_backward_impl("mr_fq_backward_signsgd_mapped", w, w_dtype, v, alpha, beta, init_scale,
+                          g, g_dtype, rows, cols, group_size, bits, mode, eps, 1, lr, coef_lo,
+                          coef_hi, v_bound, nullptr, nullptr, nullptr,
+                          mr::RowMap{row_block, row_stride, row_offset, 0}, stream);
 }
 
 }  // extern "C"

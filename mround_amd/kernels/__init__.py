@@ -71,6 +71,12 @@ _SIGNATURES = {
     "mr_delta_loss_workspace_bytes": (ctypes.c_size_t, [_L, _L, _I]),
     "mr_delta_loss": (_I, [_P, _I, _P, _L, _L, _I, _P, _I, _I, _F, _P, _P, _P]),
     "mr_copy_bytes": (_I, [_P, _P, ctypes.c_size_t, _P]),
+    "mr_gemm": (_I, [_I, _L, _L, _L, _P, _L, _P, _L, _P, _I, _L, _P, _P, _L, _P]),
+    "mr_gemm_swiglu": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P]),
+    "mr_fq_forward_mapped": (_I, [_P, _I, _P, _P, _P, _P, _L, _L, _I, _I, _I, _F, _P, _I, _L, _L,
+                                  _L, _P]),
+    "mr_fq_backward_signsgd_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F,
+                                           _F, _F, _F, _F, _L, _L, _L, _P]),
 }
 
 
@@ -245,6 +251,58 @@ def delta_loss(weight, grad, *, group_size, bits_list, mode, eps, scores_out, wo
                              cols, group_size, arr, n_bits, MODE[mode], eps, _ptr(scores_out),
                              _ptr(workspace), _stream(weight))
     _check(rc, "mr_delta_loss")
+
+
+# -------------------------------------------------------------------- GEMM --
+
+GEMM_LAYOUT = {"nt": 0, "nn": 1, "tn": 2}
+
+
+def gemm(layout: str, a, b, c, *, M, N, K, bias=None, resid=None) -> None:
+    """``mr_gemm``: C = op(A) op(B) (+ bias) (+ resid); leading dims from strides."""
+    rc = lib().mr_gemm(GEMM_LAYOUT[layout], M, N, K, _ptr(a), a.stride(0), _ptr(b), b.stride(0),
+                       _ptr(c), dtype_code(c.dtype), c.stride(0), _ptr(_f32(bias, "bias")),
+                       _ptr(_f32(resid, "resid")), resid.stride(0) if resid is not None else 0,
+                       _stream(a))
+    _check(rc, "mr_gemm")
+
+
+def gemm_swiglu(x, wgu, act, gu=None) -> None:
+    """``mr_gemm_swiglu`` over the 32-row interleaved gate/up weight ``wgu`` [2N, K]."""
+    M, K = x.shape
+    N = wgu.shape[0] // 2
+    rc = lib().mr_gemm_swiglu(M, N, K, _ptr(x), x.stride(0), _ptr(wgu), wgu.stride(0), _ptr(act),
+                              act.stride(0), _ptr(gu), gu.stride(0) if gu is not None else 0,
+                              _stream(x))
+    _check(rc, "mr_gemm_swiglu")
+
+
+def fq_forward_mapped(weight, v, alpha, beta, *, bits, group_size, mode, eps, wq_out, row_block,
+                      row_stride, row_offset, init_scale=None) -> None:
+    """``mr_fq_forward_mapped``: W' rows placed inside the larger ``wq_out``."""
+    rows, cols = weight.shape
+    if wq_out.shape[1] != cols:
+        raise KernelError("the placed output must have the weight's column count")
+    rc = lib().mr_fq_forward_mapped(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(v, "v")), _ptr(_f32(alpha, "alpha")),
+        _ptr(_f32(beta, "beta")), _ptr(_f32(init_scale, "init_scale")), rows, cols, group_size,
+        bits, MODE[mode], eps, _ptr(wq_out), dtype_code(wq_out.dtype), row_block, row_stride,
+        row_offset, _stream(weight))
+    _check(rc, "mr_fq_forward_mapped")
+
+
+def fq_step_mapped(weight, v, alpha, beta, grad, *, bits, group_size, mode, eps, lr, coef_lo,
+                   coef_hi, v_bound, row_block, row_stride, row_offset, init_scale=None) -> None:
+    """``mr_fq_backward_signsgd_mapped``: fused step, dL/dW' read from a placed buffer."""
+    rows, cols = weight.shape
+    if grad.shape[1] != cols:
+        raise KernelError("the placed gradient must have the weight's column count")
+    rc = lib().mr_fq_backward_signsgd_mapped(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(v, "v")), _ptr(_f32(alpha, "alpha")),
+        _ptr(_f32(beta, "beta")), _ptr(_f32(init_scale, "init_scale")), _ptr(grad),
+        dtype_code(grad.dtype), rows, cols, group_size, bits, MODE[mode], eps, lr, coef_lo, coef_hi,
+        v_bound, row_block, row_stride, row_offset, _stream(weight))
+    _check(rc, "mr_fq_backward_signsgd_mapped")
 
 
 def copy_bytes(src, dst, nbytes: int) -> None:

@@ -1,0 +1,117 @@
+"""GPU parity of the MFMA GEMMs against a float64 CPU product of the same bf16 inputs.
+
+The inputs are bf16 (exact in fp32), the products are exact in fp32, and the
+only error is fp32 accumulation: |C - ref| <= K * 2^-23 * (|A| |B|) elementwise.
+bf16 outputs add one rounding (2^-8 relative).
+"""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from mround_amd import kernels as K
+from tests.helpers import dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(*shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(torch.bfloat16)
+
+
+def _bound(a64, b64, k):
+    return (a64.abs() @ b64.abs()) * (k * 2.0**-23) + 1e-30
+
+
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (200, 136, 128), (1024, 512, 320), (8, 8, 64),
+                                 (576, 192, 576), (4096, 576, 1536), (512, 768, 896)])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_gemm_layouts(layout, mnk, out):
+    M, N, Kd = mnk
+    print("case gemm", layout, mnk, out, flush=True, file=sys.stderr)
+    if layout == "nt":
+        a, b = _rand(M, Kd, seed=1), _rand(N, Kd, seed=2)
+        a64, b64 = a.double(), b.double().t()
+    elif layout == "nn":
+        a, b = _rand(M, Kd, seed=3), _rand(Kd, N, seed=4)
+        a64, b64 = a.double(), b.double()
+    else:
+        a, b = _rand(Kd, M, seed=5), _rand(Kd, N, seed=6)
+        a64, b64 = a.double().t(), b.double()
+    ref = a64 @ b64
+    c = torch.empty(M, N, dtype=out, device=dev())
+    K.gemm(layout, a.to(dev()), b.to(dev()), c, M=M, N=N, K=Kd)
+    got = c.double().cpu()
+    tol = _bound(a64, b64, Kd)
+    if out == torch.bfloat16:
+        tol = tol + ref.abs() * 2.0**-8
+    assert torch.all((got - ref).abs() <= tol), float(((got - ref).abs() / tol).max())
+
+
+def test_gemm_bias_and_residual():
+    M, N, Kd = 304, 264, 128
+    a, b = _rand(M, Kd, seed=7), _rand(N, Kd, seed=8)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(9))
+    resid = torch.randn(M, N, generator=torch.Generator().manual_seed(10))
+    ref = resid.double() + (a.double() @ b.double().t() + bias.double())
+    c = torch.empty(M, N, device=dev())
+    K.gemm("nt", a.to(dev()), b.to(dev()), c, M=M, N=N, K=Kd, bias=bias.to(dev()),
+           resid=resid.to(dev()))
+    tol = _bound(a.double(), b.double().t(), Kd) + ref.abs() * 2.0**-23 * 4
+    assert torch.all((c.double().cpu() - ref).abs() <= tol)
+
+
+def interleave_gate_up(wg, wu):
+    """Rows 64b..64b+31 = gate rows 32b.., rows 64b+32.. = the matching up rows."""
+    n, k = wg.shape
+    return torch.stack([wg.reshape(n // 32, 32, k), wu.reshape(n // 32, 32, k)], 1).reshape(2 * n, k)
+
+
+@pytest.mark.parametrize("mnk", [(512, 256, 128), (200, 96, 64), (4096, 1536, 576), (1024, 4864, 896)])
+def test_swiglu(mnk):
+    M, N, Kd = mnk
+    x, wg, wu = _rand(M, Kd, seed=11), _rand(N, Kd, seed=12), _rand(N, Kd, seed=13)
+    g = x.double() @ wg.double().t()
+    u = x.double() @ wu.double().t()
+    act_ref = torch.nn.functional.silu(g) * u
+    act = torch.empty(M, N, dtype=torch.bfloat16, device=dev())
+    gu = torch.empty(M, 2 * N, dtype=torch.bfloat16, device=dev())
+    K.gemm_swiglu(x.to(dev()), interleave_gate_up(wg, wu).to(dev()), act, gu)
+    tg = _bound(x.double(), wg.double().t(), Kd)
+    tu = _bound(x.double(), wu.double().t(), Kd)
+    gu_c = gu.double().cpu().reshape(M, N // 32, 2, 32)
+    got_g = gu_c[:, :, 0, :].reshape(M, N)
+    got_u = gu_c[:, :, 1, :].reshape(M, N)
+    assert torch.all((got_g - g).abs() <= tg + g.abs() * 2.0**-8)
+    assert torch.all((got_u - u).abs() <= tu + u.abs() * 2.0**-8)
+    # act from fp32 g, u: silu' <= 1.1, plus the bf16 rounding of act and the fast exp
+    tol = (1.1 * tg * u.abs() + tu * torch.nn.functional.silu(g).abs() + act_ref.abs() * 2.0**-7
+           + 1e-6)
+    assert torch.all((act.double().cpu() - act_ref).abs() <= tol)
+
+
+def test_nn_over_interleaved_pair_equals_sum():
+    """dx = dgu Wgu over the interleaved K = 2N equals dgate Wg + dup Wu."""
+    M, N, Kd = 256, 192, 128
+    dg, du = _rand(M, N, seed=14), _rand(M, N, seed=15)
+    wg, wu = _rand(N, Kd, seed=16), _rand(N, Kd, seed=17)
+    dgu = torch.stack([dg.reshape(M, N // 32, 32), du.reshape(M, N // 32, 32)], 2).reshape(M, 2 * N)
+    wgu = interleave_gate_up(wg, wu)
+    ref = dg.double() @ wg.double() + du.double() @ wu.double()
+    c = torch.empty(M, Kd, device=dev())
+    K.gemm("nn", dgu.to(dev()), wgu.to(dev()), c, M=M, N=Kd, K=2 * N)
+    tol = _bound(dgu.double(), wgu.double(), 2 * N)
+    assert torch.all((c.double().cpu() - ref).abs() <= tol)
+
+
+def test_gemm_rejects_bad_shapes():
+    a = torch.zeros(10, 64, dtype=torch.bfloat16, device=dev())
+    b = torch.zeros(16, 64, dtype=torch.bfloat16, device=dev())
+    c = torch.zeros(10, 16, device=dev())
+    with pytest.raises(Exception, match="multiples of 8"):
+        K.gemm("nt", a, b, c, M=10, N=16, K=64)

@@ -168,3 +168,37 @@ def test_zero_rows_and_validation():
     with pytest.raises(ValueError, match="searched scale"):
         QZ.fake_quantize(torch.zeros(4, 64, device=dev()), None,
                          QuantScheme(bits=4, group_size=64, scale_init="searched"))
+
+
+@pytest.mark.parametrize("shape", [(64, 512, 64), (96, 256, 32), (32, 200, -1)])
+def test_mapped_placement(shape):
+    """W' rows placed in a stacked / interleaved buffer, gradients read back the same way."""
+    from mround_amd import kernels as K
+
+    rows, cols, gs = shape
+    scheme = QuantScheme(bits=2, group_size=gs, symmetry="asym")
+    w = weight(rows, cols, seed=rows).to(dev())
+    v, a, b = params(rows, cols, gs, seed=3, coef_jitter=0.2)
+    ref = QZ.fake_quantize(w, {"v": v.to(dev()), "alpha": a.to(dev()), "beta": b.to(dev())}, scheme)
+    big = torch.zeros(2 * rows + 64, cols, dtype=torch.bfloat16, device=dev())
+    for blk, stride, off in ((rows, 0, 17), (32, 64, 32), (32, 64, 0)):
+        if blk == 32 and rows % 32:
+            continue
+        big.zero_()
+        K.fq_forward_mapped(w, v.to(dev()), a.to(dev()), b.to(dev()), bits=2, group_size=gs,
+                            mode="asym", eps=1e-8, wq_out=big, row_block=blk, row_stride=stride,
+                            row_offset=off)
+        idx = torch.tensor([(r // blk) * stride + off + r % blk for r in range(rows)])
+        assert torch.equal(big[idx.to(dev())], ref)
+        # the fused step reading g from the same placement equals the plain one
+        g = torch.randn(rows, cols, generator=torch.Generator().manual_seed(5)).to(dev()) * 1e-3
+        gbig = torch.zeros(2 * rows + 64, cols, device=dev())
+        gbig[idx.to(dev())] = g
+        p1 = {"v": v.clone().to(dev()), "alpha": a.clone().to(dev()), "beta": b.clone().to(dev())}
+        p2 = {k: t.clone() for k, t in p1.items()}
+        SG.fused_step(w, p1, g, scheme, 0.005)
+        K.fq_step_mapped(w, p2["v"], p2["alpha"], p2["beta"], gbig, bits=2, group_size=gs,
+                         mode="asym", eps=1e-8, lr=0.005, coef_lo=0.1, coef_hi=1.0, v_bound=0.5,
+                         row_block=blk, row_stride=stride, row_offset=off)
+        for k in p1:
+            assert torch.equal(p1[k], p2[k]), k

@@ -190,6 +190,59 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
 int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* Wgu,
                    int64_t ldw, void* act, int64_t ldact, void* gu, int64_t ldgu, void* stream);
 
+/*
+ * Input gradient of the down projection fused with the SwiGLU backward:
+ * dact = dd Wd (dd [M, K] bf16, Wd [K, N] bf16 = down weight [hidden, inter]),
+ * then from the saved gu (mr_gemm_swiglu's interleaved gate/up):
+ *   dgate = dact * u * silu'(g), dup = dact * silu(g), written interleaved to
+ *   dgu [M, 2N] bf16 (same layout as gu). The MLX autodiff of the mlp's
+ *   silu(g) * u and down linear (mround/pipeline/runner.py:920).
+ */
+int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t ldd,
+                       const void* Wd, int64_t ldw, const void* gu, int64_t ldgu, void* dgu,
+                       int64_t lddgu, void* stream);
+
+/*
+ * RMSNorm over rows of the fp32 residual stream, y = h rsqrt(mean(h^2) + eps) w
+ * as bf16 (the next GEMM's operand) plus the per-row rsqrt for the backward;
+ * the backward adds the residual gradient: dh = dres + d(rmsnorm)/dh^T dy.
+ * mlx-lm's RMSNorm in the block (mround/pipeline/blocks.py:605).
+ */
+int mr_rmsnorm_fwd(const float* h, const float* w, int64_t T, int64_t H, float eps, void* y_bf16,
+                   float* rstd_out, void* stream);
+int mr_rmsnorm_bwd(const float* dy, const float* h, const float* w, const float* rstd,
+                   const float* dres, int64_t T, int64_t H, void* dh_bf16, float* dh_f32,
+                   void* stream);
+
+/*
+ * Rotary embedding (non-interleaved halves) in place on the first n_heads
+ * heads of rows of x (bf16, leading dimension ld), position = row % S, with
+ * cos/sin from cos_sin [S, head_dim/2, 2] fp32; backward = 1 applies the
+ * transpose rotation to gradients. mlx-lm's rope (traditional=False).
+ */
+int mr_rope(void* x_bf16, int64_t ld, int64_t T, int S, int n_heads, int head_dim,
+            const float* cos_sin, int backward, void* stream);
+
+/*
+ * Causal grouped-query attention on the packed bf16 qkv rows [B*S, ld]
+ * (q heads, then k heads, then v heads; query head h uses kv head
+ * h / (Hq / Hkv)), head_dim 64 or 128, S a multiple of 128. The forward
+ * writes out [B*S, Hq*head_dim] bf16 (leading dimension ldo) and the natural
+ * log-sum-exp per (b, h, s) for the backward. The backward takes dout, writes
+ * the gradient of the (post-rope) q/k/v into dqkv (same layout as qkv) and
+ * uses dsum_ws (B*Hq*S floats) as workspace. The scaled-dot-product
+ * attention of the mlx-lm block (mround/pipeline/blocks.py:605) and its
+ * autodiff.
+ */
+int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int head_dim,
+                float scale, void* out, int64_t ldo, float* lse, void* stream);
+int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, int64_t ldo,
+                const float* lse, float* dsum_ws, int B, int S, int Hq, int Hkv, int head_dim,
+                float scale, void* dqkv, void* stream);
+
+/* fp32 -> bf16 (round to nearest even), n elements. */
+int mr_cast_f32_bf16(const float* x, void* y, int64_t n, void* stream);
+
 /* Plain device copy of `bytes` bytes, used to calibrate traffic counters. */
 int mr_copy_bytes(const void* src, void* dst, size_t bytes, void* stream);
 

@@ -45,6 +45,7 @@ enum Epi : int {
   EPI_STORE = 0,   // C = acc (+ bias[n])
   EPI_RESID = 1,   // C = resid[m, n] + acc (+ bias[n]), fp32
   EPI_SWIGLU = 2,  // act = silu(g) * u from row-interleaved gate/up weights
+  EPI_SWIGLU_BWD = 3,  // dgu (interleaved) from dact = acc and the saved gate/up
 };
 
 struct GemmParams {
@@ -60,7 +61,7 @@ struct GemmParams {
   const float* resid;
   int64_t ldr;
   uint16_t* gu;        // SWIGLU: gate/up copy, [M, 2 * n_out] bf16, interleaved like B
-  int64_t ldgu;
+  int64_t ldgu;        // (SWIGLU_BWD reads the saved gate/up from gu and writes dgu to C)
   int grid_m, grid_n;
 };
 
@@ -292,6 +293,34 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
         }
       }
     }
+  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+    // acc is dact[row, col]; gate and up of act column col sit at interleaved
+    // columns (col / 32) * 64 + col % 32 and +32 of gu; dgu uses the same places.
+    uint16_t* dgu = static_cast<uint16_t*>(p.C);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lcol;
+        const int gcol = (col >> 5) * 64 + (col & 31);
+        const f32x16 t = acc[i][j];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
+          if (row < p.M && col < p.N) {
+            const int64_t o = static_cast<int64_t>(row) * p.ldgu + gcol;
+            const float g = bf16_to_f32(p.gu[o]);
+            const float u = bf16_to_f32(p.gu[o + 32]);
+            const float sg = 1.0f / (1.0f + __expf(-g));
+            const float da = t[r];
+            const float dsilu = sg * (1.0f + g * (1.0f - sg));
+            const int64_t od = static_cast<int64_t>(row) * p.ldc + gcol;
+            dgu[od] = f32_to_bf16(da * u * dsilu);
+            dgu[od + 32] = f32_to_bf16(da * g * sg);
+          }
+        }
+      }
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -414,6 +443,33 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
   p.gu = static_cast<uint16_t*>(gu);
   p.ldgu = ldgu;
   return dispatch<true, true, EPI_SWIGLU, true>(p, static_cast<hipStream_t>(stream));
+}
+
+int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t ldd,
+                       const void* Wd, int64_t ldw, const void* gu, int64_t ldgu, void* dgu,
+                       int64_t lddgu, void* stream) {
+  using namespace mr;
+  clear_error();
+  if (M <= 0 || N <= 0) return MR_OK;
+  if (!dd || !Wd || !gu || !dgu) return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: null operand");
+  if (M % 8 || N % 32 || K % BK || K == 0)
+    return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: M %% 8, N %% 32 and K %% %d must be 0", BK);
+  if (!ok16(dd, ldd) || !ok16(Wd, ldw))
+    return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: operands must be 16-byte aligned");
+  if (ldgu != lddgu) return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: gu and dgu must share a layout");
+  GemmParams p{};
+  p.M = static_cast<int>(M);
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.A = static_cast<const uint16_t*>(dd);
+  p.lda = ldd;
+  p.B = static_cast<const uint16_t*>(Wd);
+  p.ldb = ldw;
+  p.C = dgu;
+  p.ldc = lddgu;
+  p.gu = const_cast<uint16_t*>(static_cast<const uint16_t*>(gu));
+  p.ldgu = ldgu;
+  return dispatch<true, false, EPI_SWIGLU_BWD, true>(p, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -73,6 +73,13 @@ _SIGNATURES = {
     "mr_copy_bytes": (_I, [_P, _P, ctypes.c_size_t, _P]),
     "mr_gemm": (_I, [_I, _L, _L, _L, _P, _L, _P, _L, _P, _I, _L, _P, _P, _L, _P]),
     "mr_gemm_swiglu": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P]),
+    "mr_gemm_swiglu_bwd": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P]),
+    "mr_rmsnorm_fwd": (_I, [_P, _P, _L, _L, _F, _P, _P, _P]),
+    "mr_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _L, _L, _P, _P, _P]),
+    "mr_rope": (_I, [_P, _L, _L, _I, _I, _I, _P, _I, _P]),
+    "mr_attn_fwd": (_I, [_P, _L, _I, _I, _I, _I, _I, _F, _P, _L, _P, _P]),
+    "mr_attn_bwd": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P]),
+    "mr_cast_f32_bf16": (_I, [_P, _P, _L, _P]),
     "mr_fq_forward_mapped": (_I, [_P, _I, _P, _P, _P, _P, _L, _L, _I, _I, _I, _F, _P, _I, _L, _L,
                                   _L, _P]),
     "mr_fq_backward_signsgd_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F,
@@ -275,6 +282,58 @@ def gemm_swiglu(x, wgu, act, gu=None) -> None:
                               act.stride(0), _ptr(gu), gu.stride(0) if gu is not None else 0,
                               _stream(x))
     _check(rc, "mr_gemm_swiglu")
+
+
+def gemm_swiglu_bwd(dd, wd, gu, dgu) -> None:
+    """``mr_gemm_swiglu_bwd``: dgu from dact = dd Wd and the saved interleaved gate/up."""
+    M, K = dd.shape
+    N = wd.shape[1]
+    rc = lib().mr_gemm_swiglu_bwd(M, N, K, _ptr(dd), dd.stride(0), _ptr(wd), wd.stride(0), _ptr(gu),
+                                  gu.stride(0), _ptr(dgu), dgu.stride(0), _stream(dd))
+    _check(rc, "mr_gemm_swiglu_bwd")
+
+
+def rmsnorm_fwd(h, w, eps, y, rstd=None) -> None:
+    T, H = h.shape
+    rc = lib().mr_rmsnorm_fwd(_ptr(_f32(h, "h")), _ptr(_f32(w, "w")), T, H, eps, _ptr(y),
+                              _ptr(_f32(rstd, "rstd")), _stream(h))
+    _check(rc, "mr_rmsnorm_fwd")
+
+
+def rmsnorm_bwd(dy, h, w, rstd, dres, dh_bf16=None, dh_f32=None) -> None:
+    T, H = h.shape
+    rc = lib().mr_rmsnorm_bwd(_ptr(_f32(dy, "dy")), _ptr(_f32(h, "h")), _ptr(_f32(w, "w")),
+                              _ptr(_f32(rstd, "rstd")), _ptr(_f32(dres, "dres")), T, H, _ptr(dh_bf16),
+                              _ptr(_f32(dh_f32, "dh")), _stream(h))
+    _check(rc, "mr_rmsnorm_bwd")
+
+
+def rope(x, *, seq_len, n_heads, head_dim, cos_sin, backward=False) -> None:
+    T = x.shape[0]
+    rc = lib().mr_rope(_ptr(x), x.stride(0), T, seq_len, n_heads, head_dim, _ptr(_f32(cos_sin, "cos_sin")),
+                       int(backward), _stream(x))
+    _check(rc, "mr_rope")
+
+
+def attn_fwd(qkv, *, batch, seq_len, n_heads, n_kv_heads, head_dim, scale, out, lse) -> None:
+    rc = lib().mr_attn_fwd(_ptr(qkv), qkv.stride(0), batch, seq_len, n_heads, n_kv_heads, head_dim,
+                           scale, _ptr(out), out.stride(0), _ptr(_f32(lse, "lse")), _stream(qkv))
+    _check(rc, "mr_attn_fwd")
+
+
+def attn_bwd(qkv, out, dout, lse, dsum, *, batch, seq_len, n_heads, n_kv_heads, head_dim, scale,
+             dqkv) -> None:
+    if dout.stride(0) != out.stride(0) or dqkv.stride(0) != qkv.stride(0):
+        raise KernelError("attention backward: dout/out and dqkv/qkv must share layouts")
+    rc = lib().mr_attn_bwd(_ptr(qkv), qkv.stride(0), _ptr(out), _ptr(dout), out.stride(0),
+                           _ptr(_f32(lse, "lse")), _ptr(_f32(dsum, "dsum")), batch, seq_len, n_heads,
+                           n_kv_heads, head_dim, scale, _ptr(dqkv), _stream(qkv))
+    _check(rc, "mr_attn_bwd")
+
+
+def cast_bf16(x, y) -> None:
+    rc = lib().mr_cast_f32_bf16(_ptr(_f32(x, "x")), _ptr(y), x.numel(), _stream(x))
+    _check(rc, "mr_cast_f32_bf16")
 
 
 def fq_forward_mapped(weight, v, alpha, beta, *, bits, group_size, mode, eps, wq_out, row_block,

@@ -1,0 +1,281 @@
+"""GPU parity of the decoder-block kernels: attention, RMSNorm, RoPE, SwiGLU backward.
+
+Every reference is float64 on the CPU over the same bf16/fp32 inputs; the
+tolerances are error bounds built from the reference quantities: bf16
+rounding is 2^-8 relative, fp32 accumulation is at most K 2^-23 of the sum of
+magnitudes. Gradients are checked against float64 autograd.
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+import torch
+
+from mround_amd import kernels as K
+from tests.helpers import dev
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0**-8  # bf16 unit roundoff
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ------------------------------------------------------------------ attention --
+
+def attention_ref(qkv, B, S, Hq, Hkv, D, scale, dout=None):
+    """float64 causal GQA attention over packed [B*S, ld] rows; returns the
+    output, the natural log-sum-exp, and (with dout) the gradient of the packed rows."""
+    width = (Hq + 2 * Hkv) * D
+    x = qkv[:, :width].double().clone().requires_grad_(dout is not None)
+    t = x.reshape(B, S, Hq + 2 * Hkv, D)
+    q = t[:, :, :Hq].permute(0, 2, 1, 3)
+    k = t[:, :, Hq:Hq + Hkv].permute(0, 2, 1, 3).repeat_interleave(Hq // Hkv, 1)
+    v = t[:, :, Hq + Hkv:].permute(0, 2, 1, 3).repeat_interleave(Hq // Hkv, 1)
+    s = (q @ k.transpose(-1, -2)) * scale
+    causal = torch.ones(S, S, dtype=torch.bool).tril()
+    s = s.masked_fill(~causal, float("-inf"))
+    lse = torch.logsumexp(s, -1)
+    p = torch.exp(s - lse[..., None])
+    o = p @ v  # [B, Hq, S, D]
+    out = o.permute(0, 2, 1, 3).reshape(B * S, Hq * D)
+    res = {"out": out.detach(), "lse": lse.detach(), "p": p.detach(), "q": q.detach(),
+           "k": k.detach(), "v": v.detach()}
+    if dout is not None:
+        (out * dout.double()).sum().backward()
+        res["dqkv"] = x.grad
+    return res
+
+
+ATTN_CASES = [
+    # B, S, Hq, Hkv, D, magnitude
+    (1, 128, 2, 1, 64, 1.0),
+    (2, 256, 4, 2, 128, 1.0),
+    (1, 384, 4, 4, 64, 1.0),
+    (1, 256, 8, 1, 128, 1.0),
+    (1, 512, 2, 2, 128, 3.0),
+    (2, 128, 14, 2, 64, 2.0),
+]
+
+
+def _attn_inputs(B, S, Hq, Hkv, D, mag, seed, pad):
+    width = (Hq + 2 * Hkv) * D
+    ld = width + pad
+    qkv = torch.full((B * S, ld), 7.0).to(torch.bfloat16)
+    qkv[:, :width] = (torch.randn(B * S, width, generator=_gen(seed)) * mag).to(torch.bfloat16)
+    return qkv, ld
+
+
+@pytest.mark.parametrize("case", ATTN_CASES)
+def test_attention_forward(case):
+    B, S, Hq, Hkv, D, mag = case
+    print("case attn fwd", case, flush=True, file=sys.stderr)
+    qkv, _ = _attn_inputs(B, S, Hq, Hkv, D, mag, seed=21, pad=64)
+    scale = 1.0 / math.sqrt(D)
+    ref = attention_ref(qkv, B, S, Hq, Hkv, D, scale)
+    ldo = Hq * D + 8
+    out = torch.full((B * S, ldo), 5.0, dtype=torch.bfloat16, device=dev())
+    lse = torch.empty(B, Hq, S, device=dev())
+    K.attn_fwd(qkv.to(dev()), batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv, head_dim=D,
+               scale=scale, out=out, lse=lse)
+    got = out.double().cpu()
+    assert torch.all(got[:, Hq * D:] == 5.0), "padding columns were written"
+    o_ref = ref["out"]
+    # P rounded to bf16 before P V, then one rounding of the output
+    pv = (ref["p"] @ ref["v"].abs()).permute(0, 2, 1, 3).reshape(B * S, Hq * D)
+    tol = 1.5 * U * pv + U * o_ref.abs() + 1e-6
+    err = (got[:, :Hq * D] - o_ref).abs()
+    print("  out max err/tol", float((err / tol).max()), file=sys.stderr)
+    assert torch.all(err <= tol)
+    assert torch.allclose(lse.double().cpu(), ref["lse"], rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("case", ATTN_CASES)
+def test_attention_backward(case):
+    B, S, Hq, Hkv, D, mag = case
+    print("case attn bwd", case, flush=True, file=sys.stderr)
+    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, mag, seed=22, pad=32)
+    width = (Hq + 2 * Hkv) * D
+    scale = 1.0 / math.sqrt(D)
+    dout = torch.randn(B * S, Hq * D, generator=_gen(23)).to(torch.bfloat16)
+    ref = attention_ref(qkv, B, S, Hq, Hkv, D, scale, dout=dout)
+
+    q_d = qkv.to(dev())
+    out = torch.empty(B * S, Hq * D, dtype=torch.bfloat16, device=dev())
+    lse = torch.empty(B, Hq, S, device=dev())
+    K.attn_fwd(q_d, batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv, head_dim=D, scale=scale,
+               out=out, lse=lse)
+    dsum = torch.empty(B, Hq, S, device=dev())
+    dqkv = torch.full((B * S, ld), 3.0, dtype=torch.bfloat16, device=dev())
+    K.attn_bwd(q_d, out, dout.to(dev()), lse, dsum, batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv,
+               head_dim=D, scale=scale, dqkv=dqkv)
+    got = dqkv.double().cpu()
+    assert torch.all(got[:, width:] == 3.0), "padding columns were written"
+    got = got[:, :width].reshape(B, S, Hq + 2 * Hkv, D)
+    want = ref["dqkv"].reshape(B, S, Hq + 2 * Hkv, D)
+
+    # error bounds from the reference quantities
+    p, q, k, v = ref["p"], ref["q"], ref["k"], ref["v"]
+    do = dout.double().reshape(B, S, Hq, D).permute(0, 2, 1, 3)
+    o = ref["out"].reshape(B, S, Hq, D).permute(0, 2, 1, 3)
+    dp = do @ v.transpose(-1, -2)
+    ds = p * (dp - (do * o).sum(-1, keepdim=True))
+    tol_o = 1.5 * U * (p @ v.abs()) + U * o.abs() + 1e-6  # the kernel's own output
+    e_d = (do.abs() * tol_o).sum(-1, keepdim=True)
+    e_ds = p * (e_d + 1e-6 * (do.abs() @ v.abs().transpose(-1, -2))) + 2 * U * ds.abs()
+    G = Hq // Hkv
+
+    def per_kv(x):  # sum the query heads of each group: [B, Hq, S, D] -> [B, Hkv, S, D]
+        return x.reshape(B, Hkv, G, S, D).sum(2)
+
+    tol_dq = scale * (e_ds @ k.abs()) * 1.5
+    tol_dk = per_kv(scale * (e_ds.transpose(-1, -2) @ q.abs())) * 1.5
+    tol_dv = per_kv(1.5 * U * (p.transpose(-1, -2) @ do.abs())) * 1.5
+    for name, sl, tol in (("dq", slice(0, Hq), tol_dq), ("dk", slice(Hq, Hq + Hkv), tol_dk),
+                          ("dv", slice(Hq + Hkv, Hq + 2 * Hkv), tol_dv)):
+        w = want[:, :, sl].permute(0, 2, 1, 3)
+        g = got[:, :, sl].permute(0, 2, 1, 3)
+        t = tol + U * w.abs() + 1e-6
+        err = (g - w).abs()
+        print(f"  {name} max err/tol", float((err / t).max()), file=sys.stderr)
+        assert torch.all(err <= t), name
+
+
+def test_attention_rejects_bad_shapes():
+    qkv = torch.zeros(200, 4 * 64, dtype=torch.bfloat16, device=dev())
+    out = torch.zeros(200, 2 * 64, dtype=torch.bfloat16, device=dev())
+    lse = torch.zeros(200 * 2, device=dev())
+    with pytest.raises(Exception, match="multiple of 128"):
+        K.attn_fwd(qkv, batch=1, seq_len=200, n_heads=2, n_kv_heads=1, head_dim=64, scale=0.125,
+                   out=out, lse=lse)
+    with pytest.raises(Exception, match="head_dim"):
+        K.attn_fwd(qkv[:128], batch=1, seq_len=128, n_heads=1, n_kv_heads=1, head_dim=96,
+                   scale=0.125, out=out[:128], lse=lse)
+
+
+# ------------------------------------------------------------------- RMSNorm --
+
+def rmsnorm_ref(h, w, eps):
+    h64 = h.double()
+    r = 1.0 / torch.sqrt((h64 * h64).mean(-1, keepdim=True) + eps)
+    return h64 * r * w.double(), r
+
+
+@pytest.mark.parametrize("shape", [(300, 896), (64, 3584), (8, 128), (17, 4096)])
+def test_rmsnorm_forward(shape):
+    T, H = shape
+    h = torch.randn(T, H, generator=_gen(31)) * 3
+    w = 1 + 0.1 * torch.randn(H, generator=_gen(32))
+    y_ref, r_ref = rmsnorm_ref(h, w, 1e-6)
+    y = torch.empty(T, H, dtype=torch.bfloat16, device=dev())
+    rstd = torch.empty(T, device=dev())
+    K.rmsnorm_fwd(h.to(dev()), w.to(dev()), 1e-6, y, rstd)
+    tol = U * y_ref.abs() * (1 + 1e-5) + 1e-5 * y_ref.abs() + 1e-30
+    assert torch.all((y.double().cpu() - y_ref).abs() <= tol)
+    assert torch.allclose(rstd.double().cpu(), r_ref[:, 0], rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("shape", [(300, 896), (64, 3584)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_rmsnorm_backward(shape, with_res):
+    T, H = shape
+    h = torch.randn(T, H, generator=_gen(33)) * 2
+    w = 1 + 0.1 * torch.randn(H, generator=_gen(34))
+    dy = torch.randn(T, H, generator=_gen(35))
+    dres = torch.randn(T, H, generator=_gen(36)) if with_res else None
+    h64 = h.double().requires_grad_(True)
+    y64, r64 = rmsnorm_ref(h64, w, 1e-6)
+    (y64 * dy.double()).sum().backward()
+    want = h64.grad + (dres.double() if with_res else 0)
+    r = r64.detach()
+    mags = (r * (w.double() * dy.double()).abs()
+            + r**3 * h.double().abs() / H * (dy.double() * w.double() * h.double()).abs().sum(-1, keepdim=True))
+    if with_res:
+        mags = mags + dres.double().abs()
+    hd, wd, dyd = h.to(dev()), w.to(dev()), dy.to(dev())
+    rstd = torch.empty(T, device=dev())
+    K.rmsnorm_fwd(hd, wd, 1e-6, torch.empty(T, H, dtype=torch.bfloat16, device=dev()), rstd)
+    dh32 = torch.empty(T, H, device=dev())
+    dh16 = torch.empty(T, H, dtype=torch.bfloat16, device=dev())
+    K.rmsnorm_bwd(dyd, hd, wd, rstd, dres.to(dev()) if with_res else None, dh_bf16=dh16, dh_f32=dh32)
+    tol = 2e-5 * mags + 1e-30
+    assert torch.all((dh32.double().cpu() - want).abs() <= tol)
+    assert torch.all((dh16.double().cpu() - want).abs() <= tol + U * want.abs())
+
+
+# ---------------------------------------------------------------------- RoPE --
+
+def rope_table(S, d, base=10000.0):
+    inv = 1.0 / (base ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+    ang = torch.arange(S, dtype=torch.float64)[:, None] * inv[None, :]
+    return torch.stack([torch.cos(ang), torch.sin(ang)], -1).float()  # [S, d/2, 2]
+
+
+def rope_ref(x, S, n_heads, d, cs, backward):
+    """float64 rotation of the first n_heads heads of each row (halves layout)."""
+    T = x.shape[0]
+    y = x.double().clone()
+    pos = torch.arange(T) % S
+    c = cs[pos, :, 0].double()[:, None, :]
+    s = cs[pos, :, 1].double()[:, None, :]
+    if backward:
+        s = -s
+    h = y[:, :n_heads * d].reshape(T, n_heads, d)
+    a, b = h[..., :d // 2].clone(), h[..., d // 2:].clone()
+    h[..., :d // 2] = a * c - b * s
+    h[..., d // 2:] = b * c + a * s
+    y[:, :n_heads * d] = h.reshape(T, n_heads * d)
+    mag = torch.zeros_like(y)
+    m = (a.abs() * c.abs() + b.abs() * s.abs())
+    mag[:, :n_heads * d] = torch.cat([m, m], -1).reshape(T, n_heads * d)
+    return y, mag
+
+
+@pytest.mark.parametrize("cfg", [(2, 128, 6, 2, 64), (1, 256, 16, 4, 128), (3, 40, 2, 1, 128)])
+@pytest.mark.parametrize("backward", [False, True])
+def test_rope(cfg, backward):
+    B, S, Hq, Hkv, d = cfg
+    T = B * S
+    width = (Hq + 2 * Hkv) * d
+    x = torch.randn(T, width + 16, generator=_gen(41)).to(torch.bfloat16)
+    cs = rope_table(S, d, base=1e6)
+    y_ref, mag = rope_ref(x, S, Hq + Hkv, d, cs, backward)
+    xd = x.to(dev())
+    K.rope(xd, seq_len=S, n_heads=Hq + Hkv, head_dim=d, cos_sin=cs.to(dev()), backward=backward)
+    got = xd.double().cpu()
+    tol = U * y_ref.abs() + 4 * 2.0**-24 * mag
+    assert torch.all((got - y_ref).abs() <= tol)
+    # v heads and padding untouched
+    assert torch.equal(got[:, (Hq + Hkv) * d:], x.double()[:, (Hq + Hkv) * d:])
+
+
+# -------------------------------------------------------------- SwiGLU bwd --
+
+@pytest.mark.parametrize("mnk", [(256, 192, 128), (200, 96, 64), (1024, 4864, 896)])
+def test_swiglu_backward(mnk):
+    M, N, Kd = mnk  # rows, intermediate, hidden
+    dd = torch.randn(M, Kd, generator=_gen(51)).to(torch.bfloat16)
+    wd = torch.randn(Kd, N, generator=_gen(52)).to(torch.bfloat16)
+    g = (torch.randn(M, N, generator=_gen(53)) * 3).to(torch.bfloat16)
+    u = torch.randn(M, N, generator=_gen(54)).to(torch.bfloat16)
+    gu = torch.stack([g.reshape(M, N // 32, 32), u.reshape(M, N // 32, 32)], 2).reshape(M, 2 * N)
+    dact = dd.double() @ wd.double()
+    g64, u64 = g.double(), u.double()
+    sg = torch.sigmoid(g64)
+    dg_ref = dact * u64 * sg * (1 + g64 * (1 - sg))
+    du_ref = dact * g64 * sg
+    dgu = torch.full((M, 2 * N), 9.0, dtype=torch.bfloat16, device=dev())
+    K.gemm_swiglu_bwd(dd.to(dev()), wd.to(dev()), gu.to(dev()), dgu)
+    out = dgu.double().cpu().reshape(M, N // 32, 2, 32)
+    got_g = out[:, :, 0, :].reshape(M, N)
+    got_u = out[:, :, 1, :].reshape(M, N)
+    e_act = (dd.double().abs() @ wd.double().abs()) * Kd * 2.0**-23
+    tol_g = 1.1 * e_act * u64.abs() + 1e-5 * (dact * u64).abs() + U * dg_ref.abs() + 1e-30
+    tol_u = e_act * (g64 * sg).abs() + 1e-5 * du_ref.abs() + U * du_ref.abs() + 1e-30
+    assert torch.all((got_g - dg_ref).abs() <= tol_g)
+    assert torch.all((got_u - du_ref).abs() <= tol_u)

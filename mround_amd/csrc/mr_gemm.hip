@@ -148,7 +148,23 @@ struct MNMajorLoader {
   }
 };
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// Logistic function with the hardware reciprocal (1 ulp); the epilogues are
+// tolerance-checked, not bit-exact, and an IEEE division per element keeps the
+// unrolled epilogue from fitting in registers.
+__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
+
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled by the front end.
+template <int B, int E>
+struct StaticFor {
+  template <typename F>
+  __device__ __forceinline__ static void run(F& f) {
+    if constexpr (B < E) {
+      f(std::integral_constant<int, B>{});
+      StaticFor<B + 1, E>::run(f);
+    }
+  }
+};
 
 template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
@@ -296,52 +312,49 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
     // acc is dact[row, col]; gate and up of act column col sit at interleaved
     // columns (col / 32) * 64 + col % 32 and +32 of gu; dgu uses the same places.
+    // Tiles are visited with compile-time indices: the unrolled body is too
+    // large for the loop unroller, and a runtime tile index would move acc to
+    // scratch memory.
     uint16_t* dgu = static_cast<uint16_t*>(p.C);
+    auto tile = [&](auto ij) {
+      constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
+      const int col = n0 + wn * WN + j * 32 + lcol;
+      const int gcol = (col >> 5) * 64 + (col & 31);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * WN + j * 32 + lcol;
-        const int gcol = (col >> 5) * 64 + (col & 31);
-        const f32x16 t = acc[i][j];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
-          if (row < p.M && col < p.N) {
-            const int64_t o = static_cast<int64_t>(row) * p.ldgu + gcol;
-            const float g = bf16_to_f32(p.gu[o]);
-            const float u = bf16_to_f32(p.gu[o + 32]);
-            const float sg = 1.0f / (1.0f + __expf(-g));
-            const float da = t[r];
-            const float dsilu = sg * (1.0f + g * (1.0f - sg));
-            const int64_t od = static_cast<int64_t>(row) * p.ldc + gcol;
-            dgu[od] = f32_to_bf16(da * u * dsilu);
-            dgu[od + 32] = f32_to_bf16(da * g * sg);
-          }
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
+        if (row < p.M && col < p.N) {
+          const int64_t o = static_cast<int64_t>(row) * p.ldgu + gcol;
+          const float g = bf16_to_f32(p.gu[o]);
+          const float u = bf16_to_f32(p.gu[o + 32]);
+          const float sg = sigmoid(g);
+          const float da = acc[i][j][r];
+          const float dsilu = sg * (1.0f + g * (1.0f - sg));
+          const int64_t od = static_cast<int64_t>(row) * p.ldc + gcol;
+          dgu[od] = f32_to_bf16(da * u * dsilu);
+          dgu[od + 32] = f32_to_bf16(da * g * sg);
         }
       }
-    }
+    };
+    StaticFor<0, TM * TN>::run(tile);
   } else {
+    auto tile = [&](auto ij) {
+      constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
+      const int col = n0 + wn * WN + j * 32 + lcol;
+      const float bias = (p.bias && col < p.N) ? p.bias[col] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * WN + j * 32 + lcol;
-        const float bias = (p.bias && col < p.N) ? p.bias[col] : 0.0f;
-        const f32x16 t = acc[i][j];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
-          if (row < p.M && col < p.N) {
-            float x = t[r] + bias;
-            if constexpr (EPI == EPI_RESID) x = p.resid[static_cast<int64_t>(row) * p.ldr + col] + x;
-            const int64_t o = static_cast<int64_t>(row) * p.ldc + col;
-            if constexpr (OUT_BF16) static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(x);
-            else static_cast<float*>(p.C)[o] = x;
-          }
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
+        if (row < p.M && col < p.N) {
+          float x = acc[i][j][r] + bias;
+          if constexpr (EPI == EPI_RESID) x = p.resid[static_cast<int64_t>(row) * p.ldr + col] + x;
+          const int64_t o = static_cast<int64_t>(row) * p.ldc + col;
+          if constexpr (OUT_BF16) static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(x);
+          else static_cast<float*>(p.C)[o] = x;
         }
       }
-    }
+    };
+    StaticFor<0, TM * TN>::run(tile);
   }
 }
 

@@ -1,0 +1,283 @@
+"""One decoder block on the GPU: forward, loss, backward and the fused
+per-layer sign-SGD step of the tuning loop.
+
+The block is the mlx-lm Qwen2 / Llama decoder layer the reference runs via
+``block_output`` (mround/pipeline/blocks.py:578-606):
+
+    x1 = rmsnorm(x) w_in;  qkv = x1 [Wq; Wk; Wv]^T (+ b);  rope(q, k)
+    o = causal GQA attention;  h = x + o Wo^T
+    x2 = rmsnorm(h) w_post;  act = silu(x2 Wg^T) * (x2 Wu^T);  out = h + act Wd^T
+
+and its backward is the autodiff the reference takes through it
+(mround/pipeline/runner.py:920) down to each layer's dL/dW'.
+
+Layout in HBM, all row-major and allocated once per (batch, seq_len):
+
+* The fake-quantized weights W' are bf16, written by the fake-quant kernel
+  straight into fused operands: q, k and v rows stacked into one
+  ``[(Hq + 2 Hkv) d, h]`` matrix, and gate/up rows interleaved in blocks of 32
+  (rows 64b..64b+31 = gate rows 32b.., rows 64b+32.. = up rows 32b..) so one
+  GEMM yields both and its epilogue applies SwiGLU.
+* dL/dW' comes out of the weight-gradient GEMMs in the same fused layouts,
+  float32, and the fused backward + update kernel reads each layer's rows
+  from there.
+* Activations: the residual stream and the block output are float32
+  ``[T, h]``; GEMM operands (normalized inputs, qkv, attention output,
+  SwiGLU output) are bf16.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from mround_amd import kernels as K
+from mround_amd.exceptions import ArchitectureError
+
+# The block's linears, in the order the reference walks them
+# (sorted(named_modules()), mround/pipeline/blocks.py:654-678).
+LAYERS = ("mlp.down_proj", "mlp.gate_proj", "mlp.up_proj", "self_attn.k_proj",
+          "self_attn.o_proj", "self_attn.q_proj", "self_attn.v_proj")
+QKV = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")
+SWIGLU_ROWS = 32  # gate/up interleave period in the fused operand
+
+
+@dataclass(frozen=True)
+class BlockShape:
+    """Geometry of a Qwen2 / Llama decoder block."""
+
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    intermediate: int
+    norm_eps: float = 1e-6
+    rope_theta: float = 10000.0
+    attn_bias: bool = False
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+    def linear_shape(self, name: str) -> tuple[int, int]:
+        h, d = self.hidden, self.head_dim
+        shapes = {
+            "self_attn.q_proj": (self.n_heads * d, h),
+            "self_attn.k_proj": (self.n_kv_heads * d, h),
+            "self_attn.v_proj": (self.n_kv_heads * d, h),
+            "self_attn.o_proj": (h, self.n_heads * d),
+            "mlp.gate_proj": (self.intermediate, h),
+            "mlp.up_proj": (self.intermediate, h),
+            "mlp.down_proj": (h, self.intermediate),
+        }
+        return shapes[name]
+
+    def validate(self, seq_len: int | None = None) -> None:
+        """Raise ``ArchitectureError`` for a geometry the block kernels cannot run."""
+        problems = []
+        if self.head_dim not in (64, 128):
+            problems.append(f"head_dim {self.head_dim} is not 64 or 128")
+        if self.n_heads % self.n_kv_heads:
+            problems.append(f"{self.n_heads} query heads do not group over {self.n_kv_heads} kv heads")
+        if self.hidden % 64 or (self.n_heads * self.head_dim) % 64:
+            problems.append("hidden and n_heads * head_dim must be multiples of 64")
+        if self.intermediate % 64:
+            problems.append(f"intermediate size {self.intermediate} is not a multiple of 64")
+        if seq_len is not None and seq_len % 128:
+            problems.append(f"sequence length {seq_len} is not a multiple of 128")
+        if problems:
+            raise ArchitectureError("unsupported block geometry: " + "; ".join(problems))
+
+
+@dataclass(frozen=True)
+class Placement:
+    """Where a layer's rows sit in its fused operand: layer row r lands on
+    ``(r // row_block) * row_stride + row_offset + r % row_block``."""
+
+    operand: str
+    row_block: int
+    row_stride: int
+    row_offset: int
+
+
+def placements(shape: BlockShape) -> dict[str, Placement]:
+    d = shape.head_dim
+    q_rows, kv_rows = shape.n_heads * d, shape.n_kv_heads * d
+    return {
+        "self_attn.q_proj": Placement("qkv", q_rows, q_rows, 0),
+        "self_attn.k_proj": Placement("qkv", kv_rows, kv_rows, q_rows),
+        "self_attn.v_proj": Placement("qkv", kv_rows, kv_rows, q_rows + kv_rows),
+        "self_attn.o_proj": Placement("o", shape.hidden, shape.hidden, 0),
+        "mlp.gate_proj": Placement("gu", SWIGLU_ROWS, 2 * SWIGLU_ROWS, 0),
+        "mlp.up_proj": Placement("gu", SWIGLU_ROWS, 2 * SWIGLU_ROWS, SWIGLU_ROWS),
+        "mlp.down_proj": Placement("down", shape.hidden, shape.hidden, 0),
+    }
+
+
+def place(fused: torch.Tensor, rows: torch.Tensor, p: Placement) -> None:
+    """Copy a layer's rows into its fused operand (host-side layout helper)."""
+    n = rows.shape[0]
+    if p.row_block == p.row_stride:
+        fused[p.row_offset:p.row_offset + n].copy_(rows)
+        return
+    view = fused.view(-1, p.row_stride, fused.shape[1])[:, p.row_offset:p.row_offset + p.row_block]
+    view.copy_(rows.view(-1, p.row_block, rows.shape[1]))
+
+
+def unplace(fused: torch.Tensor, n: int, p: Placement) -> torch.Tensor:
+    """A layer's rows out of its fused operand."""
+    if p.row_block == p.row_stride:
+        return fused[p.row_offset:p.row_offset + n]
+    view = fused.view(-1, p.row_stride, fused.shape[1])[:, p.row_offset:p.row_offset + p.row_block]
+    return view.reshape(n, fused.shape[1])
+
+
+@dataclass
+class BlockWeights:
+    """A block's parameters on the device: the seven linears ``[out, in]`` in
+    the model dtype, the q/k/v biases (float32, when the block has them) and
+    the two RMSNorm weights (float32)."""
+
+    linears: dict[str, torch.Tensor]
+    biases: dict[str, torch.Tensor] = field(default_factory=dict)
+    input_norm: torch.Tensor | None = None
+    post_norm: torch.Tensor | None = None
+
+    @classmethod
+    def random(cls, shape: BlockShape, *, dtype: torch.dtype, device, seed: int, std: float = 0.02):
+        """Random-init weights N(0, std) (norm weights 1, biases N(0, std))."""
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        lin = {n: (torch.randn(*shape.linear_shape(n), generator=g) * std).to(dtype).to(device)
+               for n in LAYERS}
+        biases = {}
+        if shape.attn_bias:
+            biases = {n: (torch.randn(shape.linear_shape(n)[0], generator=g) * std).to(device)
+                      for n in QKV}
+        ones = torch.ones(shape.hidden, device=device)
+        return cls(lin, biases, ones, ones.clone())
+
+
+def rope_table(seq_len: int, head_dim: int, theta: float, device) -> torch.Tensor:
+    """cos/sin of ``pos * theta^(-2i/d)``, float32 ``[S, d/2, 2]`` (computed in float64)."""
+    inv = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim)
+    ang = torch.arange(seq_len, dtype=torch.float64)[:, None] * inv[None, :]
+    return torch.stack([torch.cos(ang), torch.sin(ang)], -1).float().to(device)
+
+
+class BlockEngine:
+    """Forward, loss and backward of one block over ``batch`` sequences of
+    ``seq_len`` tokens, with every buffer allocated once."""
+
+    def __init__(self, shape: BlockShape, *, batch: int, seq_len: int, device) -> None:
+        shape.validate(seq_len)
+        self.shape, self.batch, self.seq_len = shape, batch, seq_len
+        self.device = torch.device(device)
+        T, h, mlp = batch * seq_len, shape.hidden, shape.intermediate
+        self.tokens = T
+        hq_d = shape.n_heads * shape.head_dim
+        bf, f32 = torch.bfloat16, torch.float32
+        e = lambda *s, dt=bf: torch.empty(*s, dtype=dt, device=self.device)
+        # fused W' operands and their gradients
+        self.wq = {"qkv": e(shape.qkv_rows, h), "o": e(h, hq_d), "gu": e(2 * mlp, h), "down": e(h, mlp)}
+        self.dw = {k: torch.empty(v.shape, dtype=f32, device=self.device) for k, v in self.wq.items()}
+        self.bias_qkv = None
+        self.norm_in = self.norm_post = None
+        # activations
+        self.x1, self.rstd1 = e(T, h), e(T, dt=f32)
+        self.qkv = e(T, shape.qkv_rows)
+        self.attn, self.lse = e(T, hq_d), e(batch, shape.n_heads, seq_len, dt=f32)
+        self.h2 = e(T, h, dt=f32)
+        self.x2, self.rstd2 = e(T, h), e(T, dt=f32)
+        self.act, self.gu = e(T, mlp), e(T, 2 * mlp)
+        # backward
+        self.grad_out, self.grad_out16 = e(T, h, dt=f32), e(T, h)
+        self.dgu = e(T, 2 * mlp)
+        self.dx2 = e(T, h, dt=f32)
+        self.dh2 = e(T, h)
+        self.dattn, self.dsum = e(T, hq_d), e(batch, shape.n_heads, seq_len, dt=f32)
+        self.dqkv = e(T, shape.qkv_rows)
+        self.loss_val = e(1, dt=f32)
+        self.threshold = e(1, dt=f32)
+        self.cos_sin = rope_table(seq_len, shape.head_dim, shape.rope_theta, self.device)
+        self.scale = 1.0 / math.sqrt(shape.head_dim)
+        self.place = placements(shape)
+        self.loss_ws = K.loss_workspace(self.device, T * h)
+
+    # ---------------------------------------------------------------- weights --
+    def set_block(self, weights: BlockWeights) -> None:
+        """Biases and norm weights of the block (kept fp32)."""
+        s = self.shape
+        if s.attn_bias:
+            if set(weights.biases) != set(QKV):
+                raise ArchitectureError("the block geometry has q/k/v biases but the weights do not")
+            self.bias_qkv = torch.cat([weights.biases[n].float() for n in QKV]).contiguous()
+        else:
+            self.bias_qkv = None
+        self.norm_in = weights.input_norm.float().contiguous()
+        self.norm_post = weights.post_norm.float().contiguous()
+
+    def load_dense(self, linears: dict[str, torch.Tensor]) -> None:
+        """W' = the given weights rounded to bf16 (the targets pass, and the
+        advance pass over committed reconstructions)."""
+        for name, p in self.place.items():
+            place(self.wq[p.operand], linears[name].to(torch.bfloat16), p)
+
+    # ---------------------------------------------------------------- forward --
+    def forward(self, x: torch.Tensor, out: torch.Tensor, *, save: bool) -> None:
+        """``out = block(x)``; ``x``/``out`` float32 ``[T, h]`` (``out`` may be ``x``).
+        ``save`` keeps what the backward reads."""
+        s, T = self.shape, self.tokens
+        if x.shape != (T, s.hidden) or out.shape != (T, s.hidden):
+            raise ArchitectureError(f"block input must be [{T}, {s.hidden}]")
+        h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
+        K.rmsnorm_fwd(x, self.norm_in, s.norm_eps, self.x1, self.rstd1)
+        K.gemm("nt", self.x1, self.wq["qkv"], self.qkv, M=T, N=s.qkv_rows, K=h, bias=self.bias_qkv)
+        K.rope(self.qkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads, head_dim=s.head_dim,
+               cos_sin=self.cos_sin)
+        K.attn_fwd(self.qkv, batch=self.batch, seq_len=self.seq_len, n_heads=s.n_heads,
+                   n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, scale=self.scale, out=self.attn,
+                   lse=self.lse)
+        K.gemm("nt", self.attn, self.wq["o"], self.h2, M=T, N=h, K=hq_d, resid=x)
+        K.rmsnorm_fwd(self.h2, self.norm_post, s.norm_eps, self.x2, self.rstd2)
+        K.gemm_swiglu(self.x2, self.wq["gu"], self.act, self.gu if save else None)
+        K.gemm("nt", self.act, self.wq["down"], out, M=T, N=h, K=mlp, resid=self.h2)
+
+    def loss(self, out: torch.Tensor, target: torch.Tensor, *, suppress: bool, with_grad: bool) -> torch.Tensor:
+        """Reconstruction loss of one batch (device scalar), and dL/dout when asked:
+        mean squared error, or with the top 0.1 % of |residuals| excluded
+        (mround/core/losses.py:42-107)."""
+        n = out.numel()
+        grad = self.grad_out if with_grad else None
+        if suppress:
+            K.loss_outlier(out, target, k=max(1, int(n * 0.001)), denom=n, loss_out=self.loss_val,
+                           threshold_out=self.threshold, grad_out=grad, workspace=self.loss_ws)
+        else:
+            K.loss_mse(out, target, denom=n, loss_out=self.loss_val, grad_out=grad,
+                       workspace=self.loss_ws)
+        return self.loss_val
+
+    # --------------------------------------------------------------- backward --
+    def backward(self) -> None:
+        """dL/dW' of all seven layers into ``self.dw`` from ``self.grad_out``
+        (after ``forward(save=True)`` and ``loss(with_grad=True)``)."""
+        s, T = self.shape, self.tokens
+        h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
+        K.cast_bf16(self.grad_out, self.grad_out16)
+        # MLP: dgu from dact = dout Wd'; dWd' = dout^T act; dx2 = dgu Wgu'; dWgu' = dgu^T x2
+        K.gemm_swiglu_bwd(self.grad_out16, self.wq["down"], self.gu, self.dgu)
+        K.gemm("tn", self.grad_out16, self.act, self.dw["down"], M=h, N=mlp, K=T)
+        K.gemm("nn", self.dgu, self.wq["gu"], self.dx2, M=T, N=h, K=2 * mlp)
+        K.gemm("tn", self.dgu, self.x2, self.dw["gu"], M=2 * mlp, N=h, K=T)
+        # dh = dout + rmsnorm'(dx2)
+        K.rmsnorm_bwd(self.dx2, self.h2, self.norm_post, self.rstd2, self.grad_out, dh_bf16=self.dh2)
+        # attention output projection
+        K.gemm("nn", self.dh2, self.wq["o"], self.dattn, M=T, N=hq_d, K=h)
+        K.gemm("tn", self.dh2, self.attn, self.dw["o"], M=h, N=hq_d, K=T)
+        K.attn_bwd(self.qkv, self.attn, self.dattn, self.lse, self.dsum, batch=self.batch,
+                   seq_len=self.seq_len, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads,
+                   head_dim=s.head_dim, scale=self.scale, dqkv=self.dqkv)
+        K.rope(self.dqkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads,
+               head_dim=s.head_dim, cos_sin=self.cos_sin, backward=True)
+        K.gemm("tn", self.dqkv, self.x1, self.dw["qkv"], M=s.qkv_rows, N=h, K=T)

@@ -1,0 +1,359 @@
+"""Block-by-block SignRound tuning on one GPU.
+
+The host side of ``QuantizationRunner`` (mround/pipeline/runner.py:427-953):
+the targets pass over the original weights, the tuning loop (score every
+batch, ``iters`` sign-SGD steps on cycled batches, score again, revert to
+round to nearest when the score did not improve), the commit of codes and
+reconstructions, and the advance of the quantized stream. Every array lives
+on the device; the loop issues kernels on the current stream and reads back
+one scalar per scored batch set, none per step.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import time
+from collections.abc import Callable, Mapping, Sequence
+
+import torch
+
+from mround_amd import kernels as K
+from mround_amd.core.quantizer import fake_quantize, mode_of, quantize_codes
+from mround_amd.core.signsgd import LinearDecay
+from mround_amd.exceptions import ArchitectureError, CalibrationError, UnsupportedSchemeError
+from mround_amd.formats.mlx_export import QuantizedLayer
+from mround_amd.pipeline.block import LAYERS, BlockEngine, BlockShape, BlockWeights, placements, unplace
+from mround_amd.schemes import DEFAULT_EPS_FP32, QuantScheme, ScaleInit, TuningConfig
+
+V_BOUND = 0.5
+
+
+@dataclasses.dataclass
+class DecoderBlock:
+    """One block of a model: its position, dotted name, geometry and weights."""
+
+    index: int
+    name: str
+    shape: BlockShape
+    weights: BlockWeights
+
+
+@dataclasses.dataclass(frozen=True)
+class BlockResult:
+    """What tuning one block achieved (mround/pipeline/runner.py:188-260)."""
+
+    index: int
+    name: str
+    initial_loss: float
+    final_loss: float
+    iterations: int
+    seconds: float
+    tuned: tuple[str, ...]
+    skipped: tuple[tuple[str, str], ...] = ()
+    reverted: bool = False
+    generalization_gap: float | None = None
+    search_seconds: float = 0.0
+    stage_seconds: Mapping[str, float] = dataclasses.field(default_factory=dict)
+    step_losses: tuple[float, ...] = ()
+
+    @property
+    def improvement(self) -> float:
+        if self.initial_loss <= 0:
+            return 0.0
+        return 1.0 - self.final_loss / self.initial_loss
+
+
+@dataclasses.dataclass(frozen=True)
+class RunSummary:
+    blocks: list[BlockResult]
+    total_seconds: float
+    peak_memory_bytes: int
+    scheme_by_layer: Mapping[str, QuantScheme]
+
+    @property
+    def mean_improvement(self) -> float:
+        if not self.blocks:
+            return 0.0
+        return sum(b.improvement for b in self.blocks) / len(self.blocks)
+
+
+def block_recipe(tuning: TuningConfig, base_bits: int, widths: Mapping[str, int], *,
+                 per_layer: bool) -> tuple[bool, dict[str, float]]:
+    """Outlier rule and per-layer initial rate (mround/pipeline/runner.py:389-425)."""
+    if not per_layer:
+        rate = tuning.resolved_lr(base_bits)
+        return tuning.resolved_suppress_outliers(base_bits), dict.fromkeys(widths, rate)
+    narrowest = min(widths.values(), default=base_bits)
+    return tuning.resolved_suppress_outliers(narrowest), {
+        name: tuning.resolved_lr(bits) for name, bits in widths.items()
+    }
+
+
+class _Layer:
+    """A linear being tuned: the original weight (model dtype, never updated),
+    its scheme, its rows' place in the fused operand, and (v, alpha, beta)."""
+
+    def __init__(self, name: str, weight: torch.Tensor, scheme: QuantScheme, placement) -> None:
+        self.name = name
+        self.weight = weight.contiguous()
+        self.scheme = scheme
+        self.mode = mode_of(scheme)
+        self.placement = placement
+        rows, cols = weight.shape
+        ng = cols // scheme.group_size
+        dev = weight.device
+        self.v = torch.zeros(rows, cols, dtype=torch.float32, device=dev)
+        self.alpha = torch.ones(rows, ng, dtype=torch.float32, device=dev)
+        self.beta = torch.ones(rows, ng, dtype=torch.float32, device=dev)
+
+    def params(self) -> dict[str, torch.Tensor]:
+        rows, cols = self.weight.shape
+        gs = self.scheme.group_size
+        return {"v": self.v.view(rows, -1, gs), "alpha": self.alpha.unsqueeze(-1),
+                "beta": self.beta.unsqueeze(-1)}
+
+    def snapshot(self):
+        return self.v.clone(), self.alpha.clone(), self.beta.clone()
+
+    def restore(self, saved) -> None:
+        for dst, src in zip((self.v, self.alpha, self.beta), saved):
+            dst.copy_(src)
+
+
+class QuantizationRunner:
+    """Walks a model block by block, quantizing each in turn."""
+
+    def __init__(self, scheme: QuantScheme, tuning: TuningConfig, *,
+                 progress: Callable[[BlockResult], None] | None = None,
+                 eps: float = DEFAULT_EPS_FP32, quantized_inputs: bool = True,
+                 holdout_batches: int = 0, per_layer_recipe: bool = False) -> None:
+        if holdout_batches < 0:
+            msg = f"holdout_batches must be zero or more, got {holdout_batches}"
+            raise CalibrationError(msg)
+        self.scheme = scheme
+        self.tuning = tuning
+        self.progress = progress
+        self.eps = eps
+        self.quantized_inputs = quantized_inputs
+        self.holdout_batches = holdout_batches
+        self.per_layer_recipe = per_layer_recipe
+        self._engines: dict = {}
+
+    def _scheme_for(self, path: str, overrides: Mapping[str, QuantScheme] | None) -> QuantScheme:
+        if overrides is None:
+            return self.scheme
+        return overrides.get(path, self.scheme)
+
+    def engine(self, shape: BlockShape, tokens: int, device) -> BlockEngine:
+        """The block engine for this geometry, built once per run."""
+        seq = self.tuning.seq_len
+        if tokens % seq:
+            raise CalibrationError(f"a batch of {tokens} tokens is not whole sequences of {seq}")
+        key = (shape, tokens, str(device))
+        eng = self._engines.get(key)
+        if eng is None:
+            eng = BlockEngine(shape, batch=tokens // seq, seq_len=seq, device=device)
+            self._engines = {key: eng}
+        return eng
+
+    # ------------------------------------------------------------------ run --
+    def run(self, blocks: Sequence[DecoderBlock], entrance: Sequence[torch.Tensor], *,
+            scheme_by_layer: Mapping[str, QuantScheme] | None = None):
+        """Quantize every block in place (mround/pipeline/runner.py:493-625).
+
+        ``entrance`` holds the first block's input hidden states, one float32
+        ``[batch * seq_len, hidden]`` device tensor per calibration batch; the
+        list is consumed (its tensors are overwritten by the streams).
+        """
+        started = time.perf_counter()
+        if not entrance:
+            raise CalibrationError("no calibration batches")
+        reference_stream = [x.float().contiguous() for x in entrance]
+        quantized_stream = [x.clone() for x in reference_stream] if self.quantized_inputs else None
+        results, exported, schemes = [], {}, {}
+        for block in blocks:
+            t0 = time.perf_counter()
+            eng = self.engine(block.shape, reference_stream[0].shape[0], reference_stream[0].device)
+            eng.set_block(block.weights)
+            # Targets: the original block over the reference stream, written over
+            # it when the quantized stream carries the inputs (two streams resident).
+            eng.load_dense(block.weights.linears)
+            if quantized_stream is not None:
+                targets = reference_stream
+                for x in targets:
+                    eng.forward(x, x, save=False)
+            else:
+                targets = []
+                for x in reference_stream:
+                    out = torch.empty_like(x)
+                    eng.forward(x, out, save=False)
+                    targets.append(out)
+            torch.cuda.synchronize(eng.device)
+            targets_seconds = time.perf_counter() - t0
+            inputs = quantized_stream if quantized_stream is not None else reference_stream
+            result, layers = self.quantize_block(block, inputs, targets, scheme_by_layer=scheme_by_layer,
+                                                 path_prefix=block.name)
+            exported.update(layers)
+            for path in layers:
+                schemes[path] = self._scheme_for(path, scheme_by_layer)
+            t1 = time.perf_counter()
+            if quantized_stream is not None:
+                eng.load_dense(block.weights.linears)
+                for x in quantized_stream:
+                    eng.forward(x, x, save=False)
+            torch.cuda.synchronize(eng.device)
+            stages = dict(result.stage_seconds)
+            stages["targets"] = targets_seconds
+            stages["advance"] = time.perf_counter() - t1
+            result = dataclasses.replace(result, stage_seconds=stages)
+            reference_stream = targets
+            results.append(result)
+            if self.progress is not None:
+                self.progress(result)
+        peak = torch.cuda.max_memory_allocated() if torch.cuda.is_available() else 0
+        return RunSummary(results, time.perf_counter() - started, peak, schemes), exported
+
+    # -------------------------------------------------------- quantize_block --
+    def quantize_block(self, block: DecoderBlock, inputs: Sequence[torch.Tensor],
+                       targets: Sequence[torch.Tensor], *,
+                       scheme_by_layer: Mapping[str, QuantScheme] | None = None,
+                       path_prefix: str = ""):
+        """Tune and commit one block (mround/pipeline/runner.py:627-710). The
+        block's linears are replaced by their reconstructions in the model dtype."""
+        started = time.perf_counter()
+        place = placements(block.shape)
+        layers: dict[str, _Layer] = {}
+        skipped = []
+        for name in LAYERS:
+            path = f"{path_prefix}.{name}" if path_prefix else name
+            scheme = self._scheme_for(path, scheme_by_layer)
+            w = block.weights.linears[name]
+            if scheme.group_size == -1 or w.shape[-1] % scheme.group_size:
+                skipped.append((name, f"last dimension {w.shape[-1]} is not a multiple of "
+                                      f"{scheme.group_size}"))
+                continue
+            if scheme.scale_init is ScaleInit.SEARCHED:
+                raise UnsupportedSchemeError("searched scale initialisation is not available in the "
+                                             "block loop; use the observed range")
+            layers[name] = _Layer(name, w, scheme, place[name])
+        if skipped:
+            # The fused operands need every layer's W'; a partly quantized block
+            # would need a dense path per skipped layer.
+            reasons = "; ".join(f"{n}: {why}" for n, why in skipped)
+            raise ArchitectureError(f"block {block.name!r} cannot be tuned whole: {reasons}")
+
+        eng = self.engine(block.shape, inputs[0].shape[0], inputs[0].device)
+        eng.set_block(block.weights)
+        outcome = self._tune(eng, layers, inputs, targets)
+        t_commit = time.perf_counter()
+        exported = {}
+        for name, layer in layers.items():
+            path = f"{path_prefix}.{name}" if path_prefix else name
+            exported[path] = self._commit(block, layer)
+        torch.cuda.synchronize(eng.device)
+        stages = dict(outcome["stages"])
+        stages["commit"] = time.perf_counter() - t_commit
+        result = BlockResult(
+            index=block.index, name=block.name, initial_loss=outcome["initial"],
+            final_loss=outcome["final"], iterations=self.tuning.iters,
+            seconds=time.perf_counter() - started, tuned=tuple(sorted(layers)),
+            reverted=outcome["reverted"], generalization_gap=outcome["gap"], stage_seconds=stages,
+            step_losses=tuple(outcome["losses"]))
+        return result, exported
+
+    def _commit(self, block: DecoderBlock, layer: _Layer) -> QuantizedLayer:
+        """Codes (one byte each), scale and zero point for export, and the
+        layer's weight replaced by its reconstruction (mround/pipeline/runner.py:760-788)."""
+        params = layer.params()
+        codes, scale, zp = quantize_codes(layer.weight, params, layer.scheme, eps=self.eps, narrow=True)
+        recon = fake_quantize(layer.weight, params, layer.scheme, eps=self.eps,
+                              out_dtype=block.weights.linears[layer.name].dtype)
+        block.weights.linears[layer.name] = recon
+        return QuantizedLayer(codes, scale, zp, layer.scheme)
+
+    # ------------------------------------------------------------------ tune --
+    def _quantize_all(self, eng: BlockEngine, layers: Mapping[str, _Layer]) -> None:
+        for layer in layers.values():
+            p = layer.placement
+            K.fq_forward_mapped(layer.weight, layer.v, layer.alpha, layer.beta,
+                                bits=layer.scheme.bits, group_size=layer.scheme.group_size,
+                                mode=layer.mode, eps=self.eps, wq_out=eng.wq[p.operand],
+                                row_block=p.row_block, row_stride=p.row_stride,
+                                row_offset=p.row_offset)
+
+    def _step_all(self, eng: BlockEngine, layers: Mapping[str, _Layer], rates: Mapping[str, float],
+                  step: int) -> None:
+        iters = self.tuning.iters
+        for name, layer in layers.items():
+            p = layer.placement
+            lo, hi = layer.scheme.coefficient_bounds
+            lr = LinearDecay(rates[name], iters)(step)
+            K.fq_step_mapped(layer.weight, layer.v, layer.alpha, layer.beta, eng.dw[p.operand],
+                             bits=layer.scheme.bits, group_size=layer.scheme.group_size,
+                             mode=layer.mode, eps=self.eps, lr=lr, coef_lo=lo, coef_hi=hi,
+                             v_bound=V_BOUND, row_block=p.row_block, row_stride=p.row_stride,
+                             row_offset=p.row_offset)
+
+    def _scores(self, eng, layers, inputs, targets, over, suppress, scratch) -> float:
+        """Mean loss over batches ``over`` with the current parameters."""
+        self._quantize_all(eng, layers)
+        acc = torch.zeros(len(over), dtype=torch.float32, device=eng.device)
+        for i, b in enumerate(over):
+            eng.forward(inputs[b], scratch, save=False)
+            acc[i:i + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress, with_grad=False))
+        return float(acc.double().sum().item()) / len(over)
+
+    def _tune(self, eng: BlockEngine, layers: Mapping[str, _Layer], inputs, targets) -> dict:
+        """mround/pipeline/runner.py:790-953: the last parameters are kept unless
+        the score did not improve."""
+        suppress, rates = block_recipe(self.tuning, self.scheme.bits,
+                                       {n: l.scheme.bits for n, l in layers.items()},
+                                       per_layer=self.per_layer_recipe)
+        n_batches = len(inputs)
+        held = min(self.holdout_batches, n_batches - 1)
+        tuning_batches = list(range(n_batches - held))
+        scoring_batches = list(range(n_batches - held, n_batches)) if held else tuning_batches
+        scratch = torch.empty_like(inputs[0])
+        stages = {}
+        t0 = time.perf_counter()
+        initial = self._scores(eng, layers, inputs, targets, scoring_batches, suppress, scratch)
+        initial_tuning = (self._scores(eng, layers, inputs, targets, tuning_batches, suppress, scratch)
+                          if held else initial)
+        stages["score"] = time.perf_counter() - t0
+        start = {n: l.snapshot() for n, l in layers.items()}
+
+        t0 = time.perf_counter()
+        iters = self.tuning.iters
+        step_losses = torch.zeros(iters, dtype=torch.float32, device=eng.device)
+        for step in range(iters):
+            b = tuning_batches[step % len(tuning_batches)]
+            self._quantize_all(eng, layers)
+            eng.forward(inputs[b], scratch, save=True)
+            step_losses[step:step + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress,
+                                                      with_grad=True))
+            eng.backward()
+            self._step_all(eng, layers, rates, step)
+        torch.cuda.synchronize(eng.device)
+        stages["tune"] = time.perf_counter() - t0
+
+        t0 = time.perf_counter()
+        final = self._scores(eng, layers, inputs, targets, scoring_batches, suppress, scratch)
+        final_tuning = (self._scores(eng, layers, inputs, targets, tuning_batches, suppress, scratch)
+                        if held else final)
+        stages["score"] += time.perf_counter() - t0
+        gap = None
+        if held:
+            gap = (1.0 - final_tuning / initial_tuning) - (1.0 - final / initial)
+        losses = step_losses.double().cpu().tolist()
+        if final >= initial:
+            for n, l in layers.items():
+                l.restore(start[n])
+            return {"initial": initial, "final": initial, "gap": gap, "reverted": True,
+                    "losses": losses, "stages": stages}
+        return {"initial": initial, "final": final, "gap": gap, "reverted": False, "losses": losses,
+                "stages": stages}
+
+
+def reconstruction_of(eng: BlockEngine, name: str, rows: int) -> torch.Tensor:
+    """A layer's current W' (bf16) out of the engine's fused operand."""
+    return unplace(eng.wq[eng.place[name].operand], rows, eng.place[name])

@@ -1,0 +1,205 @@
+"""GPU block engine and tuning loop against the float64 block oracle.
+
+The GPU path rounds GEMM operands (normalized activations, W', attention
+probabilities, gradients) to bf16 and accumulates in fp32; the oracle is
+float64 throughout with fp32 fake quantization. The stated tolerance for
+per-step losses and reconstructions computed through bf16 is 1e-2 relative.
+Codes are bit-exact given identical v and scales.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from mround_amd.pipeline.block import LAYERS, BlockEngine, BlockShape, BlockWeights, placements, unplace
+from mround_amd.pipeline.runner import DecoderBlock, QuantizationRunner
+from mround_amd.schemes import QuantScheme, Symmetry, TuningConfig
+from oracle import block as OB
+from oracle import quantize as OQ
+from tests.helpers import dev
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = {
+    "tiny_qwen": (BlockShape(hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, intermediate=256,
+                             rope_theta=1e6, attn_bias=True), 2, 128),
+    "smollm": (BlockShape(hidden=576, n_heads=9, n_kv_heads=3, head_dim=64, intermediate=1536,
+                          norm_eps=1e-5), 2, 256),
+    "d128": (BlockShape(hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512,
+                        attn_bias=True), 1, 256),
+}
+
+
+def _oracle_shape(s: BlockShape) -> OB.Shape:
+    return OB.Shape(hidden=s.hidden, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim,
+                    intermediate=s.intermediate, norm_eps=s.norm_eps, rope_theta=s.rope_theta,
+                    attn_bias=s.attn_bias)
+
+
+def _problem(key, seed=0, std=0.05):
+    shape, B, S = SHAPES[key]
+    w = BlockWeights.random(shape, dtype=torch.bfloat16, device="cpu", seed=seed, std=std)
+    g = torch.Generator().manual_seed(seed + 100)
+    w.input_norm = 1 + 0.1 * torch.randn(shape.hidden, generator=g)
+    w.post_norm = 1 + 0.1 * torch.randn(shape.hidden, generator=g)
+    if shape.attn_bias:
+        w.biases = {n: torch.randn(shape.linear_shape(n)[0], generator=g) * 0.1 for n in w.biases}
+    x = torch.randn(B * S, shape.hidden, generator=g)
+    return shape, B, S, w, x
+
+
+def _oracle_forward(shape, B, S, w, x, linears=None):
+    lin = {n: (linears or w.linears)[n].double() for n in LAYERS}
+    biases = {n: b.double() for n, b in w.biases.items()}
+    norms = (w.input_norm.double(), w.post_norm.double())
+    return OB.block_forward(x.double().view(B, S, -1), lin, biases, norms, _oracle_shape(shape))
+
+
+def _to_dev(w: BlockWeights) -> BlockWeights:
+    return BlockWeights({n: t.to(dev()) for n, t in w.linears.items()},
+                        {n: t.to(dev()) for n, t in w.biases.items()},
+                        w.input_norm.to(dev()), w.post_norm.to(dev()))
+
+
+@pytest.mark.parametrize("key", list(SHAPES))
+def test_block_forward(key):
+    print("case block fwd", key, flush=True, file=sys.stderr)
+    shape, B, S, w, x = _problem(key)
+    ref = _oracle_forward(shape, B, S, w, x).reshape(B * S, -1)
+    eng = BlockEngine(shape, batch=B, seq_len=S, device=dev())
+    wd = _to_dev(w)
+    eng.set_block(wd)
+    eng.load_dense(wd.linears)
+    out = torch.empty(B * S, shape.hidden, device=dev())
+    eng.forward(x.to(dev()), out, save=False)
+    got = out.double().cpu()
+    delta_ref = ref - x.double()
+    err = (got - ref).norm() / delta_ref.norm()
+    print("  rel err of the block's update", float(err), file=sys.stderr)
+    assert err < 1e-2
+    # in place (out aliasing x) gives the same result
+    xd = x.to(dev())
+    eng.forward(xd, xd, save=False)
+    assert torch.equal(xd, out)
+
+
+def _rtn_bf16(w: torch.Tensor, bits: int = 2) -> torch.Tensor:
+    """Round-to-nearest W' (the first tuning step's weights), rounded to bf16."""
+    qdq, _, _, _ = OQ.fake_quantize(w.float().numpy(), None, None, None, bits=bits, group_size=64,
+                                   mode="asym")
+    return torch.from_numpy(np.ascontiguousarray(qdq)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("key", list(SHAPES))
+def test_block_backward(key):
+    """dL/dW' of every layer at the first tuning step: W' = 2-bit round to
+    nearest, target = the original block's output, L = mean squared error."""
+    print("case block bwd", key, flush=True, file=sys.stderr)
+    shape, B, S, w, x = _problem(key, seed=1)
+    target = _oracle_forward(shape, B, S, w, x).reshape(B * S, -1)
+    wq = {n: _rtn_bf16(w.linears[n]) for n in LAYERS}
+    lin = {n: wq[n].double().requires_grad_(True) for n in LAYERS}
+    pred = _oracle_forward(shape, B, S, w, x, linears=lin).reshape(B * S, -1)
+    loss = ((pred - target) ** 2).mean()
+    loss.backward()
+
+    eng = BlockEngine(shape, batch=B, seq_len=S, device=dev())
+    eng.set_block(_to_dev(w))
+    eng.load_dense({n: t.to(dev()) for n, t in wq.items()})
+    out = torch.empty(B * S, shape.hidden, device=dev())
+    eng.forward(x.to(dev()), out, save=True)
+    got_loss = eng.loss(out, target.float().to(dev()), suppress=False, with_grad=True)
+    eng.backward()
+    print(f"  loss gpu {float(got_loss):.6e} oracle {float(loss):.6e}", file=sys.stderr)
+    assert abs(float(got_loss) - float(loss)) <= 1e-2 * float(loss)
+    place = placements(shape)
+    for n in LAYERS:
+        ref = lin[n].grad
+        got = unplace(eng.dw[place[n].operand], ref.shape[0], place[n]).double().cpu()
+        rel = float((got - ref).norm() / ref.norm())
+        # the update takes signs: the gradient mass whose sign flips is what matters
+        flipped = float(ref.abs()[torch.sign(got) != torch.sign(ref)].sum() / ref.abs().sum())
+        print(f"  {n}: rel err {rel:.2e}, flipped mass {flipped:.2e}", file=sys.stderr)
+        assert rel < 5e-2, n
+        assert flipped < 1e-2, n
+
+
+def _tiny_tune(bits, iters):
+    shape, B, S, w, x = _problem("tiny_qwen", seed=3)
+    g = torch.Generator().manual_seed(5)
+    inputs = [x, torch.randn(B * S, shape.hidden, generator=g)]
+    targets = [_oracle_forward(shape, B, S, w, xi).reshape(B * S, -1).float() for xi in inputs]
+    return shape, B, S, w, inputs, targets
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_tuning_trajectory_matches_oracle(bits):
+    # The first steps of a 200-step schedule (rate 1/200): sign-SGD flips a
+    # parameter by the full rate wherever a gradient changes sign, so the
+    # comparison is meaningful at the real rate, not at 1/12.
+    iters, lr = 12, 0.005
+    print("case block tune", bits, flush=True, file=sys.stderr)
+    shape, B, S, w, inputs, targets = _tiny_tune(bits, iters)
+    scheme = QuantScheme(bits=bits, group_size=64, symmetry=Symmetry.ASYMMETRIC)
+    tuning = TuningConfig(iters=iters, batch_size=B, n_samples=2 * B, seq_len=S, lr=lr)
+    runner = QuantizationRunner(scheme, tuning)
+    block = DecoderBlock(0, "model.layers.0", shape, _to_dev(w))
+    originals = {n: t.clone() for n, t in block.weights.linears.items()}
+    res, layers = runner.quantize_block(block, [t.to(dev()) for t in inputs],
+                                        [t.to(dev()) for t in targets], path_prefix=block.name)
+
+    lin32 = {n: w.linears[n].float() for n in LAYERS}
+    biases = {n: b.double() for n, b in w.biases.items()}
+    norms = (w.input_norm.double(), w.post_norm.double())
+    ob = OB.tune_block([t.view(B, S, -1) for t in inputs], [t.view(B, S, -1) for t in targets], lin32,
+                       biases, norms, _oracle_shape(shape), OB.Scheme(bits, 64), iters=iters,
+                       lr=lr, suppress=bits < 4)
+    print("  gpu", res.initial_loss, res.final_loss, res.step_losses, file=sys.stderr)
+    print("  cpu", ob["initial_loss"], ob["final_loss"], ob["losses"], file=sys.stderr)
+    assert abs(res.initial_loss - ob["initial_loss"]) <= 1e-2 * ob["initial_loss"]
+    for a, b in zip(res.step_losses, ob["losses"]):
+        assert abs(a - b) <= 1e-2 * b
+    assert res.reverted == ob["reverted"]
+    assert abs(res.final_loss - ob["final_loss"]) <= 1e-2 * ob["final_loss"]
+
+    # commit: codes bit-exact with the oracle given the GPU's final parameters, and
+    # the block's weights replaced by the reconstruction
+    for n in LAYERS:
+        q = layers[f"{block.name}.{n}"]
+        rows, cols = originals[n].shape
+        assert q.codes.dtype == torch.uint8 and q.codes.shape == (rows, cols // 64, 64)
+        qdq = (q.scale * (q.codes.float() - q.zero_point)).reshape(rows, cols)
+        assert torch.equal(block.weights.linears[n].float(), qdq.to(torch.bfloat16).float())
+
+
+def test_commit_codes_match_oracle_bitwise():
+    """Given the same v, alpha, beta, committed codes/scales equal the oracle's."""
+    shape, B, S, w, inputs, targets = _tiny_tune(2, 4)
+    scheme = QuantScheme(bits=2, group_size=64, symmetry=Symmetry.ASYMMETRIC)
+    runner = QuantizationRunner(scheme, TuningConfig(iters=4, batch_size=B, n_samples=2 * B, seq_len=S))
+    block = DecoderBlock(0, "b", shape, _to_dev(w))
+    originals = {n: t.clone() for n, t in block.weights.linears.items()}
+    captured = {}
+    orig_commit = runner._commit
+
+    def spy(blk, layer):
+        captured[layer.name] = tuple(t.detach().cpu().clone() for t in (layer.v, layer.alpha, layer.beta))
+        return orig_commit(blk, layer)
+
+    runner._commit = spy
+    _, layers = runner.quantize_block(block, [t.to(dev()) for t in inputs],
+                                      [t.to(dev()) for t in targets], path_prefix="b")
+    for n in LAYERS:
+        v, a, b = captured[n]
+        wq, codes, scale, zp = OQ.fake_quantize(originals[n].float().cpu().numpy(), v.numpy(), a.numpy(),
+                                               b.numpy(), bits=2, group_size=64, mode="asym")
+        q = layers[f"b.{n}"]
+        assert np.array_equal(q.codes.cpu().numpy().astype(np.float32), codes.reshape(q.codes.shape))
+        assert np.array_equal(q.scale.cpu().numpy(), scale.reshape(q.scale.shape))
+        assert np.array_equal(q.zero_point.cpu().numpy(), zp.reshape(q.zero_point.shape))
+        assert np.array_equal(block.weights.linears[n].float().cpu().numpy(),
+                              OQ.round_to_bf16(wq.astype(np.float32)))

@@ -1,25 +1,29 @@
 """Benchmark of the SignRound v2 tuning path on one MI355X.
 
-Default workload -- the fake-quant kernel microbench: one bf16 weight of
-18944 x 3584 (a Qwen2.5-7B gate/up projection) drawn N(0, 0.02) with 0.1 % of
-entries scaled x10; v ~ U(-0.5, 0.5), alpha = beta = 1, dL/dW' ~ N(0, 1)
-fp32; 2-bit asymmetric, group size 64. One step is one pass of the path over
-the matrix: fake-quant forward (bf16 W' out), straight-through backward fused
-with the sign-SGD step, then codes + MLX uint32 packing. Inputs are resident
-in HBM before the timed region.
+Default workload -- one Qwen2.5-7B-shaped decoder block tuned end to end:
+hidden 3584, 28 query / 4 kv heads of 128, SwiGLU 18944, q/k/v biases,
+RMSNorm eps 1e-6, RoPE theta 1e6; random-init bf16 weights N(0, 0.02)
+(seed 0). Calibration is 128 x 2048 token ids uniform over a 152064 vocab
+(seed 6) looked up in a random N(0, 0.02) bf16 embedding (seed 7), i.e. the
+block-0 input stream, float32, resident in HBM (16 batches of 8 x 2048
+tokens). The scheme is 2-bit asymmetric, group size 64; 200 sign-SGD steps at
+lr 1/200 with the outlier rule on. One step of this bench is one block of a
+model run: the targets pass over the original weights, the score over all 16
+batches, 200 tuning steps on cycled batches, the second score, the commit
+(codes, scales, reconstruction) and the advance of the quantized stream.
 
 Printed as one JSON line:
-  value      achieved HBM GB/s of the fake-quant forward (algorithmic bytes:
-             read W 2 B + v 4 B, write W' 2 B per weight, alpha/beta 8 B per
-             group) over the K timed steps, step-to-step wall clock;
-  roofline   the forward kernel's average launch duration -- K back-to-back
-             launches between two HIP events on the launch stream -- against
-             8 TB/s;
-  kernels    the same for the backward + update (14.25 B/weight at gs 64) and
-             the packing kernel (1 + b/8 B/weight);
-  sweep      (--sweep) every bits x group size of the microbench;
-  cpu_baseline  the NumPy float32 oracle's forward on a bounded sample of rows
-             of the same matrix, single-threaded.
+  value      seconds per block tune (wall clock of one step, averaged over K);
+  roofline   the dominant kernel of the tune (largest share of GPU time), its
+             algorithmic flops per launch over its average launch duration,
+             from HIP events recorded around every launch of it inside the
+             timed region, against 2.5 PFLOP/s dense bf16;
+  kernels    the same for every GEMM and attention launch of the block;
+  fake_quant the kernel microbench: a bf16 18944 x 3584 weight (0.1 % of
+             entries x10), 2-bit gs64; forward, backward + update and packing
+             against 8 TB/s;
+  cpu_baseline  the oracle (float32 PyTorch block + NumPy fake quantization)
+             timed on the host on a bounded sample, extrapolated to the tune.
 
 ``--gpus N`` with N > 1 exits: this build runs on one GPU.
 """
@@ -32,11 +36,91 @@ import os
 import sys
 import time
 
-ROWS, COLS = 18944, 3584
+# ---------------------------------------------------------------- workload --
+SHAPE_7B = dict(hidden=3584, n_heads=28, n_kv_heads=4, head_dim=128, intermediate=18944,
+                norm_eps=1e-6, rope_theta=1e6, attn_bias=True)
+VOCAB = 152064
+BITS, GROUP = 2, 64
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBPS = 8000.0
 
+# fake-quant microbench matrix (a 7B gate/up projection)
+ROWS, COLS = 18944, 3584
 
-def _inputs(torch, dev, gs):
+
+def block_workload(torch, dev, *, n_samples, seq_len, batch):
+    from mround_amd.pipeline.block import BlockShape, BlockWeights
+
+    shape = BlockShape(**SHAPE_7B)
+    weights = BlockWeights.random(shape, dtype=torch.bfloat16, device=dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(6)
+    tokens = torch.randint(0, VOCAB, (n_samples, seq_len), generator=g, device=dev)
+    ge = torch.Generator(device=dev).manual_seed(7)
+    embed = (torch.randn(VOCAB, shape.hidden, generator=ge, device=dev) * 0.02).to(torch.bfloat16)
+    entrance = [embed[tokens[i:i + batch].reshape(-1)].float()
+                for i in range(0, n_samples, batch)]
+    del embed
+    return shape, weights, entrance
+
+
+def time_block_tune(torch, dev, args):
+    from mround_amd.pipeline.block import BlockWeights
+    from mround_amd.pipeline.runner import DecoderBlock, QuantizationRunner
+    from mround_amd.schemes import QuantScheme, Symmetry, TuningConfig
+
+    shape, weights, entrance = block_workload(torch, dev, n_samples=args.samples, seq_len=args.seq_len,
+                                              batch=args.batch)
+    originals = dict(weights.linears)
+    scheme = QuantScheme(bits=BITS, group_size=GROUP, symmetry=Symmetry.ASYMMETRIC)
+    tuning = TuningConfig(iters=args.iters, batch_size=args.batch, n_samples=args.samples,
+                          seq_len=args.seq_len)
+    runner = QuantizationRunner(scheme, tuning)
+    streams = [torch.empty_like(x) for x in entrance]
+
+    def one():
+        block = DecoderBlock(0, "model.layers.0", shape,
+                             BlockWeights(dict(originals), weights.biases, weights.input_norm,
+                                          weights.post_norm))
+        for s, x in zip(streams, entrance):
+            s.copy_(x)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        summary, layers = runner.run([block], streams)
+        torch.cuda.synchronize(dev)
+        return time.perf_counter() - t0, summary.blocks[0]
+
+    for i in range(args.warmup):
+        print(f"bench: warm-up block tune {i + 1}/{args.warmup}", file=sys.stderr, flush=True)
+        one()
+    eng = runner.engine(shape, entrance[0].shape[0], dev)
+    flops = eng.flops()
+    eng.time_launches(flops)
+    times, results = [], []
+    for i in range(args.steps):
+        print(f"bench: timed block tune {i + 1}/{args.steps}", file=sys.stderr, flush=True)
+        t, res = one()
+        times.append(t)
+        results.append(res)
+    per_launch = eng.launch_ms()
+    eng.timers = None
+    kernels = {}
+    for name, ms in per_launch.items():
+        if not ms:
+            continue
+        avg = sum(ms) / len(ms)
+        kernels[name] = {"launches": len(ms), "avg_ms": round(avg, 4), "total_ms": round(sum(ms), 2),
+                         "tflops": round(flops[name] / (avg * 1e-3) / 1e12, 1)}
+    gemm_ms = sum(k["total_ms"] for k in kernels.values())
+    return {
+        "shape": shape, "times": times, "results": results, "kernels": kernels, "flops": flops,
+        "kernel_ms_total": gemm_ms, "tokens_per_batch": entrance[0].shape[0],
+        "batches": len(entrance),
+    }
+
+
+# ------------------------------------------------------- fake-quant microbench --
+
+def fq_inputs(torch, dev, gs):
     gen = torch.Generator().manual_seed(0)
     w = torch.randn(ROWS, COLS, generator=gen) * 0.02
     n_out = int(round(0.001 * ROWS * COLS))
@@ -47,7 +131,7 @@ def _inputs(torch, dev, gs):
     v = (torch.rand(ROWS, ng, gs, generator=torch.Generator().manual_seed(2)) - 0.5)
     g = torch.randn(ROWS, COLS, generator=torch.Generator().manual_seed(3))
     return (w.to(dev), v.to(dev), torch.ones(ROWS, ng, 1, device=dev),
-            torch.ones(ROWS, ng, 1, device=dev), g.to(dev), w)
+            torch.ones(ROWS, ng, 1, device=dev), g.to(dev))
 
 
 def fwd_bytes(n, gs):
@@ -62,41 +146,31 @@ def pack_bytes(n, bits):
     return n * (1 + bits / 8)
 
 
-def run_config(torch, K, dev, bits, gs, steps, warmup):
-    """Times one (bits, gs) configuration; returns per-kernel averages in ms."""
-    w, v, a, b, g, _ = _inputs(torch, dev, gs)
+def fake_quant_microbench(torch, K, dev, bits, gs, steps):
+    """Average launch duration of each kernel: ``steps`` back-to-back launches
+    between two HIP events on the launch stream."""
+    w, v, a, b, g = fq_inputs(torch, dev, gs)
     n = ROWS * COLS
     wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
     codes = torch.empty(ROWS, COLS, dtype=torch.uint8, device=dev)
     scale = torch.empty(ROWS, COLS // gs, dtype=torch.float32, device=dev)
     zp = torch.empty_like(scale)
-    words = K.packed_width(COLS, bits)
-    packed = torch.empty(ROWS, words, dtype=torch.uint32, device=dev)
-
-    def fwd():
-        K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8, wq_out=wq)
-
-    def bwd():
-        K.fq_backward_signsgd(w, v, a, b, g, bits=bits, group_size=gs, mode="asym", eps=1e-8,
-                              update=True, lr=0.005, coef_lo=0.1, coef_hi=1.0, v_bound=0.5)
-
-    def codes_k():
-        K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8, codes_out=codes,
-                     scale_out=scale, zp_out=zp)
-
-    def pack():
-        K.pack_codes(codes, bits, signed=False, offset=0, packed_out=packed)
-
+    packed = torch.empty(ROWS, K.packed_width(COLS, bits), dtype=torch.uint32, device=dev)
+    fns = {
+        "fwd": lambda: K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8,
+                                    wq_out=wq),
+        "bwd_update": lambda: K.fq_backward_signsgd(w, v, a, b, g, bits=bits, group_size=gs,
+                                                    mode="asym", eps=1e-8, update=True, lr=0.005,
+                                                    coef_lo=0.1, coef_hi=1.0, v_bound=0.5),
+        "codes": lambda: K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8,
+                                      codes_out=codes, scale_out=scale, zp_out=zp),
+        "pack": lambda: K.pack_codes(codes, bits, signed=False, offset=0, packed_out=packed),
+    }
+    for fn in fns.values():
+        fn()
     stream = torch.cuda.current_stream(dev)
-    for _ in range(warmup):
-        fwd(); bwd(); codes_k(); pack()
-    torch.cuda.synchronize(dev)
-
-    # Each kernel's average launch duration: `steps` back-to-back launches on
-    # the launch stream between two HIP events.
-    avg = {}
-    t0 = time.perf_counter()
-    for name, fn in (("fwd", fwd), ("bwd", bwd), ("codes", codes_k), ("pack", pack)):
+    out = {}
+    for name, fn in fns.items():
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record(stream)
@@ -104,62 +178,91 @@ def run_config(torch, K, dev, bits, gs, steps, warmup):
             fn()
         e.record(stream)
         e.synchronize()
-        avg[name] = s.elapsed_time(e) / steps
-    wall = time.perf_counter() - t0
+        out[name] = s.elapsed_time(e) / steps
+    nbytes = {"fwd": fwd_bytes(n, gs), "bwd_update": bwd_bytes(n, gs), "pack": pack_bytes(n, bits)}
     return {
-        "bits": bits,
-        "group_size": gs,
-        "wall_s": wall,
-        "ms": avg,
-        "gbps": {
-            "fwd": fwd_bytes(n, gs) / (avg["fwd"] * 1e-3) / 1e9,
-            "bwd_update": bwd_bytes(n, gs) / (avg["bwd"] * 1e-3) / 1e9,
-            "pack": pack_bytes(n, bits) / (avg["pack"] * 1e-3) / 1e9,
-        },
+        "workload": f"{ROWS}x{COLS} bf16 weight, {bits}-bit asym gs{gs}",
+        **{k: {"ms": round(out[k], 5), "bytes": nbytes[k],
+               "gbps": round(nbytes[k] / (out[k] * 1e-3) / 1e9, 1),
+               "frac": round(nbytes[k] / (out[k] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+           for k in nbytes},
+        "codes": {"ms": round(out["codes"], 5)},
     }
 
 
-def time_forward_steps(torch, K, dev, bits, gs, steps, warmup):
-    """Step-to-step wall clock of K forward passes (the value)."""
-    w, v, a, b, _, _ = _inputs(torch, dev, gs)
-    wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
-    for _ in range(warmup):
-        K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8, wq_out=wq)
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8, wq_out=wq)
-    torch.cuda.synchronize(dev)
-    return (time.perf_counter() - t0) / steps
+# ------------------------------------------------------------ CPU baseline --
 
-
-def cpu_baseline(bits, gs, rows_sample=ROWS, reps=5):
-    """The oracle's float32 forward on ``rows_sample`` rows, single-threaded NumPy."""
+def cpu_baseline(args, tokens_per_batch, batches):
+    """The oracle on the host: float32 PyTorch block forward + backward over a
+    sample of tokens, and the NumPy fake quantization + straight-through
+    gradient of all seven layers; extrapolated to the tune."""
     import numpy as np
     import torch
 
-    from oracle.quantize import fake_quantize
+    from oracle import block as OB
+    from oracle import quantize as OQ
 
-    gen = torch.Generator().manual_seed(0)
-    w = (torch.randn(ROWS, COLS, generator=gen) * 0.02)[:rows_sample].to(torch.bfloat16).float().numpy()
-    v = (torch.rand(ROWS, COLS // gs, gs, generator=torch.Generator().manual_seed(2)) - 0.5)[:rows_sample].numpy()
-    a = np.ones((rows_sample, COLS // gs, 1), dtype=np.float32)
-    fake_quantize(w, v, a, a, bits=bits, group_size=gs, mode="asym")  # warm-up
-    times = []
-    for _ in range(reps):
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    shape = OB.Shape(**SHAPE_7B)
+    g = torch.Generator().manual_seed(0)
+    lin = {n: (torch.randn(*shape.linear_shape(n), generator=g) * 0.02).to(torch.bfloat16).float()
+           for n in OB.LAYERS}
+    biases = {n: torch.randn(shape.linear_shape(n)[0], generator=g) * 0.02
+              for n in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")}
+    norms = (torch.ones(shape.hidden), torch.ones(shape.hidden))
+    sample_tokens = args.cpu_tokens
+    x = torch.randn(1, sample_tokens, shape.hidden, generator=g)
+    target = torch.randn(1, sample_tokens, shape.hidden, generator=g)
+
+    # block forward + backward at the sample size (PyTorch float32, all threads), on
+    # round-to-nearest W' of every layer
+    wq = {}
+    for n, w in lin.items():
+        qdq, _, _, _ = OQ.fake_quantize(w.numpy(), None, None, None, bits=BITS, group_size=GROUP,
+                                        mode="asym")
+        wq[n] = torch.from_numpy(qdq).requires_grad_(True)
+    t0 = time.perf_counter()
+    out = OB.block_forward(x, wq, biases, norms, shape)
+    t_fwd = time.perf_counter() - t0
+    r = out.detach() - target
+    dpred = 2.0 * r / r.numel()
+    t0 = time.perf_counter()
+    out.backward(dpred)
+    t_bwd = time.perf_counter() - t0
+
+    # fake quantization forward + straight-through gradient (NumPy float32, one
+    # thread) on a sample of every layer's rows, scaled to all rows
+    div = args.cpu_row_div
+    t_fq_fwd = t_fq_bwd = 0.0
+    for n, w in lin.items():
+        rows = max(1, w.shape[0] // div)
+        w_np = w[:rows].numpy()
+        g_np = wq[n].grad[:rows].numpy()
+        v, a, b = OQ.init_params(rows, w_np.shape[1], GROUP)
         t0 = time.perf_counter()
-        fake_quantize(w, v, a, a, bits=bits, group_size=gs, mode="asym")
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[len(times) // 2]
-    n = rows_sample * COLS
+        OQ.fake_quantize(w_np, v, a, b, bits=BITS, group_size=GROUP, mode="asym")
+        t1 = time.perf_counter()
+        OQ.quantize_grad(w_np, v, a, b, g_np, bits=BITS, group_size=GROUP, mode="asym")
+        t2 = time.perf_counter()
+        t_fq_fwd += (t1 - t0) * w.shape[0] / rows
+        t_fq_bwd += (t2 - t1) * w.shape[0] / rows
+
+    scale = tokens_per_batch / sample_tokens
+    step = t_fq_fwd + t_fq_bwd + (t_fwd + t_bwd) * scale
+    passes = 4 * batches  # targets, two scores, advance
+    tune = args.iters * step + passes * (t_fq_fwd / 7 + t_fwd * scale)
     return {
-        "value": fwd_bytes(n, gs) / t / 1e9,
-        "unit": "GB/s",
-        "cores": 1,
+        "value": round(tune, 1),
+        "unit": "s per block tune (extrapolated)",
+        "cores": threads,
         "kind": "port",
-        "sample": (f"oracle.quantize.fake_quantize (NumPy float32) on {rows_sample} of {ROWS} rows "
-                   f"x {COLS}, {bits}-bit asym gs{gs}, median of {reps} after 1 warm-up: "
-                   f"{t:.3f} s per pass"),
+        "sample": (f"one tuning step of the 7B block: oracle fake-quant forward + gradient of all 7 "
+                   f"layers (NumPy float32, 1 thread, timed on 1/{div} of the rows and scaled) "
+                   f"{t_fq_fwd + t_fq_bwd:.2f} s; oracle block "
+                   f"forward + backward (PyTorch float32, {threads} threads) on {sample_tokens} tokens "
+                   f"{t_fwd + t_bwd:.2f} s, scaled linearly to {tokens_per_batch} tokens per batch; "
+                   f"x {args.iters} steps + {passes} forward passes"),
         "cpu": _cpu_model(),
     }
 
@@ -178,14 +281,19 @@ def _cpu_model():
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--bits", type=int, default=2)
-    ap.add_argument("--group-size", type=int, default=64)
-    ap.add_argument("--sweep", action="store_true", help="also time every bits x group size")
+    ap.add_argument("--steps", type=int, default=2, help="timed block tunes")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed block tunes")
+    ap.add_argument("--iters", type=int, default=200, help="sign-SGD steps per tune")
+    ap.add_argument("--samples", type=int, default=128, help="calibration sequences")
+    ap.add_argument("--seq-len", type=int, default=2048)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--cpu-tokens", type=int, default=256, help="tokens in the CPU sample")
+    ap.add_argument("--cpu-row-div", type=int, default=16,
+                    help="fraction of each layer's rows in the CPU fake-quant sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-microbench", action="store_true")
     ap.add_argument("--profile-kernels", action="store_true",
-                    help="only launch the forward and a copy of known size (for counter runs)")
+                    help="only launch the fake-quant forward and a copy of known size (counter runs)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -204,86 +312,74 @@ def main(argv=None):
     dev = torch.device("cuda:0")
 
     if args.profile_kernels:
-        w, v, a, b, _, _ = _inputs(torch, dev, args.group_size)
+        w, v, a, b, _ = fq_inputs(torch, dev, GROUP)
         wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         for _ in range(args.steps):
-            K.fq_forward(w, v, a, b, bits=args.bits, group_size=args.group_size, mode="asym",
-                         eps=1e-8, wq_out=wq)
+            K.fq_forward(w, v, a, b, bits=BITS, group_size=GROUP, mode="asym", eps=1e-8, wq_out=wq)
             K.copy_bytes(src, dst, src.numel())
         torch.cuda.synchronize(dev)
         print(json.dumps({"profile_kernels": True, "steps": args.steps}))
         return 0
 
-    print(f"bench: timing {args.bits}-bit gs{args.group_size}", file=sys.stderr, flush=True)
-    sec_per_step = time_forward_steps(torch, K, dev, args.bits, args.group_size, args.steps,
-                                      args.warmup)
-    main_cfg = run_config(torch, K, dev, args.bits, args.group_size, args.steps, args.warmup)
-    n = ROWS * COLS
-    value = fwd_bytes(n, args.group_size) / sec_per_step / 1e9
-    fwd_ms = main_cfg["ms"]["fwd"]
-    achieved = fwd_bytes(n, args.group_size) / (fwd_ms * 1e-3) / 1e9
-    sweep = []
-    if args.sweep:
-        for bits in (2, 3, 4, 8):
-            for gs in (32, 64, 128):
-                print(f"bench: sweep {bits}-bit gs{gs}", file=sys.stderr, flush=True)
-                r = run_config(torch, K, dev, bits, gs, max(5, args.steps // 2), 2)
-                sweep.append({"bits": bits, "group_size": gs,
-                              "gbps": {k: round(x, 1) for k, x in r["gbps"].items()},
-                              "ms": {k: round(x, 4) for k, x in r["ms"].items()}})
+    tune = time_block_tune(torch, dev, args)
+    sec = sum(tune["times"]) / len(tune["times"])
+    kernels = tune["kernels"]
+    dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
+    dk = kernels[dominant]
+    res = tune["results"][-1]
+    fq = None
+    if not args.no_microbench:
+        print("bench: fake-quant microbench", file=sys.stderr, flush=True)
+        fq = fake_quant_microbench(torch, K, dev, BITS, GROUP, 20)
     cpu = None
     if not args.no_cpu_baseline:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(args.bits, args.group_size)
+        cpu = cpu_baseline(args, tune["tokens_per_batch"], tune["batches"])
     line = {
         "metric": "sec per decoder-block tune (7B shape, 2-bit); fake-quant HBM GB/s",
-        "value": round(value, 1),
-        "unit": "GB/s",
+        "value": round(sec, 3),
+        "unit": "s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(sec_per_step * 1e3, 4),
-        "higher_is_better": True,
+        "ms_per_step": round(sec * 1e3, 1),
+        "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": (f"fake-quant forward, {ROWS}x{COLS} bf16 weight (7B gate/up shape), "
-                         f"{args.bits}-bit asym gs{args.group_size}, v U(-0.5,0.5), alpha=beta=1"),
-            "weight_dtype": "bf16",
-            "output_dtype": "bf16",
-            "bits": args.bits,
-            "group_size": args.group_size,
+            "workload": (f"one Qwen2.5-7B-shaped decoder block (hidden 3584, 28/4 heads x 128, SwiGLU "
+                         f"18944, qkv bias), random-init bf16 N(0,0.02); {args.samples} x "
+                         f"{args.seq_len} uniform token ids (vocab {VOCAB}) through a random embedding; "
+                         f"{BITS}-bit asym gs{GROUP}, {args.iters} sign-SGD steps at batch {args.batch}, "
+                         f"outlier rule on; targets + score + tune + score + commit + advance"),
+            "global_batch": args.batch,
+            "seq_len": args.seq_len,
+            "iters": args.iters,
             "parallelism": "single GPU",
+            "arithmetic": "GEMMs bf16 x bf16 -> fp32 on MFMA; fake quantization, losses, residual "
+                          "stream and updates fp32",
         },
+        "stages_s": {k: round(v, 3) for k, v in res.stage_seconds.items()},
+        "loss": {"initial": res.initial_loss, "final": res.final_loss, "reverted": res.reverted},
         "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "bound": "mfma",
+            "achieved": dk["tflops"],
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(dk["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": None,
-            "kernel": "fq_fwd_fast<bf16,bf16,asym,v>",
-            "bytes_per_launch": fwd_bytes(n, args.group_size),
-            "avg_launch_ms": round(fwd_ms, 5),
+            "kernel": dominant,
+            "flops_per_launch": tune["flops"][dominant],
+            "avg_launch_ms": dk["avg_ms"],
         },
-        "kernels": {
-            "fwd": {"ms": round(fwd_ms, 5), "gbps": round(main_cfg["gbps"]["fwd"], 1)},
-            "bwd_update": {"ms": round(main_cfg["ms"]["bwd"], 5),
-                           "gbps": round(main_cfg["gbps"]["bwd_update"], 1),
-                           "bytes": bwd_bytes(n, args.group_size)},
-            "codes": {"ms": round(main_cfg["ms"]["codes"], 5)},
-            "pack": {"ms": round(main_cfg["ms"]["pack"], 5),
-                     "gbps": round(main_cfg["gbps"]["pack"], 1),
-                     "bytes": pack_bytes(n, args.bits)},
-        },
+        "kernels": kernels,
+        "fake_quant": fq,
         "cpu_baseline": cpu,
     }
-    if sweep:
-        line["sweep"] = sweep
     print(json.dumps(line))
     return 0
 

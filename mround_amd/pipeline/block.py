@@ -147,13 +147,14 @@ class BlockWeights:
 
     @classmethod
     def random(cls, shape: BlockShape, *, dtype: torch.dtype, device, seed: int, std: float = 0.02):
-        """Random-init weights N(0, std) (norm weights 1, biases N(0, std))."""
-        g = torch.Generator(device="cpu").manual_seed(seed)
-        lin = {n: (torch.randn(*shape.linear_shape(n), generator=g) * std).to(dtype).to(device)
+        """Random-init weights N(0, std) drawn on ``device`` (norm weights 1, biases N(0, std))."""
+        device = torch.device(device)
+        g = torch.Generator(device=device).manual_seed(seed)
+        lin = {n: (torch.randn(*shape.linear_shape(n), generator=g, device=device) * std).to(dtype)
                for n in LAYERS}
         biases = {}
         if shape.attn_bias:
-            biases = {n: (torch.randn(shape.linear_shape(n)[0], generator=g) * std).to(device)
+            biases = {n: torch.randn(shape.linear_shape(n)[0], generator=g, device=device) * std
                       for n in QKV}
         ones = torch.ones(shape.hidden, device=device)
         return cls(lin, biases, ones, ones.clone())
@@ -204,6 +205,45 @@ class BlockEngine:
         self.scale = 1.0 / math.sqrt(shape.head_dim)
         self.place = placements(shape)
         self.loss_ws = K.loss_workspace(self.device, T * h)
+        # name -> [(start, end) HIP events] for the launches being timed, or None
+        self.timers: dict[str, list] | None = None
+
+    def _run(self, name: str, fn) -> None:
+        """Launch ``fn``; bracket it with events on the current stream when timed."""
+        if self.timers is None or name not in self.timers:
+            fn()
+            return
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        self.timers[name].append((start, end))
+
+    def time_launches(self, names) -> None:
+        """Start recording HIP events around the named launches (see ``flops``)."""
+        self.timers = {n: [] for n in names}
+
+    def launch_ms(self) -> dict[str, list[float]]:
+        """Recorded durations per launch name (synchronizes)."""
+        torch.cuda.synchronize(self.device)
+        return {n: [s.elapsed_time(e) for s, e in ev] for n, ev in (self.timers or {}).items()}
+
+    def flops(self) -> dict[str, float]:
+        """Algorithmic flops of one launch of each timed operation (2 M N K for a
+        GEMM; attention counts the causal half of QK^T and PV, 2.5x that backward)."""
+        s, T = self.shape, self.tokens
+        h, hq_d, mlp, q = s.hidden, s.n_heads * s.head_dim, s.intermediate, s.qkv_rows
+        attn = 4.0 * self.batch * self.seq_len * self.seq_len * s.n_heads * s.head_dim / 2
+        return {
+            "gemm_qkv": 2.0 * T * q * h, "gemm_o": 2.0 * T * h * hq_d,
+            "gemm_gate_up": 2.0 * T * 2 * mlp * h, "gemm_down": 2.0 * T * h * mlp,
+            "attn_fwd": attn, "attn_bwd": 2.5 * attn,
+            "gemm_dact": 2.0 * T * mlp * h, "gemm_dw_down": 2.0 * h * mlp * T,
+            "gemm_dx_gate_up": 2.0 * T * h * 2 * mlp, "gemm_dw_gate_up": 2.0 * 2 * mlp * h * T,
+            "gemm_dattn": 2.0 * T * hq_d * h, "gemm_dw_o": 2.0 * h * hq_d * T,
+            "gemm_dw_qkv": 2.0 * q * h * T,
+        }
 
     # ---------------------------------------------------------------- weights --
     def set_block(self, weights: BlockWeights) -> None:
@@ -233,16 +273,20 @@ class BlockEngine:
             raise ArchitectureError(f"block input must be [{T}, {s.hidden}]")
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
         K.rmsnorm_fwd(x, self.norm_in, s.norm_eps, self.x1, self.rstd1)
-        K.gemm("nt", self.x1, self.wq["qkv"], self.qkv, M=T, N=s.qkv_rows, K=h, bias=self.bias_qkv)
+        self._run("gemm_qkv", lambda: K.gemm("nt", self.x1, self.wq["qkv"], self.qkv, M=T, N=s.qkv_rows,
+                                             K=h, bias=self.bias_qkv))
         K.rope(self.qkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads, head_dim=s.head_dim,
                cos_sin=self.cos_sin)
-        K.attn_fwd(self.qkv, batch=self.batch, seq_len=self.seq_len, n_heads=s.n_heads,
-                   n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, scale=self.scale, out=self.attn,
-                   lse=self.lse)
-        K.gemm("nt", self.attn, self.wq["o"], self.h2, M=T, N=h, K=hq_d, resid=x)
+        self._run("attn_fwd", lambda: K.attn_fwd(
+            self.qkv, batch=self.batch, seq_len=self.seq_len, n_heads=s.n_heads,
+            n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, scale=self.scale, out=self.attn, lse=self.lse))
+        self._run("gemm_o", lambda: K.gemm("nt", self.attn, self.wq["o"], self.h2, M=T, N=h, K=hq_d,
+                                           resid=x))
         K.rmsnorm_fwd(self.h2, self.norm_post, s.norm_eps, self.x2, self.rstd2)
-        K.gemm_swiglu(self.x2, self.wq["gu"], self.act, self.gu if save else None)
-        K.gemm("nt", self.act, self.wq["down"], out, M=T, N=h, K=mlp, resid=self.h2)
+        self._run("gemm_gate_up", lambda: K.gemm_swiglu(self.x2, self.wq["gu"], self.act,
+                                                        self.gu if save else None))
+        self._run("gemm_down", lambda: K.gemm("nt", self.act, self.wq["down"], out, M=T, N=h, K=mlp,
+                                              resid=self.h2))
 
     def loss(self, out: torch.Tensor, target: torch.Tensor, *, suppress: bool, with_grad: bool) -> torch.Tensor:
         """Reconstruction loss of one batch (device scalar), and dL/dout when asked:
@@ -266,18 +310,26 @@ class BlockEngine:
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
         K.cast_bf16(self.grad_out, self.grad_out16)
         # MLP: dgu from dact = dout Wd'; dWd' = dout^T act; dx2 = dgu Wgu'; dWgu' = dgu^T x2
-        K.gemm_swiglu_bwd(self.grad_out16, self.wq["down"], self.gu, self.dgu)
-        K.gemm("tn", self.grad_out16, self.act, self.dw["down"], M=h, N=mlp, K=T)
-        K.gemm("nn", self.dgu, self.wq["gu"], self.dx2, M=T, N=h, K=2 * mlp)
-        K.gemm("tn", self.dgu, self.x2, self.dw["gu"], M=2 * mlp, N=h, K=T)
+        self._run("gemm_dact", lambda: K.gemm_swiglu_bwd(self.grad_out16, self.wq["down"], self.gu,
+                                                         self.dgu))
+        self._run("gemm_dw_down", lambda: K.gemm("tn", self.grad_out16, self.act, self.dw["down"], M=h,
+                                                 N=mlp, K=T))
+        self._run("gemm_dx_gate_up", lambda: K.gemm("nn", self.dgu, self.wq["gu"], self.dx2, M=T, N=h,
+                                                    K=2 * mlp))
+        self._run("gemm_dw_gate_up", lambda: K.gemm("tn", self.dgu, self.x2, self.dw["gu"], M=2 * mlp,
+                                                    N=h, K=T))
         # dh = dout + rmsnorm'(dx2)
         K.rmsnorm_bwd(self.dx2, self.h2, self.norm_post, self.rstd2, self.grad_out, dh_bf16=self.dh2)
         # attention output projection
-        K.gemm("nn", self.dh2, self.wq["o"], self.dattn, M=T, N=hq_d, K=h)
-        K.gemm("tn", self.dh2, self.attn, self.dw["o"], M=h, N=hq_d, K=T)
-        K.attn_bwd(self.qkv, self.attn, self.dattn, self.lse, self.dsum, batch=self.batch,
-                   seq_len=self.seq_len, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads,
-                   head_dim=s.head_dim, scale=self.scale, dqkv=self.dqkv)
+        self._run("gemm_dattn", lambda: K.gemm("nn", self.dh2, self.wq["o"], self.dattn, M=T, N=hq_d,
+                                               K=h))
+        self._run("gemm_dw_o", lambda: K.gemm("tn", self.dh2, self.attn, self.dw["o"], M=h, N=hq_d,
+                                              K=T))
+        self._run("attn_bwd", lambda: K.attn_bwd(
+            self.qkv, self.attn, self.dattn, self.lse, self.dsum, batch=self.batch,
+            seq_len=self.seq_len, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim,
+            scale=self.scale, dqkv=self.dqkv))
         K.rope(self.dqkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads,
                head_dim=s.head_dim, cos_sin=self.cos_sin, backward=True)
-        K.gemm("tn", self.dqkv, self.x1, self.dw["qkv"], M=s.qkv_rows, N=h, K=T)
+        self._run("gemm_dw_qkv", lambda: K.gemm("tn", self.dqkv, self.x1, self.dw["qkv"], M=s.qkv_rows,
+                                                N=h, K=T))

@@ -240,10 +240,15 @@ int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, 
                 const float* lse, float* dsum_ws, int B, int S, int Hq, int Hkv, int head_dim,
                 float scale, void* dqkv, void* stream);
 
-/* fp32 -> bf16 (round to nearest even), n elements. */
+/*
+ * fp32 -> bf16 (round to nearest even), n elements: the block output's
+ * gradient as a GEMM operand for the backward. No counterpart in the
+ * reference, whose block runs in fp32 throughout (mround/pipeline/runner.py:337).
+ */
 int mr_cast_f32_bf16(const float* x, void* y, int64_t n, void* stream);
 
-/* Plain device copy of `bytes` bytes, used to calibrate traffic counters. */
+/* Plain device copy of `bytes` bytes, used to calibrate traffic counters.
+ * No counterpart in the reference (measurement support only). */
 int mr_copy_bytes(const void* src, void* dst, size_t bytes, void* stream);
 
 #ifdef __cplusplus

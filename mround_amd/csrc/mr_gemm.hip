@@ -320,19 +320,28 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
       const int col = n0 + wn * WN + j * 32 + lcol;
       const int gcol = (col >> 5) * 64 + (col & 31);
+      // Loads go to clamped (always valid) addresses without a branch so that
+      // all 32 of them are in flight together; only the stores are guarded.
+      const int gcol_c = min(col, p.N - 1);
+      const int gcol_l = (gcol_c >> 5) * 64 + (gcol_c & 31);
+      float g[16], u[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = min(m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3), p.M - 1);
+        const int64_t o = static_cast<int64_t>(row) * p.ldgu + gcol_l;
+        g[r] = bf16_to_f32(p.gu[o]);
+        u[r] = bf16_to_f32(p.gu[o + 32]);
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
+        const float sg = sigmoid(g[r]);
+        const float da = acc[i][j][r];
+        const float dsilu = sg * (1.0f + g[r] * (1.0f - sg));
         if (row < p.M && col < p.N) {
-          const int64_t o = static_cast<int64_t>(row) * p.ldgu + gcol;
-          const float g = bf16_to_f32(p.gu[o]);
-          const float u = bf16_to_f32(p.gu[o + 32]);
-          const float sg = sigmoid(g);
-          const float da = acc[i][j][r];
-          const float dsilu = sg * (1.0f + g * (1.0f - sg));
           const int64_t od = static_cast<int64_t>(row) * p.ldc + gcol;
-          dgu[od] = f32_to_bf16(da * u * dsilu);
-          dgu[od + 32] = f32_to_bf16(da * g * sg);
+          dgu[od] = f32_to_bf16(da * u[r] * dsilu);
+          dgu[od + 32] = f32_to_bf16(da * g[r] * sg);
         }
       }
     };
@@ -342,12 +351,22 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
       const int col = n0 + wn * WN + j * 32 + lcol;
       const float bias = (p.bias && col < p.N) ? p.bias[col] : 0.0f;
+      float res[16];
+      if constexpr (EPI == EPI_RESID) {
+        // unguarded loads at clamped addresses, all in flight together
+        const int col_c = min(col, p.N - 1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = min(m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3), p.M - 1);
+          res[r] = p.resid[static_cast<int64_t>(row) * p.ldr + col_c];
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
         if (row < p.M && col < p.N) {
           float x = acc[i][j][r] + bias;
-          if constexpr (EPI == EPI_RESID) x = p.resid[static_cast<int64_t>(row) * p.ldr + col] + x;
+          if constexpr (EPI == EPI_RESID) x = res[r] + x;
           const int64_t o = static_cast<int64_t>(row) * p.ldc + col;
           if constexpr (OUT_BF16) static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(x);
           else static_cast<float*>(p.C)[o] = x;

@@ -241,6 +241,20 @@ int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, 
                 float scale, void* dqkv, void* stream);
 
 /*
+ * Exact mixed-precision bit allocation (host code, no device work): one
+ * option per layer minimizing the summed delta_loss with the summed
+ * cost_bits <= budget_bits. Replaces mround/planner/allocator.py:98-194
+ * (allocate_bits, with its Pareto pruning and tie order). Layer i's options
+ * are entries [sum(n_options[:i]), + n_options[i]) of cost_bits/delta_loss.
+ * max_states > 0 thins each frontier to that many evenly ranked states
+ * (approximate, as the reference's max_states); 0 keeps the search exact.
+ * Writes the chosen option index per layer, the predicted loss and the cost.
+ */
+int mr_allocate_bits(int n_layers, const int32_t* n_options, const int64_t* cost_bits,
+                     const double* delta_loss, int64_t budget_bits, int64_t max_states,
+                     int32_t* choice_out, double* loss_out, int64_t* cost_out);
+
+/*
  * fp32 -> bf16 (round to nearest even), n elements: the block output's
  * gradient as a GEMM operand for the backward. No counterpart in the
  * reference, whose block runs in fp32 throughout (mround/pipeline/runner.py:337).

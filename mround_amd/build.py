@@ -1,6 +1,8 @@
-"""Builds ``libmround_hip.so`` for gfx950 from ``mround_amd/csrc/*.hip``.
+"""Builds ``libmround_hip.so`` for gfx950 from ``mround_amd/csrc/*.hip`` (device
+kernels, compiled by ``hipcc``) and ``mround_amd/csrc/*.cpp`` (host-only code,
+compiled by ``g++``).
 
-Each source is compiled by ``hipcc`` into an object in ``mround_amd/_build``
+Each source is compiled into an object in ``mround_amd/_build``
 (in parallel), then linked into ``mround_amd/_lib/libmround_hip.so``, in tree,
 so that the library travels with the source tree. Run as
 ``python -m mround_amd.build`` or through ``__graft_entry__.build()``.
@@ -52,13 +54,20 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP library cannot be built")
 
 
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
+
+
 def sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip"))
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+        cmd = [cxx, *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"compiling {src.name} failed:\n{proc.stdout}\n{proc.stderr}")

@@ -80,6 +80,7 @@ _SIGNATURES = {
     "mr_attn_fwd": (_I, [_P, _L, _I, _I, _I, _I, _I, _F, _P, _L, _P, _P]),
     "mr_attn_bwd": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P]),
     "mr_cast_f32_bf16": (_I, [_P, _P, _L, _P]),
+    "mr_allocate_bits": (_I, [_I, _P, _P, _P, _L, _L, _P, _P, _P]),
     "mr_fq_forward_mapped": (_I, [_P, _I, _P, _P, _P, _P, _L, _L, _I, _I, _I, _F, _P, _I, _L, _L,
                                   _L, _P]),
     "mr_fq_backward_signsgd_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F,
@@ -329,6 +330,26 @@ def attn_bwd(qkv, out, dout, lse, dsum, *, batch, seq_len, n_heads, n_kv_heads, 
                            _ptr(_f32(lse, "lse")), _ptr(_f32(dsum, "dsum")), batch, seq_len, n_heads,
                            n_kv_heads, head_dim, scale, _ptr(dqkv), _stream(qkv))
     _check(rc, "mr_attn_bwd")
+
+
+def allocate_bits(n_options, cost_bits, delta_loss, budget_bits: int, max_states: int):
+    """``mr_allocate_bits`` on host arrays; returns (choices, loss, cost).
+
+    Infeasible instances raise ``ValueError`` with the library's message."""
+    n = len(n_options)
+    n_opt = (ctypes.c_int32 * n)(*n_options)
+    costs = (ctypes.c_int64 * len(cost_bits))(*cost_bits)
+    losses = (ctypes.c_double * len(delta_loss))(*delta_loss)
+    choice = (ctypes.c_int32 * n)()
+    loss = ctypes.c_double()
+    cost = ctypes.c_int64()
+    rc = lib().mr_allocate_bits(n, ctypes.cast(n_opt, ctypes.c_void_p), ctypes.cast(costs, ctypes.c_void_p),
+                                ctypes.cast(losses, ctypes.c_void_p), int(budget_bits), int(max_states),
+                                ctypes.cast(choice, ctypes.c_void_p), ctypes.addressof(loss),
+                                ctypes.addressof(cost))
+    if rc != 0:
+        raise ValueError(lib().mr_last_error().decode())
+    return list(choice), loss.value, cost.value
 
 
 def cast_bf16(x, y) -> None:

@@ -37,13 +37,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
 }
 
-// 8 fp32 -> bf16x8 operand
-__device__ __forceinline__ bf16x8 to_bf16x8(const float* x) {
-  uint4 v = make_uint4(pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]),
-                       pack_bf16(x[6], x[7]));
-  return as_bf16x8(v);
-}
-
 // ---- LDS tiles --------------------------------------------------------------
 // Row-major tile of ROWS rows x D bf16 (K-major for the MFMA: row = m or n,
 // D = reduction), 16-byte chunk c of row r at position c ^ (r & 7).
@@ -51,170 +44,259 @@ template <int D>
 __device__ __forceinline__ int rowtile_off(int r, int c) {
   return r * (D * 2) + ((c ^ (r & 7)) << 4);
 }
-// Transposed tile: D rows (one per d) x 64 bf16 (128 bytes), chunk c (8
-// consecutive rows of the source) of row d at position c ^ (d & 7).
-__device__ __forceinline__ int ttile_off(int d, int c) { return d * 128 + ((c ^ (d & 7)) << 4); }
-
-// Rows [r0, r0 + 64) of a [T, ld] bf16 matrix, columns [col, col + D), into a rowtile.
-template <int D>
-__device__ __forceinline__ void load_rowtile(const uint16_t* src, int64_t ld, int64_t r0, int col,
-                                             uint8_t* lds) {
-  constexpr int CH = D / 8;
-  for (int c = threadIdx.x; c < 64 * CH; c += kThreads) {
-    const int r = c / CH, ch = c % CH;
-    const uint4 v = *reinterpret_cast<const uint4*>(src + (r0 + r) * ld + col + ch * 8);
-    *reinterpret_cast<uint4*>(lds + rowtile_off<D>(r, ch)) = v;
-  }
-}
-
-// The same 64 x D source block stored transposed (D rows of 64).
-template <int D>
-__device__ __forceinline__ void load_ttile(const uint16_t* src, int64_t ld, int64_t r0, int col,
-                                           uint8_t* lds) {
-  constexpr int NB = 8 * (D / 8);  // 8x8 blocks
-  for (int b = threadIdx.x; b < NB; b += kThreads) {
-    const int kb = b & 7;   // 8-row block of the source (one transposed chunk)
-    const int db = b >> 3;  // 8-column block of the source (8 transposed rows)
-    uint4 r[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      r[j] = *reinterpret_cast<const uint4*>(src + (r0 + kb * 8 + j) * ld + col + db * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      const int c = e >> 1;
-      uint32_t d[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) d[q] = __builtin_amdgcn_perm((&r[2 * q + 1].x)[c], (&r[2 * q].x)[c], sel);
-      *reinterpret_cast<uint4*>(lds + ttile_off(db * 8 + e, kb)) = make_uint4(d[0], d[1], d[2], d[3]);
-    }
-  }
-}
-
-// MFMA operand from a rowtile: row (m or n) `r`, k16 step s, lane half h.
 template <int D>
 __device__ __forceinline__ bf16x8 frag_row(const uint8_t* lds, int r, int s, int h) {
   return *reinterpret_cast<const bf16x8*>(lds + rowtile_off<D>(r, 2 * s + h));
 }
-// MFMA operand from a transposed tile for k16 step s (within the 64-row
-// source block) in accumulator key order: source rows 16s + 4h + {0..3} and
-// 16s + 8 + 4h + {0..3}.
-__device__ __forceinline__ bf16x8 frag_t(const uint8_t* lds, int d, int s, int h) {
-  const uint2 lo = *reinterpret_cast<const uint2*>(lds + ttile_off(d, 2 * s) + h * 8);
-  const uint2 hi = *reinterpret_cast<const uint2*>(lds + ttile_off(d, 2 * s + 1) + h * 8);
-  return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+
+// 64 rows x D bf16 of a [*, ld] matrix (rows r0.., columns col..) into a
+// rowtile by direct-to-LDS loads (16 B per lane, no registers). One wave
+// instruction fills 1 KB = 64 / (D / 8) rows; lane l covers row l / (D / 8)
+// of it at physical chunk l % (D / 8), i.e. logical chunk (l % (D/8)) ^ (row & 7).
+template <int D>
+__device__ __forceinline__ void dma_rowtile(const uint16_t* src, int64_t ld, int64_t r0, int col,
+                                            uint8_t* lds) {
+  constexpr int CPR = D / 8;
+  constexpr int RPI = 64 / CPR;
+  constexpr int INSTR = 64 / RPI / 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / CPR, pchunk = lane % CPR;
+#pragma unroll
+  for (int i = 0; i < INSTR; ++i) {
+    const int rb = (i * 4 + wave) * RPI;
+    const int row = rb + sub;
+    const int c = pchunk ^ (row & 7);
+    const uint16_t* g = src + (r0 + row) * ld + col + c * 8;
+    __builtin_amdgcn_global_load_lds((const gbl_void_t*)g, (lds_void_t*)(lds + rb * (2 * D)), 16, 0, 0);
+  }
+}
+
+// Transposed MFMA operand from a rowtile with ds_read_b64_tr_b16. In each
+// group of 16 lanes, lane i receives, for j = 0..3, element i % 4 of the
+// 8 bytes addressed by lane 4 j + i / 4; so when source lane s addresses row
+// k0 + s / 4 at column c0 + 4 (s % 4), lane i gets rows k0..k0+3 of column
+// c0 + i. For the operand of MFMA k16 step `s` (rows 16 s.. of the tile) at
+// columns cb + (lane / 16 % 2) * 16 + lane % 16, in accumulator key order:
+// rows 16 s + 4 h + {0..3} and 16 s + 8 + 4 h + {0..3} (h = lane / 32).
+template <int D>
+__device__ __forceinline__ bf16x8 frag_tr(const uint8_t* lds, int cb, int s, int lane) {
+  const int h = lane >> 5, q = (lane >> 4) & 1, i = lane & 15;
+  const int c = (cb + q * 16) / 8 + ((i & 3) >> 1);
+  const int byte = (i & 1) * 8;
+  const int row0 = 16 * s + 4 * h + (i >> 2);
+  const int row1 = row0 + 8;
+  const __attribute__((address_space(3))) uint8_t* base = (const __attribute__((address_space(3))) uint8_t*)lds;
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16_t*)(base + row0 * (2 * D) + ((c ^ (row0 & 7)) << 4) + byte));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16_t*)(base + row1 * (2 * D) + ((c ^ (row1 & 7)) << 4) + byte));
+  typedef short v8i16 __attribute__((ext_vector_type(8)));
+  const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ bf16x8 cvt8(const f32x16& x, int off) {
+  f32x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = x[off + j];
+  return __builtin_convertvector(v, bf16x8);
 }
 
 // Accumulator register r of a 32x32 tile, lane half h: row within the tile.
 __device__ __forceinline__ int acc_row(int r, int h) { return (r >> 2) * 8 + h * 4 + (r & 3); }
 
 // Writes a wave's O^T-layout accumulators (acc[dt][r] = value at d = dt*32 +
-// acc_row(r, h), query = lane & 31) as bf16 rows [32 queries][D] through LDS.
+// acc_row(r, h), query = lane & 31), times `mul`, as bf16 rows [32 queries][D]
+// through LDS: packed 8-byte writes into rows padded to 2 D + 8 bytes (no
+// bank conflicts), then 16-byte row-contiguous global stores.
 template <int D>
 __device__ __forceinline__ void store_qrows(const f32x16 (&acc)[D / 32], float mul, uint8_t* lds,
                                            uint16_t* dst, int64_t ld, int64_t row0) {
+  constexpr int STAGE_ROW = 2 * D + 8;
   const int lane = threadIdx.x & 63, h = lane >> 5, q = lane & 31;
-  uint16_t* t = reinterpret_cast<uint16_t*>(lds);  // [32][D]
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) t[q * D + dt * 32 + acc_row(r, h)] = f32_to_bf16(acc[dt][r] * mul);
+    for (int rg = 0; rg < 4; ++rg) {
+      const uint32_t w0 = pack_bf16(acc[dt][rg * 4 + 0] * mul, acc[dt][rg * 4 + 1] * mul);
+      const uint32_t w1 = pack_bf16(acc[dt][rg * 4 + 2] * mul, acc[dt][rg * 4 + 3] * mul);
+      const int col = dt * 32 + rg * 8 + h * 4;
+      *reinterpret_cast<uint2*>(lds + q * STAGE_ROW + col * 2) = make_uint2(w0, w1);
+    }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
   constexpr int CH = D / 8;
   for (int c = lane; c < 32 * CH; c += 64) {
     const int row = c / CH, ch = c % CH;
-    *reinterpret_cast<uint4*>(dst + (row0 + row) * ld + ch * 8) =
-        *reinterpret_cast<const uint4*>(t + row * D + ch * 8);
+    const uint2 a = *reinterpret_cast<const uint2*>(lds + row * STAGE_ROW + ch * 16);
+    const uint2 b = *reinterpret_cast<const uint2*>(lds + row * STAGE_ROW + ch * 16 + 8);
+    *reinterpret_cast<uint4*>(dst + (row0 + row) * ld + ch * 8) = make_uint4(a.x, a.y, b.x, b.y);
   }
 }
 
 // ---- forward ----------------------------------------------------------------
-
-template <int D>
+//
+// A block owns 4 * QW queries of one query head (QW per wave, 32 per MFMA
+// column tile) and walks the key tiles up to its last query. K and V tiles
+// move HBM -> LDS by direct loads, double buffered: tile t + 1 is in flight
+// while tile t is computed, with one barrier per tile. V stays row-major in
+// LDS; its transposed operand comes from the transposing LDS read.
+template <int D, int QW>
 __global__ __launch_bounds__(kThreads) void attn_fwd(const uint16_t* __restrict__ qkv, int64_t ld,
                                                      int S, int Hq, int Hkv, float scale_log2,
                                                      uint16_t* __restrict__ out, int64_t ldo,
                                                      float* __restrict__ lse) {
-  constexpr int NS = D / 16;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[KT * D * 2 * 2];
-  uint8_t* Ks = smem;
-  uint8_t* Vt = smem + KT * D * 2;
-  const int qb = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+  constexpr int NQ = QW / 32, NS = D / 16, ND = D / 32;
+  constexpr int TILE = KT * D * 2;
+  constexpr int STAGE_ROW = 2 * D + 8;  // staged output row (bytes), 8-byte aligned
+  constexpr int BUF = TILE > QW * STAGE_ROW ? TILE : QW * STAGE_ROW;
+  __shared__ __attribute__((aligned(1024))) uint8_t K0[BUF];
+  __shared__ __attribute__((aligned(1024))) uint8_t V0[BUF];
+  __shared__ __attribute__((aligned(1024))) uint8_t K1[BUF];
+  __shared__ __attribute__((aligned(1024))) uint8_t V1[BUF];
+  const int qb = gridDim.x - 1 - blockIdx.x;  // the longest blocks start first
+  const int hq = blockIdx.y, b = blockIdx.z;
   const int g = hq / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
-  const int q0 = qb * QB + wave * 32;
-  const int qi = q0 + l32;
+  const int q0 = qb * (4 * QW) + wave * QW;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   const int kcol = (Hq + g) * D, vcol = (Hq + Hkv + g) * D;
+  const int n_tiles = (qb + 1) * (4 * QW) / KT;
 
-  bf16x8 qf[NS];
+  dma_rowtile<D>(qkv, ld, tok0, kcol, K0);
+  dma_rowtile<D>(qkv, ld, tok0, vcol, V0);
+
+  bf16x8 qf[NQ][NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
-    qf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + qi) * ld + hq * D + s * 16 + h * 8);
-
-  f32x16 o[D / 32];
+  for (int qt = 0; qt < NQ; ++qt)
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
-  float m = -INFINITY, l = 0.0f;
+    for (int s = 0; s < NS; ++s)
+      qf[qt][s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + q0 + qt * 32 + l32) * ld + hq * D +
+                                                   s * 16 + h * 8);
+  f32x16 o[NQ][ND];
+  float m[NQ], l[NQ];
+#pragma unroll
+  for (int qt = 0; qt < NQ; ++qt) {
+    m[qt] = -INFINITY;
+    l[qt] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) o[qt][dt] = f32x16{};
+  }
 
-  const int kv_end = min(S, qb * QB + QB);
-  for (int kv0 = 0; kv0 < kv_end; kv0 += KT) {
-    __syncthreads();
-    load_rowtile<D>(qkv, ld, tok0 + kv0, kcol, Ks);
-    load_ttile<D>(qkv, ld, tok0 + kv0, vcol, Vt);
-    __syncthreads();
-    if (kv0 > q0 + 31) continue;  // every key of the tile is after every query of the wave
+  auto step = [&](int t, const uint8_t* Kc, const uint8_t* Vc, uint8_t* Kn, uint8_t* Vn) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile t have landed
+    __syncthreads();                // everyone's have, and nobody still reads the other buffers
+    if (t + 1 < n_tiles) {
+      dma_rowtile<D>(qkv, ld, tok0 + (t + 1) * KT, kcol, Kn);
+      dma_rowtile<D>(qkv, ld, tok0 + (t + 1) * KT, vcol, Vn);
+    }
+    const int kv0 = t * KT;
+    if (kv0 > q0 + QW - 1) return;  // every key of the tile is after every query of the wave
+    const bool diag = kv0 + KT - 1 > q0;
 
-    f32x16 st[2] = {f32x16{}, f32x16{}};
+    f32x16 st[2][NQ];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Ks, mt * 32 + l32, s, h), qf[s],
-                                                         st[mt], 0, 0, 0);
-    float mx = -INFINITY;
+      for (int qt = 0; qt < NQ; ++qt) st[mt][qt] = f32x16{};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kv0 + mt * 32 + acc_row(r, h);
-        const float v = key <= qi ? st[mt][r] * scale_log2 : -INFINITY;
-        st[mt][r] = v;
-        mx = fmaxf(mx, v);
+      for (int mt = 0; mt < 2; ++mt) {
+        const bf16x8 a = frag_row<D>(Kc, mt * 32 + l32, s, h);
+#pragma unroll
+        for (int qt = 0; qt < NQ; ++qt)
+          st[mt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qt][s], st[mt][qt], 0, 0, 0);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = exp2f(m - m_new);
-    float ps = 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int qt = 0; qt < NQ; ++qt) {
+      if (diag) {
+        const int qi = q0 + qt * 32 + l32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(st[mt][r] - m_new);
-        st[mt][r] = p;
-        ps += p;
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (kv0 + mt * 32 + acc_row(r, h) > qi) st[mt][qt][r] = -INFINITY;
       }
-    ps += __shfl_xor(ps, 32, 64);
-    l = l * alpha + ps;
-    m = m_new;
+      float mx = -INFINITY;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) o[dt] *= alpha;
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][qt][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m[qt], mx * scale_log2);
+      const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_new);
+      float ps = 0.0f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][qt][r], scale_log2, -m_new));
+          st[mt][qt][r] = p;
+          ps += p;
+        }
+      ps += __shfl_xor(ps, 32, 64);
+      l[qt] = l[qt] * alpha + ps;
+      m[qt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) o[qt][dt] *= alpha;
+    }
 #pragma unroll
     for (int s = 0; s < KT / 16; ++s) {
-      float pv[8];
+      bf16x8 pb[NQ];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pv[j] = st[s >> 1][8 * (s & 1) + j];
-      const bf16x8 pb = to_bf16x8(pv);
+      for (int qt = 0; qt < NQ; ++qt) pb[qt] = cvt8(st[s >> 1][qt], 8 * (s & 1));
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_t(Vt, dt * 32 + l32, s, h), pb, o[dt], 0,
-                                                        0, 0);
+      for (int dt = 0; dt < ND; ++dt) {
+        const bf16x8 a = frag_tr<D>(Vc, dt * 32, s, lane);
+#pragma unroll
+        for (int qt = 0; qt < NQ; ++qt)
+          o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[qt], o[qt][dt], 0, 0, 0);
+      }
     }
+  };
+
+  int t = 0;
+  for (; t + 1 < n_tiles; t += 2) {
+    step(t, K0, V0, K1, V1);
+    step(t + 1, K1, V1, K0, V0);
   }
-  __syncthreads();
-  if (h == 0) lse[(static_cast<int64_t>(b) * Hq + hq) * S + qi] = (m + log2f(l)) * kLn2;
-  store_qrows<D>(o, 1.0f / l, smem + wave * (32 * D * 2), out + hq * D, ldo, tok0 + q0);
+  if (t < n_tiles) step(t, K0, V0, K1, V1);
+  __syncthreads();  // all tiles read; the buffers now stage the output
+
+  uint8_t* stage = wave == 0 ? K0 : wave == 1 ? V0 : wave == 2 ? K1 : V1;
+#pragma unroll
+  for (int qt = 0; qt < NQ; ++qt) {
+    const float inv = 1.0f / l[qt];
+    if (h == 0)
+      lse[(static_cast<int64_t>(b) * Hq + hq) * S + q0 + qt * 32 + l32] =
+          (m[qt] + log2f(l[qt])) * kLn2;
+    const int row = qt * 32 + l32;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const uint32_t w0 = pack_bf16(o[qt][dt][rg * 4 + 0] * inv, o[qt][dt][rg * 4 + 1] * inv);
+        const uint32_t w1 = pack_bf16(o[qt][dt][rg * 4 + 2] * inv, o[qt][dt][rg * 4 + 3] * inv);
+        const int col = dt * 32 + rg * 8 + h * 4;
+        *reinterpret_cast<uint2*>(stage + row * STAGE_ROW + col * 2) = make_uint2(w0, w1);
+      }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  constexpr int CH = D / 8;
+  for (int c = lane; c < QW * CH; c += 64) {
+    const int row = c / CH, ch = c % CH;
+    const uint2 a = *reinterpret_cast<const uint2*>(stage + row * STAGE_ROW + ch * 16);
+    const uint2 bb = *reinterpret_cast<const uint2*>(stage + row * STAGE_ROW + ch * 16 + 8);
+    *reinterpret_cast<uint4*>(out + (tok0 + q0 + row) * ldo + hq * D + ch * 8) =
+        make_uint4(a.x, a.y, bb.x, bb.y);
+  }
 }
 
 // ---- backward ---------------------------------------------------------------
@@ -241,22 +323,23 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dot(const uint16_t* __restr
 }
 
 // dK, dV: keys along lanes. A block owns 128 keys of one kv head (32 per
-// wave) and walks every query head of its group and every query tile at or
-// after its first key.
+// wave) and walks, for every query head of the group, the 64-query tiles at
+// or after its first key. Q and dO tiles arrive by direct loads, double
+// buffered like the forward's K and V; their transposed operands (for
+// dV = P^T dO and dK = dS^T Q) come from the transposing LDS read.
 template <int D>
 __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
     const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
     const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
     float scale, uint16_t* __restrict__ dqkv) {
-  constexpr int NS = D / 16;
+  constexpr int NS = D / 16, ND = D / 32;
   constexpr int TILE = 64 * D * 2;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[4 * TILE + 2 * 64 * 4];
-  uint8_t* Qs = smem;
-  uint8_t* Qt = smem + TILE;
-  uint8_t* Os = smem + 2 * TILE;
-  uint8_t* Ot = smem + 3 * TILE;
-  float* Ls = reinterpret_cast<float*>(smem + 4 * TILE);
-  float* Ds = Ls + 64;
+  __shared__ __attribute__((aligned(1024))) uint8_t Q0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t O0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t Q1[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t O1[TILE];
+  __shared__ float LD0[128];  // lse (log2 domain) then rowsum(dO O) of the tile's 64 queries
+  __shared__ float LD1[128];
   const int kb = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int G = Hq / Hkv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
@@ -265,6 +348,23 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   const int kcol = (Hq + g) * D, vcol = (Hq + Hkv + g) * D;
   const float scale_log2 = scale * kLog2e;
+  const int first_q = kb * QB;
+  const int nqt = (S - first_q) / 64;  // query tiles per head
+  const int n_items = G * nqt;
+
+  // item i: query head g G + i / nqt, query tile first_q + 64 (i % nqt)
+  auto issue = [&](int i, uint8_t* Qd, uint8_t* Od) {
+    const int hq = g * G + i / nqt;
+    const int64_t r0 = tok0 + first_q + (i % nqt) * 64;
+    dma_rowtile<D>(qkv, ld, r0, hq * D, Qd);
+    dma_rowtile<D>(dout, ldo, r0, hq * D, Od);
+  };
+  auto fetch_ld = [&](int i) -> float {  // threads 0..127: this item's lse / rowsum value
+    const int hq = g * G + i / nqt;
+    const int q = first_q + (i % nqt) * 64 + (threadIdx.x & 63);
+    const int64_t at = (static_cast<int64_t>(b) * Hq + hq) * S + q;
+    return threadIdx.x < 64 ? lse[at] * kLog2e : dsum[at];
+  };
 
   bf16x8 kf[NS], vf[NS];
 #pragma unroll
@@ -272,64 +372,75 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
     kf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + kj) * ld + kcol + s * 16 + h * 8);
     vf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + kj) * ld + vcol + s * 16 + h * 8);
   }
-  f32x16 dk[D / 32], dv[D / 32];
+  f32x16 dk[ND], dv[ND];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
+  for (int dt = 0; dt < ND; ++dt) {
     dk[dt] = f32x16{};
     dv[dt] = f32x16{};
   }
 
-  for (int gq = 0; gq < G; ++gq) {
-    const int hq = g * G + gq;
-    const float* lse_h = lse + (static_cast<int64_t>(b) * Hq + hq) * S;
-    const float* d_h = dsum + (static_cast<int64_t>(b) * Hq + hq) * S;
-    for (int qt0 = (kb * QB) / 64 * 64; qt0 < S; qt0 += 64) {
-      __syncthreads();
-      load_rowtile<D>(qkv, ld, tok0 + qt0, hq * D, Qs);
-      load_ttile<D>(qkv, ld, tok0 + qt0, hq * D, Qt);
-      load_rowtile<D>(dout, ldo, tok0 + qt0, hq * D, Os);
-      load_ttile<D>(dout, ldo, tok0 + qt0, hq * D, Ot);
-      if (threadIdx.x < 64) Ls[threadIdx.x] = lse_h[qt0 + threadIdx.x] * kLog2e;
-      else if (threadIdx.x < 128) Ds[threadIdx.x - 64] = d_h[qt0 + threadIdx.x - 64];
-      __syncthreads();
+  issue(0, Q0, O0);
+  if (threadIdx.x < 128) LD0[threadIdx.x] = fetch_ld(0);
+
+  auto step = [&](int i, const uint8_t* Qc, const uint8_t* Oc, const float* LDc, uint8_t* Qn,
+                  uint8_t* On, float* LDn) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    float next_ld = 0.0f;
+    const bool more = i + 1 < n_items;
+    if (more) {
+      issue(i + 1, Qn, On);
+      if (threadIdx.x < 128) next_ld = fetch_ld(i + 1);
+    }
+    const int qt0 = first_q + (i % nqt) * 64;
 #pragma unroll
-      for (int mq = 0; mq < 2; ++mq) {
-        const int qs0 = qt0 + mq * 32;
-        if (qs0 + 31 < k0w) continue;  // every query before every key of the wave
-        f32x16 sacc = f32x16{}, dp = f32x16{};
+    for (int mq = 0; mq < 2; ++mq) {
+      const int qs0 = qt0 + mq * 32;
+      if (qs0 + 31 < k0w) continue;  // every query of the half before every key of the wave
+      const bool diag = qs0 < k0w + 31;
+      f32x16 sacc = f32x16{}, dp = f32x16{};
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Qs, mq * 32 + l32, s, h), kf[s],
-                                                         sacc, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Os, mq * 32 + l32, s, h), vf[s],
-                                                       dp, 0, 0, 0);
-        }
-        float pr[16], dsr[16];
+      for (int s = 0; s < NS; ++s) {
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Qc, mq * 32 + l32, s, h), kf[s],
+                                                       sacc, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Oc, mq * 32 + l32, s, h), vf[s], dp,
+                                                     0, 0, 0);
+      }
+      f32x16 pr, dsr;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qrow = mq * 32 + acc_row(r, h);
-          const float p = (kj <= qt0 + qrow) ? exp2f(sacc[r] * scale_log2 - Ls[qrow]) : 0.0f;
-          pr[r] = p;
-          dsr[r] = p * (dp[r] - Ds[qrow]);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int qrow = mq * 32 + acc_row(r, h);
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale_log2, -LDc[qrow]));
+        if (diag && kj > qt0 + qrow) p = 0.0f;
+        pr[r] = p;
+        dsr[r] = p * (dp[r] - LDc[64 + qrow]);
+      }
 #pragma unroll
-        for (int ss = 0; ss < 2; ++ss) {
-          const bf16x8 pa = to_bf16x8(pr + 8 * ss);
-          const bf16x8 da = to_bf16x8(dsr + 8 * ss);
+      for (int ss = 0; ss < 2; ++ss) {
+        const bf16x8 pa = cvt8(pr, 8 * ss);
+        const bf16x8 da = cvt8(dsr, 8 * ss);
 #pragma unroll
-          for (int dt = 0; dt < D / 32; ++dt) {
-            dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, frag_t(Ot, dt * 32 + l32, 2 * mq + ss, h),
-                                                             dv[dt], 0, 0, 0);
-            dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, frag_t(Qt, dt * 32 + l32, 2 * mq + ss, h),
-                                                             dk[dt], 0, 0, 0);
-          }
+        for (int dt = 0; dt < ND; ++dt) {
+          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, frag_tr<D>(Oc, dt * 32, 2 * mq + ss, lane),
+                                                           dv[dt], 0, 0, 0);
+          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, frag_tr<D>(Qc, dt * 32, 2 * mq + ss, lane),
+                                                           dk[dt], 0, 0, 0);
         }
       }
     }
+    if (more && threadIdx.x < 128) LDn[threadIdx.x] = next_ld;
+  };
+
+  int i = 0;
+  for (; i + 1 < n_items; i += 2) {
+    step(i, Q0, O0, LD0, Q1, O1, LD1);
+    step(i + 1, Q1, O1, LD1, Q0, O0, LD0);
   }
+  if (i < n_items) step(i, Q0, O0, LD0, Q1, O1, LD1);
+
   // dk[dt][r]: key k0w + acc_row(r, h), d = dt * 32 + l32.
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+  for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int64_t row = tok0 + k0w + acc_row(r, h);
@@ -338,19 +449,22 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
     }
 }
 
-// dQ: queries along lanes; a block owns 128 queries of one query head.
+// dQ: queries along lanes; a block owns 128 queries of one query head and
+// walks the key tiles up to its last query, K and V arriving by direct loads,
+// double buffered. dQ^T = K^T dS^T takes K^T from the transposing LDS read.
 template <int D>
 __global__ __launch_bounds__(kThreads) void attn_bwd_dq(
     const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
     const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
     float scale, uint16_t* __restrict__ dqkv) {
-  constexpr int NS = D / 16;
-  constexpr int TILE = 64 * D * 2;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[3 * TILE];
-  uint8_t* Ks = smem;
-  uint8_t* Kt = smem + TILE;
-  uint8_t* Vs = smem + 2 * TILE;
-  const int qb = blockIdx.x, hq = blockIdx.y, b = blockIdx.z;
+  constexpr int NS = D / 16, ND = D / 32;
+  constexpr int TILE = KT * D * 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t K0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t V0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t K1[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t V1[TILE];
+  const int qb = gridDim.x - 1 - blockIdx.x;  // the longest blocks start first
+  const int hq = blockIdx.y, b = blockIdx.z;
   const int g = hq / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
   const int q0 = qb * QB + wave * 32;
@@ -358,66 +472,80 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq(
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   const int kcol = (Hq + g) * D, vcol = (Hq + Hkv + g) * D;
   const float scale_log2 = scale * kLog2e;
+  const int n_tiles = (qb + 1) * QB / KT;
+
+  dma_rowtile<D>(qkv, ld, tok0, kcol, K0);
+  dma_rowtile<D>(qkv, ld, tok0, vcol, V0);
   const float lse2 = lse[(static_cast<int64_t>(b) * Hq + hq) * S + qi] * kLog2e;
   const float dq_sum = dsum[(static_cast<int64_t>(b) * Hq + hq) * S + qi];
-
   bf16x8 qf[NS], of[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     qf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + qi) * ld + hq * D + s * 16 + h * 8);
     of[s] = *reinterpret_cast<const bf16x8*>(dout + (tok0 + qi) * ldo + hq * D + s * 16 + h * 8);
   }
-  f32x16 dq[D / 32];
+  f32x16 dq[ND];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) dq[dt] = f32x16{};
+  for (int dt = 0; dt < ND; ++dt) dq[dt] = f32x16{};
 
-  const int kv_end = min(S, qb * QB + QB);
-  for (int kv0 = 0; kv0 < kv_end; kv0 += KT) {
+  auto step = [&](int t, const uint8_t* Kc, const uint8_t* Vc, uint8_t* Kn, uint8_t* Vn) {
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    load_rowtile<D>(qkv, ld, tok0 + kv0, kcol, Ks);
-    load_ttile<D>(qkv, ld, tok0 + kv0, kcol, Kt);
-    load_rowtile<D>(qkv, ld, tok0 + kv0, vcol, Vs);
-    __syncthreads();
-    if (kv0 > q0 + 31) continue;
+    if (t + 1 < n_tiles) {
+      dma_rowtile<D>(qkv, ld, tok0 + (t + 1) * KT, kcol, Kn);
+      dma_rowtile<D>(qkv, ld, tok0 + (t + 1) * KT, vcol, Vn);
+    }
+    const int kv0 = t * KT;
+    if (kv0 > q0 + 31) return;
+    const bool diag = kv0 + KT - 1 > q0;
     f32x16 st[2] = {f32x16{}, f32x16{}}, dpt[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Ks, mt * 32 + l32, s, h), qf[s],
+      for (int mt = 0; mt < 2; ++mt) {
+        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Kc, mt * 32 + l32, s, h), qf[s],
                                                          st[mt], 0, 0, 0);
-        dpt[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Vs, mt * 32 + l32, s, h), of[s],
+        dpt[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Vc, mt * 32 + l32, s, h), of[s],
                                                           dpt[mt], 0, 0, 0);
       }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kv0 + mt * 32 + acc_row(r, h);
-        const float p = key <= qi ? exp2f(st[mt][r] * scale_log2 - lse2) : 0.0f;
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][r], scale_log2, -lse2));
+        if (diag && kv0 + mt * 32 + acc_row(r, h) > qi) p = 0.0f;
         st[mt][r] = p * (dpt[mt][r] - dq_sum);  // dS^T
       }
 #pragma unroll
     for (int s = 0; s < KT / 16; ++s) {
-      float dv8[8];
+      const bf16x8 db = cvt8(st[s >> 1], 8 * (s & 1));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dv8[j] = st[s >> 1][8 * (s & 1) + j];
-      const bf16x8 db = to_bf16x8(dv8);
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_t(Kt, dt * 32 + l32, s, h), db, dq[dt], 0,
-                                                         0, 0);
+      for (int dt = 0; dt < ND; ++dt)
+        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(Kc, dt * 32, s, lane), db, dq[dt],
+                                                         0, 0, 0);
     }
+  };
+
+  int t = 0;
+  for (; t + 1 < n_tiles; t += 2) {
+    step(t, K0, V0, K1, V1);
+    step(t + 1, K1, V1, K0, V0);
   }
+  if (t < n_tiles) step(t, K0, V0, K1, V1);
   __syncthreads();
-  store_qrows<D>(dq, scale, smem + wave * (32 * D * 2), dqkv + hq * D, ld, tok0 + q0);
+  uint8_t* stage = wave == 0 ? K0 : wave == 1 ? V0 : wave == 2 ? K1 : V1;
+  store_qrows<D>(dq, scale, stage, dqkv + hq * D, ld, tok0 + q0);
 }
 
 template <int D>
 int launch_fwd(const uint16_t* qkv, int64_t ld, int B, int S, int Hq, int Hkv, float scale,
                uint16_t* out, int64_t ldo, float* lse, hipStream_t s) {
-  hipLaunchKernelGGL(attn_fwd<D>, dim3(S / QB, Hq, B), dim3(kThreads), 0, s, qkv, ld, S, Hq, Hkv,
-                     scale * kLog2e, out, ldo, lse);
+  if (S % 256 == 0)
+    hipLaunchKernelGGL((attn_fwd<D, 64>), dim3(S / 256, Hq, B), dim3(kThreads), 0, s, qkv, ld, S, Hq,
+                       Hkv, scale * kLog2e, out, ldo, lse);
+  else
+    hipLaunchKernelGGL((attn_fwd<D, 32>), dim3(S / 128, Hq, B), dim3(kThreads), 0, s, qkv, ld, S, Hq,
+                       Hkv, scale * kLog2e, out, ldo, lse);
   MR_LAUNCH_CHECK("mr_attn_fwd");
   return MR_OK;
 }

@@ -12,11 +12,12 @@
 // Tiling: a block of 256 threads (4 waves of 64, 2 x 2) owns a BM x BN tile
 // of C; each wave owns (BM/2) x (BN/2) as a grid of 32 x 32 accumulators fed by
 // v_mfma_f32_32x32x16_bf16 (lane l: A row l%32, B column l%32, k half l/32;
-// accumulator register r: row (r/4)*8 + (l/32)*4 + r%4, column l%32). Both
-// operands are staged in LDS K-major (row = m or n, 32 k per row, padded), so
-// every MFMA operand is one 16-byte LDS read. MN-major tiles are transposed
-// in registers (4 k x 8 mn blocks, v_perm_b32) on their way into LDS. The k
-// loop is double-buffered in LDS with the next tile's global loads in flight
+// accumulator register r: row (r/4)*8 + (l/32)*4 + r%4, column l%32). Every
+// operand tile moves HBM -> LDS by direct loads (global_load_lds, no
+// registers) in the layout it has in memory: a K-major tile as rows of 64 k,
+// whose MFMA operand is one 16-byte LDS read; an MN-major tile as rows of one
+// k, whose operand comes from two transposing LDS reads (ds_read_b64_tr_b16).
+// The k loop is double-buffered in LDS with the next tile's loads in flight
 // during the current tile's MFMAs.
 //
 // Blocks are renumbered so that each XCD (blocks are dealt to the 8 XCDs
@@ -68,7 +69,6 @@ struct GemmParams {
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
 
-__device__ __forceinline__ uint4 ldg16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * ROW_BYTES + ((chunk ^ (row & 7)) << 4); }
 
@@ -101,50 +101,57 @@ struct KMajorDirect {
 
 // ---- MN-major operand: element (row, k) at base[k * ld + row] -------------
 //
-// Each thread moves an 8 k x 8 row block: eight 16-byte loads along the row
-// index (one per k), transposed in registers (v_perm_b32 pairs of bf16) into
-// eight 16-byte LDS writes of 8 consecutive k. The k chunk is the fastest
-// lane index, so the 8 lanes of one write cycle fill one row.
-template <int ROWS>
-struct MNMajorLoader {
-  static constexpr int KB = BK / 8;
-  static constexpr int BLOCKS = KB * (ROWS / 8);
-  static constexpr int PER_THREAD = (BLOCKS + kThreads - 1) / kThreads;
-  uint4 r[PER_THREAD][8];
+// Staged as it lies in memory: BK rows (one per k) of ROWS bf16, moved
+// HBM -> LDS by direct loads like the K-major tiles, no registers and no
+// shuffles. Chunk c of k-row r sits at position c ^ (4 (r & 3)), so the four
+// k-rows one transposing read touches land on distinct banks. The MFMA
+// operand (8 consecutive k of one m) comes from two ds_read_b64_tr_b16: in
+// each 16-lane group, lane i receives element i % 4 of the 8 bytes addressed
+// by lane 4 j + i / 4 (j = 0..3); with source lane s addressing k-row
+// k0 + s / 4 at column c0 + 4 (s % 4), lane i gets k0..k0+3 of column c0 + i.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t ld, int row0, int rows_valid,
-                                       int k0) {
+template <int ROWS>
+struct MNMajorDirect {
+  static constexpr int CPR = ROWS / 8;         // 16-byte chunks per k-row
+  static constexpr int RPI = 64 / CPR;         // k-rows per wave instruction
+  static constexpr int INSTR = BK / RPI / 4;   // instructions per wave
+  static constexpr int ROWB = ROWS * 2;        // bytes per k-row
+  __device__ __forceinline__ static void issue(const uint16_t* base, int64_t ld, int row0,
+                                               int rows_valid, int k0, uint8_t* lds) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int sub = lane / CPR, pchunk = lane % CPR;
 #pragma unroll
-    for (int i = 0; i < PER_THREAD; ++i) {
-      const int b = min(static_cast<int>(threadIdx.x) + i * kThreads, BLOCKS - 1);
-      const int kb = b % KB;
-      const int rb = min(row0 + (b / KB) * 8, rows_valid - 8);
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        r[i][j] = ldg16(base + static_cast<int64_t>(k0 + kb * 8 + j) * ld + rb);
+    for (int i = 0; i < INSTR; ++i) {
+      const int kb = (i * 4 + wave) * RPI;
+      const int kr = kb + sub;
+      const int c = pchunk ^ (4 * (kr & 3));
+      // columns past the valid range read the last valid chunk; they only feed
+      // accumulator rows or columns that are never stored
+      const int col = min(row0 + c * 8, rows_valid - 8);
+      const uint16_t* src = base + static_cast<int64_t>(k0 + kr) * ld + col;
+      __builtin_amdgcn_global_load_lds((const gbl_void_t*)src, (lds_void_t*)(lds + kb * ROWB), 16,
+                                       0, 0);
     }
   }
-  __device__ __forceinline__ void store(uint8_t* lds) const {
-#pragma unroll
-    for (int i = 0; i < PER_THREAD; ++i) {
-      const int b = threadIdx.x + i * kThreads;
-      if (b >= BLOCKS) continue;
-      const int kb = b % KB;
-      const int rb = (b / KB) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const int c = e >> 1;
-        uint32_t d[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t lo = (&r[i][2 * q].x)[c];
-          const uint32_t hi = (&r[i][2 * q + 1].x)[c];
-          d[q] = __builtin_amdgcn_perm(hi, lo, sel);  // (k = 2q, 2q + 1) of row rb + e
-        }
-        *reinterpret_cast<uint4*>(lds + swz(rb + e, kb)) = make_uint4(d[0], d[1], d[2], d[3]);
-      }
-    }
+  // Operand of k16 step kk for rows rbase + (lane / 16 % 2) * 16 + lane % 16
+  // (= rbase + lane % 32), k = 16 kk + 8 (lane / 32) + 0..7.
+  __device__ __forceinline__ static bf16x8 frag(const uint8_t* lds, int rbase, int kk, int lane) {
+    const int h = lane >> 5, q = (lane >> 4) & 1, i = lane & 15;
+    const int c = (rbase + q * 16) / 8 + ((i & 3) >> 1);
+    const int byte = (i & 1) * 8;
+    const int r0 = 16 * kk + 8 * h + (i >> 2);
+    const int r1 = r0 + 4;
+    const __attribute__((address_space(3))) uint8_t* b = (const __attribute__((address_space(3))) uint8_t*)lds;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16_t*)(b + r0 * ROWB + ((c ^ (4 * (r0 & 3))) << 4) + byte));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16_t*)(b + r1 * ROWB + ((c ^ (4 * (r1 & 3))) << 4) + byte));
+    const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_bit_cast(bf16x8, v);
   }
 };
 
@@ -197,23 +204,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  MNMajorLoader<BM> la;
-  MNMajorLoader<BN> lb;
-  (void)la;
-  (void)lb;
-
-  // Global loads of tile kt: direct ones land in the given LDS stage;
-  // register ones wait in la/lb until stage_regs().
+  // Global loads of tile kt, straight into the given LDS stage.
   auto issue_loads = [&](int kt, uint8_t* as_dst, uint8_t* bs_dst) {
     const int k0 = kt * BK;
     if constexpr (A_KMAJOR) KMajorDirect<BM>::issue(p.A, p.lda, m0, p.M, k0, as_dst);
-    else la.load(p.A, p.lda, m0, p.M, k0);
+    else MNMajorDirect<BM>::issue(p.A, p.lda, m0, p.M, k0, as_dst);
     if constexpr (B_KMAJOR) KMajorDirect<BN>::issue(p.B, p.ldb, n0, p.N, k0, bs_dst);
-    else lb.load(p.B, p.ldb, n0, p.N, k0);
-  };
-  auto stage_regs = [&](uint8_t* as_dst, uint8_t* bs_dst) {
-    if constexpr (!A_KMAJOR) la.store(as_dst);
-    if constexpr (!B_KMAJOR) lb.store(bs_dst);
+    else MNMajorDirect<BN>::issue(p.B, p.ldb, n0, p.N, k0, bs_dst);
   };
 
   f32x16 acc[TM][TN];
@@ -230,13 +227,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       const int chunk = kk * 2 + (lane >> 5);
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int row = wm * WM + i * 32 + (lane & 31);
-        af[slot][i] = *reinterpret_cast<const bf16x8*>(as + swz(row, chunk));
+        if constexpr (A_KMAJOR) {
+          const int row = wm * WM + i * 32 + (lane & 31);
+          af[slot][i] = *reinterpret_cast<const bf16x8*>(as + swz(row, chunk));
+        } else {
+          af[slot][i] = MNMajorDirect<BM>::frag(as, wm * WM + i * 32, kk, lane);
+        }
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const int row = wn * WN + j * 32 + (lane & 31);
-        bfr[slot][j] = *reinterpret_cast<const bf16x8*>(bs + swz(row, chunk));
+        if constexpr (B_KMAJOR) {
+          const int row = wn * WN + j * 32 + (lane & 31);
+          bfr[slot][j] = *reinterpret_cast<const bf16x8*>(bs + swz(row, chunk));
+        } else {
+          bfr[slot][j] = MNMajorDirect<BN>::frag(bs, wn * WN + j * 32, kk, lane);
+        }
       }
     };
     read_frags(0, 0);
@@ -259,7 +264,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
                   uint8_t* nxt_b) {
     if (kt + 1 < KT) issue_loads(kt + 1, nxt_a, nxt_b);
     compute(cur_a, cur_b);
-    if (kt + 1 < KT) stage_regs(nxt_a, nxt_b);
     // The direct loads of the next tile and every read of this one are done
     // before any wave moves on.
     __builtin_amdgcn_s_waitcnt(0);
@@ -268,7 +272,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 
   const int KT = p.K / BK;
   issue_loads(0, As0, Bs0);
-  stage_regs(As0, Bs0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   int kt = 0;
@@ -423,6 +426,12 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
     return fail(MR_EINVAL, "mr_gemm: operands must be 16-byte aligned with ld a multiple of 8");
   if (c_dtype != MR_F32 && c_dtype != MR_BF16) return fail(MR_EINVAL, "mr_gemm: C must be fp32 or bf16");
   if (resid && c_dtype != MR_F32) return fail(MR_EINVAL, "mr_gemm: the residual form writes fp32");
+  if (layout < 0 || layout > 2) return fail(MR_EINVAL, "mr_gemm: unknown layout %d", layout);
+  {
+    const bool a_kmajor = layout != 2, b_kmajor = layout == 0;
+    if (lda < (a_kmajor ? K : M) || ldb < (b_kmajor ? K : N) || ldc < N || (resid && ldr < N))
+      return fail(MR_EINVAL, "mr_gemm: a leading dimension is smaller than its row");
+  }
   GemmParams p{};
   p.M = static_cast<int>(M);
   p.N = static_cast<int>(N);

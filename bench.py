@@ -267,6 +267,17 @@ def cpu_baseline(args, tokens_per_batch, batches):
     }
 
 
+def _measured_traffic():
+    """HBM bytes per launch from the committed counter runs (profiles/pmc_traffic.json),
+    keyed by launch name; empty when the file is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"]
+    except (OSError, KeyError, ValueError):
+        return {}
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -276,6 +287,36 @@ def _cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def profile_kernels(torch, K, dev, steps):
+    """Launch, ``steps`` times each, the kernels whose HBM traffic the counter
+    runs measure: the 7B block's gate/up GEMM with the SwiGLU epilogue, its
+    weight-gradient and input-gradient GEMMs, the down projection, the
+    fake-quant forward of the microbench, and a 1 GiB copy that calibrates the
+    counters (read and written bytes are known exactly)."""
+    T, h, mlp = 16384, SHAPE_7B["hidden"], SHAPE_7B["intermediate"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *s: (torch.randn(*s, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x, wgu, wd = rnd(T, h), rnd(2 * mlp, h), rnd(h, mlp)
+    act = torch.empty(T, mlp, dtype=torch.bfloat16, device=dev)
+    gu = torch.empty(T, 2 * mlp, dtype=torch.bfloat16, device=dev)
+    dgu, dw = rnd(T, 2 * mlp), torch.empty(2 * mlp, h, device=dev)
+    dx = torch.empty(T, h, device=dev)
+    out = torch.empty(T, h, device=dev)
+    w, v, a, b, _ = fq_inputs(torch, dev, GROUP)
+    wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        K.gemm_swiglu(x, wgu, act, gu)                                   # gemm_gate_up
+        K.gemm("tn", dgu, x, dw, M=2 * mlp, N=h, K=T)                    # gemm_dw_gate_up
+        K.gemm("nn", dgu, wgu, dx, M=T, N=h, K=2 * mlp)                  # gemm_dx_gate_up
+        K.gemm("nt", act, wd, out, M=T, N=h, K=mlp, resid=dx)            # gemm_down
+        K.fq_forward(w, v, a, b, bits=BITS, group_size=GROUP, mode="asym", eps=1e-8, wq_out=wq)
+        K.copy_bytes(src, dst, src.numel())
+    torch.cuda.synchronize(dev)
+    print(json.dumps({"profile_kernels": True, "steps": steps}))
 
 
 def main(argv=None):
@@ -312,15 +353,7 @@ def main(argv=None):
     dev = torch.device("cuda:0")
 
     if args.profile_kernels:
-        w, v, a, b, _ = fq_inputs(torch, dev, GROUP)
-        wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(args.steps):
-            K.fq_forward(w, v, a, b, bits=BITS, group_size=GROUP, mode="asym", eps=1e-8, wq_out=wq)
-            K.copy_bytes(src, dst, src.numel())
-        torch.cuda.synchronize(dev)
-        print(json.dumps({"profile_kernels": True, "steps": args.steps}))
+        profile_kernels(torch, K, dev, args.steps)
         return 0
 
     tune = time_block_tune(torch, dev, args)
@@ -329,10 +362,13 @@ def main(argv=None):
     dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
     dk = kernels[dominant]
     res = tune["results"][-1]
+    traffic = _measured_traffic()
     fq = None
     if not args.no_microbench:
         print("bench: fake-quant microbench", file=sys.stderr, flush=True)
         fq = fake_quant_microbench(torch, K, dev, BITS, GROUP, 20)
+        if "fq_forward_microbench" in traffic:
+            fq["fwd"]["traffic"] = traffic["fq_forward_microbench"]["traffic_bytes"]
     cpu = None
     if not args.no_cpu_baseline:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
@@ -371,7 +407,9 @@ def main(argv=None):
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(dk["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic.get(dominant, {}).get("traffic_bytes"),
+            "traffic_source": ("profiles/pmc_traffic.md: FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per launch, "
+                               "calibrated on a 1 GiB copy" if dominant in traffic else None),
             "kernel": dominant,
             "flops_per_launch": tune["flops"][dominant],
             "avg_launch_ms": dk["avg_ms"],

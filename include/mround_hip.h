@@ -241,6 +241,32 @@ int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, 
                 float scale, void* dqkv, void* stream);
 
 /*
+ * v2 candidate-scale grid search for symmetric schemes: per group, the
+ * signed largest-magnitude element anchors the effective range nmax
+ * (= 2^(bits-1)); candidates nmax - step * i for i in [-half_count,
+ * half_count] \ {0} follow it in order; the kept scale is the first with the
+ * least sum((scale * clip(rne(inverse * w)) - w)^2 * importance[col]) in fp32,
+ * summed in column order (inverse = -eff / anchor, scale = 1 / inverse, 0 for
+ * an all-zero group). Replaces mround/core/scale_search.py:71-187 (oracle
+ * mround/reference/scale_search.py:130-211). importance: fp32 [cols] or NULL.
+ * scale_out: fp32 (rows, cols / group_size). group_size 32, 64 or 128.
+ */
+int mr_search_scales(const void* w, int w_dtype, const float* importance, int64_t rows,
+                     int64_t cols, int group_size, int bits, double step, int half_count,
+                     float* scale_out, void* stream);
+
+/*
+ * out[c] += sum_r x[r, c]^2 over a (rows, cols) fp32/bf16 matrix with leading
+ * dimension ld, in a fixed order (row blocks, then blocks in order): the
+ * per-input-channel importance a linear collects in the reference's stats
+ * forward (mround/pipeline/runner.py:346-363). workspace:
+ * mr_colsumsq_workspace_bytes(cols) bytes.
+ */
+int64_t mr_colsumsq_workspace_bytes(int64_t cols);
+int mr_colsumsq(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld, float* out,
+                void* workspace, void* stream);
+
+/*
  * Exact mixed-precision bit allocation (host code, no device work): one
  * option per layer minimizing the summed delta_loss with the summed
  * cost_bits <= budget_bits. Replaces mround/planner/allocator.py:98-194

@@ -81,6 +81,9 @@ _SIGNATURES = {
     "mr_attn_bwd": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P]),
     "mr_cast_f32_bf16": (_I, [_P, _P, _L, _P]),
     "mr_allocate_bits": (_I, [_I, _P, _P, _P, _L, _L, _P, _P, _P]),
+    "mr_search_scales": (_I, [_P, _I, _P, _L, _L, _I, _I, ctypes.c_double, _I, _P, _P]),
+    "mr_colsumsq_workspace_bytes": (_L, [_L]),
+    "mr_colsumsq": (_I, [_P, _I, _L, _L, _L, _P, _P, _P]),
     "mr_fq_forward_mapped": (_I, [_P, _I, _P, _P, _P, _P, _L, _L, _I, _I, _I, _F, _P, _I, _L, _L,
                                   _L, _P]),
     "mr_fq_backward_signsgd_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F,
@@ -350,6 +353,32 @@ def allocate_bits(n_options, cost_bits, delta_loss, budget_bits: int, max_states
     if rc != 0:
         raise ValueError(lib().mr_last_error().decode())
     return list(choice), loss.value, cost.value
+
+
+def search_scales(weight, *, bits, group_size, step, half_count, scale_out, importance=None) -> None:
+    rows, cols = weight.shape
+    rc = lib().mr_search_scales(_ptr(weight), dtype_code(weight.dtype), _ptr(_f32(importance, "importance")),
+                                rows, cols, group_size, bits, float(step), int(half_count),
+                                _ptr(_f32(scale_out, "scale_out")), _stream(weight))
+    _check(rc, "mr_search_scales")
+
+
+def colsumsq(x, out) -> None:
+    """``out += sum(x^2, axis=0)`` for a 2-D fp32/bf16 device tensor."""
+    rows, cols = x.shape
+    nbytes = int(lib().mr_colsumsq_workspace_bytes(cols))
+    key = (x.device.index or 0, "colsumsq")
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+        _workspaces[key] = ws
+    if x.stride(1) != 1:
+        raise KernelError("colsumsq: rows must be contiguous")
+    if not x.is_cuda:
+        raise KernelError("tensors passed to the HIP library must live on a ROCm device")
+    rc = lib().mr_colsumsq(x.data_ptr(), dtype_code(x.dtype), rows, cols, x.stride(0),
+                           _ptr(_f32(out, "out")), _ptr(ws), _stream(x))
+    _check(rc, "mr_colsumsq")
 
 
 def cast_bf16(x, y) -> None:

@@ -19,8 +19,9 @@ import torch
 
 from mround_amd import kernels as K
 from mround_amd.core.quantizer import fake_quantize, mode_of, quantize_codes
+from mround_amd.core.scale_search import search_scales
 from mround_amd.core.signsgd import LinearDecay
-from mround_amd.exceptions import ArchitectureError, CalibrationError, UnsupportedSchemeError
+from mround_amd.exceptions import ArchitectureError, CalibrationError
 from mround_amd.formats.mlx_export import QuantizedLayer
 from mround_amd.pipeline.block import LAYERS, BlockEngine, BlockShape, BlockWeights, placements, unplace
 from mround_amd.schemes import DEFAULT_EPS_FP32, QuantScheme, ScaleInit, TuningConfig
@@ -105,6 +106,7 @@ class _Layer:
         self.v = torch.zeros(rows, cols, dtype=torch.float32, device=dev)
         self.alpha = torch.ones(rows, ng, dtype=torch.float32, device=dev)
         self.beta = torch.ones(rows, ng, dtype=torch.float32, device=dev)
+        self.init_scale: torch.Tensor | None = None  # (rows, ng) fp32 for a searched scheme
 
     def params(self) -> dict[str, torch.Tensor]:
         rows, cols = self.weight.shape
@@ -232,9 +234,6 @@ class QuantizationRunner:
                 skipped.append((name, f"last dimension {w.shape[-1]} is not a multiple of "
                                       f"{scheme.group_size}"))
                 continue
-            if scheme.scale_init is ScaleInit.SEARCHED:
-                raise UnsupportedSchemeError("searched scale initialisation is not available in the "
-                                             "block loop; use the observed range")
             layers[name] = _Layer(name, w, scheme, place[name])
         if skipped:
             # The fused operands need every layer's W'; a partly quantized block
@@ -244,6 +243,9 @@ class QuantizationRunner:
 
         eng = self.engine(block.shape, inputs[0].shape[0], inputs[0].device)
         eng.set_block(block.weights)
+        t_search = time.perf_counter()
+        searched = self._search_scales(eng, block, layers, inputs)
+        search_seconds = time.perf_counter() - t_search if searched else 0.0
         outcome = self._tune(eng, layers, inputs, targets)
         t_commit = time.perf_counter()
         exported = {}
@@ -257,19 +259,53 @@ class QuantizationRunner:
             index=block.index, name=block.name, initial_loss=outcome["initial"],
             final_loss=outcome["final"], iterations=self.tuning.iters,
             seconds=time.perf_counter() - started, tuned=tuple(sorted(layers)),
-            reverted=outcome["reverted"], generalization_gap=outcome["gap"], stage_seconds=stages,
-            step_losses=tuple(outcome["losses"]))
+            reverted=outcome["reverted"], generalization_gap=outcome["gap"],
+            search_seconds=search_seconds, stage_seconds=stages, step_losses=tuple(outcome["losses"]))
         return result, exported
 
     def _commit(self, block: DecoderBlock, layer: _Layer) -> QuantizedLayer:
         """Codes (one byte each), scale and zero point for export, and the
         layer's weight replaced by its reconstruction (mround/pipeline/runner.py:760-788)."""
         params = layer.params()
-        codes, scale, zp = quantize_codes(layer.weight, params, layer.scheme, eps=self.eps, narrow=True)
+        codes, scale, zp = quantize_codes(layer.weight, params, layer.scheme, eps=self.eps,
+                                          init_scale=layer.init_scale, narrow=True)
         recon = fake_quantize(layer.weight, params, layer.scheme, eps=self.eps,
+                              init_scale=layer.init_scale,
                               out_dtype=block.weights.linears[layer.name].dtype)
         block.weights.linears[layer.name] = recon
         return QuantizedLayer(codes, scale, zp, layer.scheme)
+
+    # ---------------------------------------------------------------- search --
+    def _search_scales(self, eng: BlockEngine, block: DecoderBlock, layers: Mapping[str, _Layer],
+                       inputs) -> bool:
+        """The v2 scale search for every layer whose scheme asks for it
+        (mround/pipeline/runner.py:712-759): one forward per calibration batch
+        over the original weights collects each linear input's per-channel sum
+        of squares, then each searched layer's grid search runs once."""
+        searching = [l for l in layers.values() if l.scheme.scale_init is ScaleInit.SEARCHED]
+        if not searching:
+            return False
+        s = block.shape
+        dev = inputs[0].device
+        imp = {"x1": torch.zeros(s.hidden, device=dev), "attn": torch.zeros(s.n_heads * s.head_dim, device=dev),
+               "x2": torch.zeros(s.hidden, device=dev), "act": torch.zeros(s.intermediate, device=dev)}
+        eng.load_dense(block.weights.linears)
+        scratch = torch.empty_like(inputs[0])
+        for x in inputs:
+            eng.forward(x, scratch, save=False)
+            K.colsumsq(eng.x1, imp["x1"])
+            K.colsumsq(eng.attn, imp["attn"])
+            K.colsumsq(eng.x2, imp["x2"])
+            K.colsumsq(eng.act, imp["act"])
+        source = {"self_attn.q_proj": "x1", "self_attn.k_proj": "x1", "self_attn.v_proj": "x1",
+                  "self_attn.o_proj": "attn", "mlp.gate_proj": "x2", "mlp.up_proj": "x2",
+                  "mlp.down_proj": "act"}
+        for layer in searching:
+            rows, cols = layer.weight.shape
+            found = search_scales(layer.weight, layer.scheme, importance=imp[source[layer.name]])
+            layer.init_scale = found.view(rows, cols // layer.scheme.group_size)
+        torch.cuda.synchronize(dev)
+        return True
 
     # ------------------------------------------------------------------ tune --
     def _quantize_all(self, eng: BlockEngine, layers: Mapping[str, _Layer]) -> None:
@@ -279,7 +315,7 @@ class QuantizationRunner:
                                 bits=layer.scheme.bits, group_size=layer.scheme.group_size,
                                 mode=layer.mode, eps=self.eps, wq_out=eng.wq[p.operand],
                                 row_block=p.row_block, row_stride=p.row_stride,
-                                row_offset=p.row_offset)
+                                row_offset=p.row_offset, init_scale=layer.init_scale)
 
     def _step_all(self, eng: BlockEngine, layers: Mapping[str, _Layer], rates: Mapping[str, float],
                   step: int) -> None:
@@ -292,7 +328,7 @@ class QuantizationRunner:
                              bits=layer.scheme.bits, group_size=layer.scheme.group_size,
                              mode=layer.mode, eps=self.eps, lr=lr, coef_lo=lo, coef_hi=hi,
                              v_bound=V_BOUND, row_block=p.row_block, row_stride=p.row_stride,
-                             row_offset=p.row_offset)
+                             row_offset=p.row_offset, init_scale=layer.init_scale)
 
     def _scores(self, eng, layers, inputs, targets, over, suppress, scratch) -> float:
         """Mean loss over batches ``over`` with the current parameters."""

@@ -1,0 +1,105 @@
+"""Command line: ``python -m mround_amd quantize MODEL -o OUT ...`` (the
+``mround quantize`` subcommand of mround/cli/main.py:66-200, for local
+checkpoints), and ``random-model`` to write a random-initialised checkpoint
+of a named geometry."""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+GEOMETRIES = {
+    # the benchmark configurations' model shapes
+    "smollm2-135m": dict(model_type="llama", hidden_size=576, num_attention_heads=9, num_key_value_heads=3,
+                         head_dim=64, intermediate_size=1536, rms_norm_eps=1e-5, rope_theta=10000.0,
+                         num_hidden_layers=30, vocab_size=49152, tie_word_embeddings=True),
+    "qwen2.5-0.5b": dict(model_type="qwen2", hidden_size=896, num_attention_heads=14, num_key_value_heads=2,
+                         intermediate_size=4864, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=24,
+                         vocab_size=151936, tie_word_embeddings=True),
+    "qwen2.5-3b": dict(model_type="qwen2", hidden_size=2048, num_attention_heads=16, num_key_value_heads=2,
+                       intermediate_size=11008, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=36,
+                       vocab_size=151936, tie_word_embeddings=True),
+    "qwen2.5-7b": dict(model_type="qwen2", hidden_size=3584, num_attention_heads=28, num_key_value_heads=4,
+                       intermediate_size=18944, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=28,
+                       vocab_size=152064, tie_word_embeddings=False),
+}
+
+
+def _parser() -> argparse.ArgumentParser:
+    p = argparse.ArgumentParser(prog="mround_amd", description="SignRound v2 quantization on MI355X")
+    sub = p.add_subparsers(dest="command", required=True)
+    q = sub.add_parser("quantize", help="quantize a local checkpoint into an MLX checkpoint")
+    q.add_argument("model", help="local checkpoint directory (config.json + *.safetensors)")
+    q.add_argument("-o", "--output-dir", required=True)
+    q.add_argument("-b", "--bits", type=int, default=4)
+    q.add_argument("-g", "--group-size", type=int, default=64)
+    q.add_argument("--asym", action="store_true", help="asymmetric codes with a zero point")
+    q.add_argument("--average-bits", type=float, default=None)
+    q.add_argument("--plan", default=None, help="JSON file mapping layer paths to widths")
+    q.add_argument("--format", default="mlx")
+    q.add_argument("--iters", type=int, default=None)
+    q.add_argument("--samples", type=int, default=None)
+    q.add_argument("--seq-len", type=int, default=None)
+    q.add_argument("--batch-size", type=int, default=None)
+    q.add_argument("--lr", type=float, default=None)
+    q.add_argument("--calibration", default="random")
+    q.add_argument("--seed", type=int, default=None)
+    q.add_argument("--allow-dense", action="store_true", help="leave embedding/head dense")
+    r = sub.add_parser("random-model", help="write a random-initialised checkpoint")
+    r.add_argument("geometry", choices=sorted(GEOMETRIES))
+    r.add_argument("output_dir")
+    r.add_argument("--layers", type=int, default=None, help="override the layer count")
+    r.add_argument("--seed", type=int, default=0)
+    r.add_argument("--device", default="cuda")
+    return p
+
+
+def _tuning(args):
+    from mround_amd.schemes import TuningConfig
+
+    kw = {}
+    for field, val in (("iters", args.iters), ("n_samples", args.samples), ("seq_len", args.seq_len),
+                       ("batch_size", args.batch_size), ("lr", args.lr)):
+        if val is not None:
+            kw[field] = val
+    return TuningConfig(**kw)
+
+
+def main(argv=None) -> int:
+    args = _parser().parse_args(argv)
+    from mround_amd.exceptions import MRoundError
+
+    try:
+        if args.command == "random-model":
+            from mround_amd.pipeline.checkpoint import write_random_checkpoint
+
+            cfg = dict(GEOMETRIES[args.geometry])
+            if args.layers is not None:
+                cfg["num_hidden_layers"] = args.layers
+            path = write_random_checkpoint(args.output_dir, cfg, seed=args.seed, device=args.device)
+            print(f"wrote {path}")
+            return 0
+        from mround_amd import api
+        from mround_amd.schemes import Symmetry
+
+        plan = None
+        if args.plan:
+            with open(args.plan) as f:
+                plan = {k: int(v) for k, v in json.load(f).items()}
+        result = api.quantize(args.model, output_dir=args.output_dir, bits=args.bits,
+                              group_size=args.group_size,
+                              symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
+                              average_bits=args.average_bits, plan=plan, tuning=_tuning(args),
+                              calibration=args.calibration, export_format=args.format,
+                              dense_remainder=args.allow_dense, seed=args.seed,
+                              progress=lambda b: print(f"  block {b.index}: loss {b.initial_loss:.4g} -> "
+                                                       f"{b.final_loss:.4g} in {b.seconds:.2f} s", flush=True))
+    except (MRoundError, ValueError) as exc:
+        print(f"mround: {exc}", file=sys.stderr)
+        return 1
+    print(f"  {result.describe()}")
+    for path, reason in result.skipped:
+        print(f"  left dense  {path}: {reason}")
+    print(f"  wrote {result.output_dir}")
+    return 0

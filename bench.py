@@ -42,6 +42,9 @@ SHAPE_7B = dict(hidden=3584, n_heads=28, n_kv_heads=4, head_dim=128, intermediat
 VOCAB = 152064
 BITS, GROUP = 2, 64
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# The reference's published seconds per 7B 2-bit block tune: Apple M5 MacBook
+# Pro, MLX, symmetric with searched scale, 4 micro-batches (ledger row 130).
+REFERENCE_SEC_PER_BLOCK = 2119.5
 HBM_PEAK_GBPS = 8000.0
 
 # fake-quant microbench matrix (a 7B gate/up projection)
@@ -63,15 +66,22 @@ def block_workload(torch, dev, *, n_samples, seq_len, batch):
     return shape, weights, entrance
 
 
-def time_block_tune(torch, dev, args):
+def time_block_tune(torch, dev, args, *, workload=None, symmetric=False, steps=None, warmup=None,
+                    instrument=True):
     from mround_amd.pipeline.block import BlockWeights
     from mround_amd.pipeline.runner import DecoderBlock, QuantizationRunner
-    from mround_amd.schemes import QuantScheme, Symmetry, TuningConfig
+    from mround_amd.schemes import QuantScheme, ScaleInit, Symmetry, TuningConfig
 
-    shape, weights, entrance = block_workload(torch, dev, n_samples=args.samples, seq_len=args.seq_len,
-                                              batch=args.batch)
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    shape, weights, entrance = workload or block_workload(torch, dev, n_samples=args.samples,
+                                                          seq_len=args.seq_len, batch=args.batch)
     originals = dict(weights.linears)
-    scheme = QuantScheme(bits=BITS, group_size=GROUP, symmetry=Symmetry.ASYMMETRIC)
+    if symmetric:
+        scheme = QuantScheme(bits=BITS, group_size=GROUP, symmetry=Symmetry.SYMMETRIC,
+                             scale_init=ScaleInit.SEARCHED)
+    else:
+        scheme = QuantScheme(bits=BITS, group_size=GROUP, symmetry=Symmetry.ASYMMETRIC)
     tuning = TuningConfig(iters=args.iters, batch_size=args.batch, n_samples=args.samples,
                           seq_len=args.seq_len)
     runner = QuantizationRunner(scheme, tuning)
@@ -89,19 +99,21 @@ def time_block_tune(torch, dev, args):
         torch.cuda.synchronize(dev)
         return time.perf_counter() - t0, summary.blocks[0]
 
-    for i in range(args.warmup):
-        print(f"bench: warm-up block tune {i + 1}/{args.warmup}", file=sys.stderr, flush=True)
+    tag = "sym searched" if symmetric else "asym"
+    for i in range(warmup):
+        print(f"bench: warm-up block tune ({tag}) {i + 1}/{warmup}", file=sys.stderr, flush=True)
         one()
     eng = runner.engine(shape, entrance[0].shape[0], dev)
     flops = eng.flops()
-    eng.time_launches(flops)
+    if instrument:
+        eng.time_launches(flops)
     times, results = [], []
-    for i in range(args.steps):
-        print(f"bench: timed block tune {i + 1}/{args.steps}", file=sys.stderr, flush=True)
+    for i in range(steps):
+        print(f"bench: timed block tune ({tag}) {i + 1}/{steps}", file=sys.stderr, flush=True)
         t, res = one()
         times.append(t)
         results.append(res)
-    per_launch = eng.launch_ms()
+    per_launch = eng.launch_ms() if instrument else {}
     eng.timers = None
     kernels = {}
     for name, ms in per_launch.items():
@@ -114,7 +126,7 @@ def time_block_tune(torch, dev, args):
     return {
         "shape": shape, "times": times, "results": results, "kernels": kernels, "flops": flops,
         "kernel_ms_total": gemm_ms, "tokens_per_batch": entrance[0].shape[0],
-        "batches": len(entrance),
+        "batches": len(entrance), "workload": (shape, weights, entrance),
     }
 
 
@@ -333,6 +345,8 @@ def main(argv=None):
                     help="fraction of each layer's rows in the CPU fake-quant sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-microbench", action="store_true")
+    ap.add_argument("--no-like-for-like", action="store_true",
+                    help="skip the extra symmetric searched-scale tune")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch the fake-quant forward and a copy of known size (counter runs)")
     args = ap.parse_args(argv)
@@ -363,6 +377,19 @@ def main(argv=None):
     dk = kernels[dominant]
     res = tune["results"][-1]
     traffic = _measured_traffic()
+    like = None
+    if not args.no_like_for_like:
+        # the reference's measured scheme: symmetric codes, searched scale
+        sym = time_block_tune(torch, dev, args, workload=tune["workload"], symmetric=True, steps=1,
+                              warmup=0, instrument=False)
+        sr = sym["results"][-1]
+        like = {"scheme": f"{BITS}-bit symmetric, searched scale, gs{GROUP}", "value": round(sym["times"][0], 3),
+                "unit": "s", "search_s": round(sr.search_seconds, 3),
+                "loss": {"initial": sr.initial_loss, "final": sr.final_loss, "reverted": sr.reverted},
+                "reference_published_s": REFERENCE_SEC_PER_BLOCK,
+                "reference_setting": "Apple M5 MacBook Pro 32 GB, MLX 0.32, same scheme, 4 micro-batches",
+                "speedup_vs_reference": round(REFERENCE_SEC_PER_BLOCK / sym["times"][0], 1)}
+    del tune["workload"]
     fq = None
     if not args.no_microbench:
         print("bench: fake-quant microbench", file=sys.stderr, flush=True)
@@ -383,7 +410,10 @@ def main(argv=None):
         "ms_per_step": round(sec * 1e3, 1),
         "higher_is_better": False,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": round(sec / REFERENCE_SEC_PER_BLOCK, 6),
+        "vs_baseline_note": ("value / 2119.5 s, the reference's published 7B 2-bit block tune (M5 MacBook "
+                             "Pro, symmetric searched scale; lower is faster); like_for_like holds the "
+                             "same scheme measured here"),
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
@@ -414,6 +444,7 @@ def main(argv=None):
             "flops_per_launch": tune["flops"][dominant],
             "avg_launch_ms": dk["avg_ms"],
         },
+        "like_for_like": like,
         "kernels": kernels,
         "fake_quant": fq,
         "cpu_baseline": cpu,

@@ -39,10 +39,23 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 
 // ---- LDS tiles --------------------------------------------------------------
 // Row-major tile of ROWS rows x D bf16 (K-major for the MFMA: row = m or n,
-// D = reduction), 16-byte chunk c of row r at position c ^ (r & 7).
+// D = reduction), 16-byte chunk c of row r at position c ^ swz_bits(r).
+// The XOR applied to a row's 16-byte chunk index. An LDS cycle serves 16
+// lanes of a 16-byte read or 32 lanes of an 8-byte read (256 bytes, all 64
+// banks): the row operand reads take 16 consecutive rows at one chunk, the
+// transposing reads 4 consecutive rows (from a multiple of 4) at 4
+// consecutive chunks. D = 128 (a row spans all banks): a 4-bit rotation of
+// the row, so 16 rows are 16 positions and rows r0..r0+3 differ in the two
+// high bits. D = 64 (two rows per bank cycle, split by parity): a 3-bit
+// rotation of r / 2 with the same two properties within each half.
+template <int D>
+__device__ __forceinline__ int swz_bits(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+}
 template <int D>
 __device__ __forceinline__ int rowtile_off(int r, int c) {
-  return r * (D * 2) + ((c ^ (r & 7)) << 4);
+  return r * (D * 2) + ((c ^ swz_bits<D>(r)) << 4);
 }
 template <int D>
 __device__ __forceinline__ bf16x8 frag_row(const uint8_t* lds, int r, int s, int h) {
@@ -57,7 +70,7 @@ typedef __attribute__((address_space(1))) void gbl_void_t;
 // 64 rows x D bf16 of a [*, ld] matrix (rows r0.., columns col..) into a
 // rowtile by direct-to-LDS loads (16 B per lane, no registers). One wave
 // instruction fills 1 KB = 64 / (D / 8) rows; lane l covers row l / (D / 8)
-// of it at physical chunk l % (D / 8), i.e. logical chunk (l % (D/8)) ^ (row & 7).
+// of it at physical chunk l % (D / 8), i.e. logical chunk (l % (D/8)) ^ swz_bits(row).
 template <int D>
 __device__ __forceinline__ void dma_rowtile(const uint16_t* src, int64_t ld, int64_t r0, int col,
                                             uint8_t* lds) {
@@ -70,7 +83,7 @@ __device__ __forceinline__ void dma_rowtile(const uint16_t* src, int64_t ld, int
   for (int i = 0; i < INSTR; ++i) {
     const int rb = (i * 4 + wave) * RPI;
     const int row = rb + sub;
-    const int c = pchunk ^ (row & 7);
+    const int c = pchunk ^ swz_bits<D>(row);
     const uint16_t* g = src + (r0 + row) * ld + col + c * 8;
     __builtin_amdgcn_global_load_lds((const gbl_void_t*)g, (lds_void_t*)(lds + rb * (2 * D)), 16, 0, 0);
   }
@@ -92,9 +105,9 @@ __device__ __forceinline__ bf16x8 frag_tr(const uint8_t* lds, int cb, int s, int
   const int row1 = row0 + 8;
   const __attribute__((address_space(3))) uint8_t* base = (const __attribute__((address_space(3))) uint8_t*)lds;
   const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16_t*)(base + row0 * (2 * D) + ((c ^ (row0 & 7)) << 4) + byte));
+      (lds_v4i16_t*)(base + rowtile_off<D>(row0, c) + byte));
   const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16_t*)(base + row1 * (2 * D) + ((c ^ (row1 & 7)) << 4) + byte));
+      (lds_v4i16_t*)(base + rowtile_off<D>(row1, c) + byte));
   typedef short v8i16 __attribute__((ext_vector_type(8)));
   const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, v);

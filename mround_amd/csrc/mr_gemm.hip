@@ -9,8 +9,8 @@
 //   input    dX = dY W     A = dY (K-major)  B = W  (MN-major)
 //   weight   dW = dY^T X   A = dY (MN-major) B = X  (MN-major)
 //
-// Tiling: a block of 256 threads (4 waves of 64, 2 x 2) owns a BM x BN tile
-// of C; each wave owns (BM/2) x (BN/2) as a grid of 32 x 32 accumulators fed by
+// Tiling: a block of 512 threads (8 waves of 64, 4 x 2) owns a BM x BN tile
+// of C; each wave owns (BM/4) x (BN/2) as a grid of 32 x 32 accumulators fed by
 // v_mfma_f32_32x32x16_bf16 (lane l: A row l%32, B column l%32, k half l/32;
 // accumulator register r: row (r/4)*8 + (l/32)*4 + r%4, column l%32). Every
 // operand tile moves HBM -> LDS by direct loads (global_load_lds, no
@@ -33,13 +33,18 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;
+// 8 waves (two per SIMD) in a 4 x 2 grid: a 256 x 256 tile gives each wave
+// 64 x 128 (128 accumulator registers), which leaves room for double-buffered
+// operands and lets the two waves of a SIMD hide each other's LDS and
+// barrier waits. A wave's columns start on a multiple of 64, which the SwiGLU
+// epilogue's gate/up pairing needs.
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kWaveRows = 4;  // waves along M
 constexpr int BK = 64;
 // LDS tiles are K-major rows of 64 bf16 (128 bytes, 8 chunks of 16 bytes)
-// with no padding; chunk c of row r is stored at position c ^ (r & 7). Eight
-// consecutive rows read at one k chunk (the MFMA operand reads of 8 lanes)
-// then cover 8 distinct positions, i.e. all 32 banks once, and the 8 chunks
-// of one row written together are a permutation of the row: no conflicts.
+// with no padding; chunk c of row r is stored at position c ^ ((r >> 1) & 7)
+// (swz below), so the 16 rows one LDS cycle serves cover all 64 banks once.
 constexpr int ROW_BYTES = BK * 2;
 
 enum Epi : int {
@@ -70,27 +75,32 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
 
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * ROW_BYTES + ((chunk ^ (row & 7)) << 4); }
+// 16 lanes are served per LDS cycle: their 16 rows must cover the 64 banks.
+// A row is 128 bytes (half the banks), so even and odd rows take the two
+// halves and (row >> 1) & 7 spreads the 8 rows of each half over its 8
+// 16-byte positions.
+__device__ __forceinline__ int swz_bits(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * ROW_BYTES + ((chunk ^ swz_bits(row)) << 4); }
 
 // ---- K-major operand: global -> LDS directly (global_load_lds, 16 B/lane) --
 //
 // One wave instruction moves 64 chunks = 8 rows; lane l covers row 8q + l/8
-// and LDS position l % 8, i.e. global chunk (l % 8) ^ (l / 8). Rows past the
+// and LDS position l % 8, i.e. global chunk (l % 8) ^ swz_bits(row). Rows past the
 // valid range are clamped to the last valid row: they only feed accumulator
 // rows or columns that are never stored.
 template <int ROWS>
 struct KMajorDirect {
-  static constexpr int INSTR = ROWS * 8 / 64 / 4;  // instructions per wave
+  static constexpr int INSTR = ROWS * 8 / 64 / kWaves;  // instructions per wave
   __device__ __forceinline__ static void issue(const uint16_t* base, int64_t ld, int row0,
                                                int rows_valid, int k0, uint8_t* lds) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int sub = lane >> 3;
-    const int chunk = (lane & 7) ^ sub;
 #pragma unroll
     for (int i = 0; i < INSTR; ++i) {
-      const int q = i * 4 + wave;
+      const int q = i * kWaves + wave;
       const int row = q * 8 + sub;
+      const int chunk = (lane & 7) ^ swz_bits(row);
       const int g = min(row0 + row, rows_valid - 1);
       const uint16_t* src = base + static_cast<int64_t>(g) * ld + k0 + chunk * 8;
       __builtin_amdgcn_global_load_lds((const gbl_void_t*)src,
@@ -117,7 +127,7 @@ template <int ROWS>
 struct MNMajorDirect {
   static constexpr int CPR = ROWS / 8;         // 16-byte chunks per k-row
   static constexpr int RPI = 64 / CPR;         // k-rows per wave instruction
-  static constexpr int INSTR = BK / RPI / 4;   // instructions per wave
+  static constexpr int INSTR = BK / RPI / kWaves;   // instructions per wave
   static constexpr int ROWB = ROWS * 2;        // bytes per k-row
   __device__ __forceinline__ static void issue(const uint16_t* base, int64_t ld, int row0,
                                                int rows_valid, int k0, uint8_t* lds) {
@@ -126,7 +136,7 @@ struct MNMajorDirect {
     const int sub = lane / CPR, pchunk = lane % CPR;
 #pragma unroll
     for (int i = 0; i < INSTR; ++i) {
-      const int kb = (i * 4 + wave) * RPI;
+      const int kb = (i * kWaves + wave) * RPI;
       const int kr = kb + sub;
       const int c = pchunk ^ (4 * (kr & 3));
       // columns past the valid range read the last valid chunk; they only feed
@@ -175,7 +185,7 @@ struct StaticFor {
 
 template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / kWaveRows, WN = BN / (kWaves / kWaveRows);
   constexpr int TM = WM / 32, TN = WN / 32;
   // Two LDS stages as four distinct arrays, indexed only with compile-time
   // stage numbers (the k loop below is unrolled by two), so that the waits
@@ -202,7 +212,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (kWaves / kWaveRows), wn = wave % (kWaves / kWaveRows);
 
   // Global loads of tile kt, straight into the given LDS stage.
   auto issue_loads = [&](int kt, uint8_t* as_dst, uint8_t* bs_dst) {
@@ -221,41 +231,48 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 
   // MFMAs over one LDS stage, with the operands of the next k16 step read
   // while the current step's MFMAs run.
+  // Every k step, fragment slot and accumulator is visited with compile-time
+  // indices (StaticFor): left to the loop unroller, a body this large can
+  // stay rolled, and a runtime index would move acc and the fragments to
+  // scratch memory.
   auto compute = [&](const uint8_t* as, const uint8_t* bs) {
     bf16x8 af[2][TM], bfr[2][TN];
-    auto read_frags = [&](int kk, int slot) {
+    auto read_frags = [&](auto kkc, auto slotc) {
+      constexpr int kk = decltype(kkc)::value, slot = decltype(slotc)::value;
       const int chunk = kk * 2 + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
+      auto ra = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
         if constexpr (A_KMAJOR) {
           const int row = wm * WM + i * 32 + (lane & 31);
           af[slot][i] = *reinterpret_cast<const bf16x8*>(as + swz(row, chunk));
         } else {
           af[slot][i] = MNMajorDirect<BM>::frag(as, wm * WM + i * 32, kk, lane);
         }
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
+      };
+      auto rb = [&](auto jc) {
+        constexpr int j = decltype(jc)::value;
         if constexpr (B_KMAJOR) {
           const int row = wn * WN + j * 32 + (lane & 31);
           bfr[slot][j] = *reinterpret_cast<const bf16x8*>(bs + swz(row, chunk));
         } else {
           bfr[slot][j] = MNMajorDirect<BN>::frag(bs, wn * WN + j * 32, kk, lane);
         }
-      }
+      };
+      StaticFor<0, TM>::run(ra);
+      StaticFor<0, TN>::run(rb);
     };
-    read_frags(0, 0);
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int cur = kk & 1;
-      if (kk + 1 < BK / 16) read_frags(kk + 1, cur ^ 1);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0,
-                                                              0, 0);
-    }
+    read_frags(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    auto kstep = [&](auto kkc) {
+      constexpr int kk = decltype(kkc)::value, cur = kk & 1;
+      if constexpr (kk + 1 < BK / 16)
+        read_frags(std::integral_constant<int, kk + 1>{}, std::integral_constant<int, cur ^ 1>{});
+      auto mm = [&](auto ijc) {
+        constexpr int i = decltype(ijc)::value / TN, j = decltype(ijc)::value % TN;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
+      };
+      StaticFor<0, TM * TN>::run(mm);
+    };
+    StaticFor<0, BK / 16>::run(kstep);
   };
 
   // One pipeline step: compute on stage (cur_a, cur_b) while tile kt + 1
@@ -263,6 +280,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   auto step = [&](int kt, int KT, const uint8_t* cur_a, const uint8_t* cur_b, uint8_t* nxt_a,
                   uint8_t* nxt_b) {
     if (kt + 1 < KT) issue_loads(kt + 1, nxt_a, nxt_b);
+    // Keep the loads of the next tile ahead of this tile's MFMAs: left to
+    // itself the scheduler sinks them to the end of the step, right in front
+    // of the wait for them, and the whole memory latency is exposed.
+    __builtin_amdgcn_sched_barrier(0);
     compute(cur_a, cur_b);
     // The direct loads of the next tile and every read of this one are done
     // before any wave moves on.

@@ -172,8 +172,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd(const uint16_t* __restrict_
   __shared__ __attribute__((aligned(1024))) uint8_t V0[BUF];
   __shared__ __attribute__((aligned(1024))) uint8_t K1[BUF];
   __shared__ __attribute__((aligned(1024))) uint8_t V1[BUF];
-  const int qb = gridDim.x - 1 - blockIdx.x;  // the longest blocks start first
-  const int hq = blockIdx.y, b = blockIdx.z;
+  const int qb = gridDim.z - 1 - blockIdx.z;  // the longest blocks start first
+  const int hq = blockIdx.x, b = blockIdx.y;
   const int g = hq / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
   const int q0 = qb * (4 * QW) + wave * QW;
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
   __shared__ __attribute__((aligned(1024))) uint8_t O1[TILE];
   __shared__ float LD0[128];  // lse (log2 domain) then rowsum(dO O) of the tile's 64 queries
   __shared__ float LD1[128];
-  const int kb = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int kb = blockIdx.z, g = blockIdx.x, b = blockIdx.y;
   const int G = Hq / Hkv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
   const int k0w = kb * QB + wave * 32;
@@ -476,8 +476,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq(
   __shared__ __attribute__((aligned(1024))) uint8_t V0[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t K1[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t V1[TILE];
-  const int qb = gridDim.x - 1 - blockIdx.x;  // the longest blocks start first
-  const int hq = blockIdx.y, b = blockIdx.z;
+  const int qb = gridDim.z - 1 - blockIdx.z;  // the longest blocks start first
+  const int hq = blockIdx.x, b = blockIdx.y;
   const int g = hq / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
   const int q0 = qb * QB + wave * 32;
@@ -550,14 +550,18 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq(
   store_qrows<D>(dq, scale, stage, dqkv + hq * D, ld, tok0 + q0);
 }
 
+// Grids put the query (or key) block index in z, the slowest dimension:
+// workgroups go to the 8 XCDs round-robin by linear id, so heads x batches
+// (x, y) spread each causal length class evenly over the XCDs, and z in
+// decreasing work order starts the longest blocks first.
 template <int D>
 int launch_fwd(const uint16_t* qkv, int64_t ld, int B, int S, int Hq, int Hkv, float scale,
                uint16_t* out, int64_t ldo, float* lse, hipStream_t s) {
   if (S % 256 == 0)
-    hipLaunchKernelGGL((attn_fwd<D, 64>), dim3(S / 256, Hq, B), dim3(kThreads), 0, s, qkv, ld, S, Hq,
+    hipLaunchKernelGGL((attn_fwd<D, 64>), dim3(Hq, B, S / 256), dim3(kThreads), 0, s, qkv, ld, S, Hq,
                        Hkv, scale * kLog2e, out, ldo, lse);
   else
-    hipLaunchKernelGGL((attn_fwd<D, 32>), dim3(S / 128, Hq, B), dim3(kThreads), 0, s, qkv, ld, S, Hq,
+    hipLaunchKernelGGL((attn_fwd<D, 32>), dim3(Hq, B, S / 128), dim3(kThreads), 0, s, qkv, ld, S, Hq,
                        Hkv, scale * kLog2e, out, ldo, lse);
   MR_LAUNCH_CHECK("mr_attn_fwd");
   return MR_OK;
@@ -571,9 +575,9 @@ int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint1
   const int64_t waves = T * Hq;
   hipLaunchKernelGGL(attn_bwd_dot<D>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(kThreads), 0,
                      s, dout, out, ldo, T, S, Hq, dsum);
-  hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(S / QB, Hkv, B), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
+  hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
                      lse, dsum, S, Hq, Hkv, scale, dqkv);
-  hipLaunchKernelGGL(attn_bwd_dq<D>, dim3(S / QB, Hq, B), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
+  hipLaunchKernelGGL(attn_bwd_dq<D>, dim3(Hq, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
                      lse, dsum, S, Hq, Hkv, scale, dqkv);
   MR_LAUNCH_CHECK("mr_attn_bwd");
   return MR_OK;

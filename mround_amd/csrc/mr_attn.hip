@@ -71,17 +71,18 @@ typedef __attribute__((address_space(1))) void gbl_void_t;
 // rowtile by direct-to-LDS loads (16 B per lane, no registers). One wave
 // instruction fills 1 KB = 64 / (D / 8) rows; lane l covers row l / (D / 8)
 // of it at physical chunk l % (D / 8), i.e. logical chunk (l % (D/8)) ^ swz_bits(row).
-template <int D>
+template <int D, int NW = 4>
 __device__ __forceinline__ void dma_rowtile(const uint16_t* src, int64_t ld, int64_t r0, int col,
                                             uint8_t* lds) {
   constexpr int CPR = D / 8;
   constexpr int RPI = 64 / CPR;
-  constexpr int INSTR = 64 / RPI / 4;
+  constexpr int INSTR = 64 / RPI / NW;
+  static_assert(INSTR * RPI * NW == 64, "the waves must split the tile evenly");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / CPR, pchunk = lane % CPR;
 #pragma unroll
   for (int i = 0; i < INSTR; ++i) {
-    const int rb = (i * 4 + wave) * RPI;
+    const int rb = (i * NW + wave) * RPI;
     const int row = rb + sub;
     const int c = pchunk ^ swz_bits<D>(row);
     const uint16_t* g = src + (r0 + row) * ld + col + c * 8;
@@ -154,123 +155,131 @@ __device__ __forceinline__ void store_qrows(const f32x16 (&acc)[D / 32], float m
 
 // ---- forward ----------------------------------------------------------------
 //
-// A block owns 4 * QW queries of one query head (QW per wave, 32 per MFMA
-// column tile) and walks the key tiles up to its last query. K and V tiles
-// move HBM -> LDS by direct loads, double buffered: tile t + 1 is in flight
-// while tile t is computed, with one barrier per tile. V stays row-major in
-// LDS; its transposed operand comes from the transposing LDS read.
-template <int D, int QW>
-__global__ __launch_bounds__(kThreads) void attn_fwd(const uint16_t* __restrict__ qkv, int64_t ld,
-                                                     int S, int Hq, int Hkv, float scale_log2,
-                                                     uint16_t* __restrict__ out, int64_t ldo,
-                                                     float* __restrict__ lse) {
-  constexpr int NQ = QW / 32, NS = D / 16, ND = D / 32;
+// A block of W waves owns 32 W queries of one query head (32 per wave, one
+// MFMA column tile) and walks the key tiles up to its last query. K and V
+// tiles move HBM -> LDS by direct loads, double buffered: tile t + 1 is in
+// flight while tile t is computed, with one barrier per tile. V stays
+// row-major in LDS; its transposed operand comes from the transposing read.
+// A wave holds Q (D / 4 registers), O^T (D / 2) and one 64-key score tile
+// (32), so two waves share each SIMD and one wave's softmax overlaps the
+// other's MFMAs.
+//
+// The running row maximum m is raised only when a tile's maximum exceeds it
+// by more than kRaise (log2 units) in some lane of the wave; until then the
+// probabilities exp2(s - m) stay below 2^kRaise, far inside fp32 and bf16
+// range. Output and log-sum-exp are relative to the same m, so the result is
+// the exact softmax up to rounding; most tiles skip the O rescale.
+constexpr float kRaise = 8.0f;
+
+// Cross-half reductions: v_permlane32_swap exchanges the two 32-lane halves,
+// leaving lane l's value and lane l ^ 32's in the two results.
+__device__ __forceinline__ float xhalf_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_fwd(const uint16_t* __restrict__ qkv, int64_t ld,
+                                                   int S, int Hq, int Hkv, float scale_log2,
+                                                   uint16_t* __restrict__ out, int64_t ldo,
+                                                   float* __restrict__ lse) {
+  constexpr int NS = D / 16, ND = D / 32;
   constexpr int TILE = KT * D * 2;
   constexpr int STAGE_ROW = 2 * D + 8;  // staged output row (bytes), 8-byte aligned
-  constexpr int BUF = TILE > QW * STAGE_ROW ? TILE : QW * STAGE_ROW;
-  __shared__ __attribute__((aligned(1024))) uint8_t K0[BUF];
-  __shared__ __attribute__((aligned(1024))) uint8_t V0[BUF];
-  __shared__ __attribute__((aligned(1024))) uint8_t K1[BUF];
-  __shared__ __attribute__((aligned(1024))) uint8_t V1[BUF];
+  constexpr int SMEM = 4 * TILE > W * 32 * STAGE_ROW ? 4 * TILE : W * 32 * STAGE_ROW;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+  uint8_t* const K0 = smem;
+  uint8_t* const V0 = smem + TILE;
+  uint8_t* const K1 = smem + 2 * TILE;
+  uint8_t* const V1 = smem + 3 * TILE;
   const int qb = gridDim.z - 1 - blockIdx.z;  // the longest blocks start first
   const int hq = blockIdx.x, b = blockIdx.y;
   const int g = hq / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
-  const int q0 = qb * (4 * QW) + wave * QW;
+  const int q0 = qb * (32 * W) + wave * 32;
+  const int qi = q0 + l32;
   const int64_t tok0 = static_cast<int64_t>(b) * S;
   const int kcol = (Hq + g) * D, vcol = (Hq + Hkv + g) * D;
-  const int n_tiles = (qb + 1) * (4 * QW) / KT;
+  const int n_tiles = (qb + 1) * (32 * W) / KT;
 
-  dma_rowtile<D>(qkv, ld, tok0, kcol, K0);
-  dma_rowtile<D>(qkv, ld, tok0, vcol, V0);
+  dma_rowtile<D, W>(qkv, ld, tok0, kcol, K0);
+  dma_rowtile<D, W>(qkv, ld, tok0, vcol, V0);
 
-  bf16x8 qf[NQ][NS];
+  bf16x8 qf[NS];
 #pragma unroll
-  for (int qt = 0; qt < NQ; ++qt)
+  for (int s = 0; s < NS; ++s)
+    qf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + qi) * ld + hq * D + s * 16 + h * 8);
+  f32x16 o[ND];
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-      qf[qt][s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + q0 + qt * 32 + l32) * ld + hq * D +
-                                                   s * 16 + h * 8);
-  f32x16 o[NQ][ND];
-  float m[NQ], l[NQ];
-#pragma unroll
-  for (int qt = 0; qt < NQ; ++qt) {
-    m[qt] = -INFINITY;
-    l[qt] = 0.0f;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt) o[qt][dt] = f32x16{};
-  }
+  for (int dt = 0; dt < ND; ++dt) o[dt] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
 
   auto step = [&](int t, const uint8_t* Kc, const uint8_t* Vc, uint8_t* Kn, uint8_t* Vn) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile t have landed
     __syncthreads();                // everyone's have, and nobody still reads the other buffers
     if (t + 1 < n_tiles) {
-      dma_rowtile<D>(qkv, ld, tok0 + (t + 1) * KT, kcol, Kn);
-      dma_rowtile<D>(qkv, ld, tok0 + (t + 1) * KT, vcol, Vn);
+      dma_rowtile<D, W>(qkv, ld, tok0 + (t + 1) * KT, kcol, Kn);
+      dma_rowtile<D, W>(qkv, ld, tok0 + (t + 1) * KT, vcol, Vn);
     }
     const int kv0 = t * KT;
-    if (kv0 > q0 + QW - 1) return;  // every key of the tile is after every query of the wave
-    const bool diag = kv0 + KT - 1 > q0;
+    if (kv0 > q0 + 31) return;  // every key of the tile is after every query of the wave
 
-    f32x16 st[2][NQ];
+    f32x16 st[2] = {f32x16{}, f32x16{}};
+    bf16x8 kfr[2][2];  // K fragments, step s + 1 read while step s multiplies
+    kfr[0][0] = frag_row<D>(Kc, l32, 0, h);
+    kfr[0][1] = frag_row<D>(Kc, 32 + l32, 0, h);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (s + 1 < NS) {
+        kfr[(s + 1) & 1][0] = frag_row<D>(Kc, l32, s + 1, h);
+        kfr[(s + 1) & 1][1] = frag_row<D>(Kc, 32 + l32, s + 1, h);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[s & 1][mt], qf[s], st[mt], 0, 0, 0);
+    }
+    if (kv0 + KT - 1 > q0) {  // the tile crosses the wave's diagonal
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kv0 + mt * 32 + acc_row(r, h) > qi) st[mt][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int qt = 0; qt < NQ; ++qt) st[mt][qt] = f32x16{};
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][r]);
+    const float mc = xhalf_max(mx) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(mc > m + kRaise)) {
+      const float m_new = fmaxf(m, mc);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      l *= alpha;
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const bf16x8 a = frag_row<D>(Kc, mt * 32 + l32, s, h);
-#pragma unroll
-        for (int qt = 0; qt < NQ; ++qt)
-          st[mt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qt][s], st[mt][qt], 0, 0, 0);
-      }
-#pragma unroll
-    for (int qt = 0; qt < NQ; ++qt) {
-      if (diag) {
-        const int qi = q0 + qt * 32 + l32;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (kv0 + mt * 32 + acc_row(r, h) > qi) st[mt][qt][r] = -INFINITY;
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[mt][qt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m[qt], mx * scale_log2);
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_new);
-      float ps = 0.0f;
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][qt][r], scale_log2, -m_new));
-          st[mt][qt][r] = p;
-          ps += p;
-        }
-      ps += __shfl_xor(ps, 32, 64);
-      l[qt] = l[qt] * alpha + ps;
-      m[qt] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) o[qt][dt] *= alpha;
+      for (int dt = 0; dt < ND; ++dt) o[dt] *= alpha;
+      m = m_new;
     }
+    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four short chains instead of one long one
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][r], scale_log2, -m));
+        st[mt][r] = pv;
+        ps[r & 3] += pv;
+      }
+    l += xhalf_sum((ps[0] + ps[1]) + (ps[2] + ps[3]));
 #pragma unroll
     for (int s = 0; s < KT / 16; ++s) {
-      bf16x8 pb[NQ];
+      const bf16x8 pb = cvt8(st[s >> 1], 8 * (s & 1));
 #pragma unroll
-      for (int qt = 0; qt < NQ; ++qt) pb[qt] = cvt8(st[s >> 1][qt], 8 * (s & 1));
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) {
-        const bf16x8 a = frag_tr<D>(Vc, dt * 32, s, lane);
-#pragma unroll
-        for (int qt = 0; qt < NQ; ++qt)
-          o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[qt], o[qt][dt], 0, 0, 0);
-      }
+      for (int dt = 0; dt < ND; ++dt)
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(Vc, dt * 32, s, lane), pb, o[dt],
+                                                        0, 0, 0);
     }
   };
 
@@ -282,34 +291,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd(const uint16_t* __restrict_
   if (t < n_tiles) step(t, K0, V0, K1, V1);
   __syncthreads();  // all tiles read; the buffers now stage the output
 
-  uint8_t* stage = wave == 0 ? K0 : wave == 1 ? V0 : wave == 2 ? K1 : V1;
-#pragma unroll
-  for (int qt = 0; qt < NQ; ++qt) {
-    const float inv = 1.0f / l[qt];
-    if (h == 0)
-      lse[(static_cast<int64_t>(b) * Hq + hq) * S + q0 + qt * 32 + l32] =
-          (m[qt] + log2f(l[qt])) * kLn2;
-    const int row = qt * 32 + l32;
-#pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const uint32_t w0 = pack_bf16(o[qt][dt][rg * 4 + 0] * inv, o[qt][dt][rg * 4 + 1] * inv);
-        const uint32_t w1 = pack_bf16(o[qt][dt][rg * 4 + 2] * inv, o[qt][dt][rg * 4 + 3] * inv);
-        const int col = dt * 32 + rg * 8 + h * 4;
-        *reinterpret_cast<uint2*>(stage + row * STAGE_ROW + col * 2) = make_uint2(w0, w1);
-      }
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  constexpr int CH = D / 8;
-  for (int c = lane; c < QW * CH; c += 64) {
-    const int row = c / CH, ch = c % CH;
-    const uint2 a = *reinterpret_cast<const uint2*>(stage + row * STAGE_ROW + ch * 16);
-    const uint2 bb = *reinterpret_cast<const uint2*>(stage + row * STAGE_ROW + ch * 16 + 8);
-    *reinterpret_cast<uint4*>(out + (tok0 + q0 + row) * ldo + hq * D + ch * 8) =
-        make_uint4(a.x, a.y, bb.x, bb.y);
-  }
+  if (h == 0) lse[(static_cast<int64_t>(b) * Hq + hq) * S + qi] = (m + log2f(l)) * kLn2;
+  store_qrows<D>(o, 1.0f / l, smem + wave * 32 * STAGE_ROW, out + hq * D, ldo, tok0 + q0);
 }
 
 // ---- backward ---------------------------------------------------------------
@@ -558,11 +541,11 @@ template <int D>
 int launch_fwd(const uint16_t* qkv, int64_t ld, int B, int S, int Hq, int Hkv, float scale,
                uint16_t* out, int64_t ldo, float* lse, hipStream_t s) {
   if (S % 256 == 0)
-    hipLaunchKernelGGL((attn_fwd<D, 64>), dim3(Hq, B, S / 256), dim3(kThreads), 0, s, qkv, ld, S, Hq,
-                       Hkv, scale * kLog2e, out, ldo, lse);
+    hipLaunchKernelGGL((attn_fwd<D, 8>), dim3(Hq, B, S / 256), dim3(512), 0, s, qkv, ld, S, Hq, Hkv,
+                       scale * kLog2e, out, ldo, lse);
   else
-    hipLaunchKernelGGL((attn_fwd<D, 32>), dim3(Hq, B, S / 128), dim3(kThreads), 0, s, qkv, ld, S, Hq,
-                       Hkv, scale * kLog2e, out, ldo, lse);
+    hipLaunchKernelGGL((attn_fwd<D, 4>), dim3(Hq, B, S / 128), dim3(256), 0, s, qkv, ld, S, Hq, Hkv,
+                       scale * kLog2e, out, ldo, lse);
   MR_LAUNCH_CHECK("mr_attn_fwd");
   return MR_OK;
 }

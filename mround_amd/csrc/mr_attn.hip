@@ -402,19 +402,18 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
         dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Oc, mq * 32 + l32, s, h), vf[s], dp,
                                                      0, 0, 0);
       }
-      f32x16 pr, dsr;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < 16; ++r) {  // P and dS overwrite S and dP in place
         const int qrow = mq * 32 + acc_row(r, h);
         float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale_log2, -LDc[qrow]));
         if (diag && kj > qt0 + qrow) p = 0.0f;
-        pr[r] = p;
-        dsr[r] = p * (dp[r] - LDc[64 + qrow]);
+        sacc[r] = p;
+        dp[r] = p * (dp[r] - LDc[64 + qrow]);
       }
 #pragma unroll
       for (int ss = 0; ss < 2; ++ss) {
-        const bf16x8 pa = cvt8(pr, 8 * ss);
-        const bf16x8 da = cvt8(dsr, 8 * ss);
+        const bf16x8 pa = cvt8(sacc, 8 * ss);
+        const bf16x8 da = cvt8(dp, 8 * ss);
 #pragma unroll
         for (int dt = 0; dt < ND; ++dt) {
           dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, frag_tr<D>(Oc, dt * 32, 2 * mq + ss, lane),
@@ -449,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
 // walks the key tiles up to its last query, K and V arriving by direct loads,
 // double buffered. dQ^T = K^T dS^T takes K^T from the transposing LDS read.
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dq(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void attn_bwd_dq(
     const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
     const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
     float scale, uint16_t* __restrict__ dqkv) {
@@ -494,31 +493,31 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq(
     const int kv0 = t * KT;
     if (kv0 > q0 + 31) return;
     const bool diag = kv0 + KT - 1 > q0;
-    f32x16 st[2] = {f32x16{}, f32x16{}}, dpt[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
+    for (int mt = 0; mt < 2; ++mt) {  // 32 keys at a time: S^T, dP^T, then their dQ share
+      if (kv0 + mt * 32 > q0 + 31) break;
+      f32x16 st = f32x16{}, dpt = f32x16{};
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Kc, mt * 32 + l32, s, h), qf[s],
-                                                         st[mt], 0, 0, 0);
-        dpt[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Vc, mt * 32 + l32, s, h), of[s],
-                                                          dpt[mt], 0, 0, 0);
+      for (int s = 0; s < NS; ++s) {
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Kc, mt * 32 + l32, s, h), qf[s], st,
+                                                     0, 0, 0);
+        dpt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Vc, mt * 32 + l32, s, h), of[s], dpt,
+                                                      0, 0, 0);
       }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][r], scale_log2, -lse2));
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], scale_log2, -lse2));
         if (diag && kv0 + mt * 32 + acc_row(r, h) > qi) p = 0.0f;
-        st[mt][r] = p * (dpt[mt][r] - dq_sum);  // dS^T
+        st[r] = p * (dpt[r] - dq_sum);  // dS^T
       }
 #pragma unroll
-    for (int s = 0; s < KT / 16; ++s) {
-      const bf16x8 db = cvt8(st[s >> 1], 8 * (s & 1));
+      for (int ss = 0; ss < 2; ++ss) {
+        const bf16x8 db = cvt8(st, 8 * ss);
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-        dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(Kc, dt * 32, s, lane), db, dq[dt],
-                                                         0, 0, 0);
+        for (int dt = 0; dt < ND; ++dt)
+          dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(Kc, dt * 32, 2 * mt + ss, lane), db,
+                                                           dq[dt], 0, 0, 0);
+      }
     }
   };
 

@@ -13,12 +13,15 @@
 // of C; each wave owns (BM/4) x (BN/2) as a grid of 32 x 32 accumulators fed by
 // v_mfma_f32_32x32x16_bf16 (lane l: A row l%32, B column l%32, k half l/32;
 // accumulator register r: row (r/4)*8 + (l/32)*4 + r%4, column l%32). Every
-// operand tile moves HBM -> LDS by direct loads (global_load_lds, no
-// registers) in the layout it has in memory: a K-major tile as rows of 64 k,
-// whose MFMA operand is one 16-byte LDS read; an MN-major tile as rows of one
-// k, whose operand comes from two transposing LDS reads (ds_read_b64_tr_b16).
-// The k loop is double-buffered in LDS with the next tile's loads in flight
-// during the current tile's MFMAs.
+// operand tile moves HBM -> LDS by direct buffer loads (buffer_load ... lds,
+// no registers) in the layout it has in memory: a K-major tile as rows of 64
+// k, whose MFMA operand is one 16-byte LDS read; an MN-major tile as rows of
+// one k, whose operand comes from two transposing LDS reads
+// (ds_read_b64_tr_b16). Each lane's load offsets are fixed for the whole k
+// loop (one 32-bit register per load); the k advance is in the scalar buffer
+// base. The k loop is double-buffered in LDS with the next tile's loads in
+// flight during the current tile's MFMAs, and within a tile the operands of
+// the next k16 step are read while the current step's MFMAs run.
 //
 // Blocks are renumbered so that each XCD (blocks are dealt to the 8 XCDs
 // round-robin) receives a contiguous run of tiles, grouped along M so that a
@@ -72,7 +75,6 @@ struct GemmParams {
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void gbl_void_t;
 
 
 // 16 lanes are served per LDS cycle: their 16 rows must cover the 64 banks.
@@ -80,7 +82,6 @@ typedef __attribute__((address_space(1))) void gbl_void_t;
 // halves and (row >> 1) & 7 spreads the 8 rows of each half over its 8
 // 16-byte positions.
 __device__ __forceinline__ int swz_bits(int row) { return (row >> 1) & 7; }
-__device__ __forceinline__ int swz(int row, int chunk) { return row * ROW_BYTES + ((chunk ^ swz_bits(row)) << 4); }
 
 // ---- K-major operand: global -> LDS directly (global_load_lds, 16 B/lane) --
 //
@@ -88,11 +89,29 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * ROW_BYTES 
 // and LDS position l % 8, i.e. global chunk (l % 8) ^ swz_bits(row). Rows past the
 // valid range are clamped to the last valid row: they only feed accumulator
 // rows or columns that are never stored.
+// Buffer resource over `bytes` bytes from `base`. Every offset the loads use
+// is already clamped inside the operand (see the loaders), so the resource
+// bound is only a second fence.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcFlags = 0x00020000;  // raw 32-bit dwords, no swizzle
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           kRsrcFlags);
+}
+
+// 16 bytes per lane from the buffer into LDS at lds + 16 * lane. (Kept out of
+// the templates: the host pass of hipcc drops the launch stubs of kernels
+// whose templates call this builtin directly.)
+__device__ __forceinline__ void load_lds16(rsrc_t r, uint8_t* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, 0, 0, 0);
+}
+
 template <int ROWS>
 struct KMajorDirect {
   static constexpr int INSTR = ROWS * 8 / 64 / kWaves;  // instructions per wave
-  __device__ __forceinline__ static void issue(const uint16_t* base, int64_t ld, int row0,
-                                               int rows_valid, int k0, uint8_t* lds) {
+  int voff[INSTR];
+  __device__ __forceinline__ void init(int64_t ld, int row0, int rows_valid) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int sub = lane >> 3;
@@ -102,9 +121,18 @@ struct KMajorDirect {
       const int row = q * 8 + sub;
       const int chunk = (lane & 7) ^ swz_bits(row);
       const int g = min(row0 + row, rows_valid - 1);
-      const uint16_t* src = base + static_cast<int64_t>(g) * ld + k0 + chunk * 8;
-      __builtin_amdgcn_global_load_lds((const gbl_void_t*)src,
-                                       (lds_void_t*)(lds + q * 8 * ROW_BYTES), 16, 0, 0);
+      voff[i] = static_cast<int>(((g - row0) * ld + chunk * 8) * 2);
+    }
+  }
+  __device__ __forceinline__ void issue(const uint16_t* base, int64_t ld, int row0, int rows_valid,
+                                        int k0, uint8_t* lds) const {
+    const uint16_t* b = base + row0 * ld + k0;
+    const rsrc_t r = make_rsrc(b, (static_cast<int64_t>(rows_valid - row0) * ld - k0) * 2);
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      const int q = i * kWaves + wave;
+      load_lds16(r, lds + q * 8 * ROW_BYTES, voff[i]);
     }
   }
 };
@@ -122,6 +150,7 @@ struct KMajorDirect {
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef short v8i16 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8_t;
 
 template <int ROWS>
 struct MNMajorDirect {
@@ -129,8 +158,8 @@ struct MNMajorDirect {
   static constexpr int RPI = 64 / CPR;         // k-rows per wave instruction
   static constexpr int INSTR = BK / RPI / kWaves;   // instructions per wave
   static constexpr int ROWB = ROWS * 2;        // bytes per k-row
-  __device__ __forceinline__ static void issue(const uint16_t* base, int64_t ld, int row0,
-                                               int rows_valid, int k0, uint8_t* lds) {
+  int voff[INSTR];
+  __device__ __forceinline__ void init(int64_t ld, int row0, int rows_valid) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int sub = lane / CPR, pchunk = lane % CPR;
@@ -139,29 +168,28 @@ struct MNMajorDirect {
       const int kb = (i * kWaves + wave) * RPI;
       const int kr = kb + sub;
       const int c = pchunk ^ (4 * (kr & 3));
-      // columns past the valid range read the last valid chunk; they only feed
-      // accumulator rows or columns that are never stored
       const int col = min(row0 + c * 8, rows_valid - 8);
-      const uint16_t* src = base + static_cast<int64_t>(k0 + kr) * ld + col;
-      __builtin_amdgcn_global_load_lds((const gbl_void_t*)src, (lds_void_t*)(lds + kb * ROWB), 16,
-                                       0, 0);
+      voff[i] = static_cast<int>((kr * ld + (col - row0)) * 2);
     }
   }
-  // Operand of k16 step kk for rows rbase + (lane / 16 % 2) * 16 + lane % 16
-  // (= rbase + lane % 32), k = 16 kk + 8 (lane / 32) + 0..7.
-  __device__ __forceinline__ static bf16x8 frag(const uint8_t* lds, int rbase, int kk, int lane) {
+  __device__ __forceinline__ void issue(const uint16_t* base, int64_t ld, int row0, int K, int k0,
+                                        uint8_t* lds) const {
+    const uint16_t* b = base + static_cast<int64_t>(k0) * ld + row0;
+    const rsrc_t r = make_rsrc(b, (static_cast<int64_t>(K - k0) * ld - row0) * 2);
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      const int kb = (i * kWaves + wave) * RPI;
+      load_lds16(r, lds + kb * ROWB, voff[i]);
+    }
+  }
+  // Lane-dependent byte offset of the k16-step-0 operand for rows rbase.. of
+  // a stage (the low 8 bytes; the high 8 are 4 k-rows further, step kk is
+  // 16 kk k-rows further).
+  __device__ __forceinline__ static uint32_t frag_off(int rbase, int lane) {
     const int h = lane >> 5, q = (lane >> 4) & 1, i = lane & 15;
     const int c = (rbase + q * 16) / 8 + ((i & 3) >> 1);
-    const int byte = (i & 1) * 8;
-    const int r0 = 16 * kk + 8 * h + (i >> 2);
-    const int r1 = r0 + 4;
-    const __attribute__((address_space(3))) uint8_t* b = (const __attribute__((address_space(3))) uint8_t*)lds;
-    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_v4i16_t*)(b + r0 * ROWB + ((c ^ (4 * (r0 & 3))) << 4) + byte));
-    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_v4i16_t*)(b + r1 * ROWB + ((c ^ (4 * (r1 & 3))) << 4) + byte));
-    const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    return __builtin_bit_cast(bf16x8, v);
+    return (8 * h + (i >> 2)) * ROWB + ((c ^ (4 * (i >> 2))) << 4) + (i & 1) * 8;
   }
 };
 
@@ -215,12 +243,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   const int wm = wave / (kWaves / kWaveRows), wn = wave % (kWaves / kWaveRows);
 
   // Global loads of tile kt, straight into the given LDS stage.
+  std::conditional_t<A_KMAJOR, KMajorDirect<BM>, MNMajorDirect<BM>> ld_a;
+  std::conditional_t<B_KMAJOR, KMajorDirect<BN>, MNMajorDirect<BN>> ld_b;
+  ld_a.init(p.lda, m0, p.M);
+  ld_b.init(p.ldb, n0, p.N);
   auto issue_loads = [&](int kt, uint8_t* as_dst, uint8_t* bs_dst) {
     const int k0 = kt * BK;
-    if constexpr (A_KMAJOR) KMajorDirect<BM>::issue(p.A, p.lda, m0, p.M, k0, as_dst);
-    else MNMajorDirect<BM>::issue(p.A, p.lda, m0, p.M, k0, as_dst);
-    if constexpr (B_KMAJOR) KMajorDirect<BN>::issue(p.B, p.ldb, n0, p.N, k0, bs_dst);
-    else MNMajorDirect<BN>::issue(p.B, p.ldb, n0, p.N, k0, bs_dst);
+    if constexpr (A_KMAJOR) ld_a.issue(p.A, p.lda, m0, p.M, k0, as_dst);
+    else ld_a.issue(p.A, p.lda, m0, p.K, k0, as_dst);
+    if constexpr (B_KMAJOR) ld_b.issue(p.B, p.ldb, n0, p.N, k0, bs_dst);
+    else ld_b.issue(p.B, p.ldb, n0, p.K, k0, bs_dst);
   };
 
   f32x16 acc[TM][TN];
@@ -235,27 +267,69 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   // indices (StaticFor): left to the loop unroller, a body this large can
   // stay rolled, and a runtime index would move acc and the fragments to
   // scratch memory.
-  auto compute = [&](const uint8_t* as, const uint8_t* bs) {
+  // LDS operand addresses: the lane-dependent parts are computed once and
+  // hidden from the optimizer, so that every operand read is its stage
+  // array plus one of these registers plus an immediate (tile, k step). Left
+  // alone, the compiler folds the tile and step offsets into a separate
+  // register per read and runs out of room for the next step's operands.
+  // The reads keep naming their stage array so that the waits for the
+  // direct loads into one stage are not put in front of reads of the other.
+  constexpr int NA = A_KMAJOR ? BK / 16 : TM, NB = B_KMAJOR ? BK / 16 : TN;
+  uint32_t a_reg[NA], b_reg[NB];
+  {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int x = 0; x < NA; ++x) {
+      if constexpr (A_KMAJOR)
+        a_reg[x] = (wm * WM + l32) * ROW_BYTES + (((2 * x + h) ^ swz_bits(l32)) << 4);
+      else
+        a_reg[x] = MNMajorDirect<BM>::frag_off(wm * WM + x * 32, lane);
+      asm volatile("" : "+v"(a_reg[x]));
+    }
+#pragma unroll
+    for (int x = 0; x < NB; ++x) {
+      if constexpr (B_KMAJOR)
+        b_reg[x] = (wn * WN + l32) * ROW_BYTES + (((2 * x + h) ^ swz_bits(l32)) << 4);
+      else
+        b_reg[x] = MNMajorDirect<BN>::frag_off(wn * WN + x * 32, lane);
+      asm volatile("" : "+v"(b_reg[x]));
+    }
+  }
+  typedef const __attribute__((address_space(3))) uint8_t* lds_ptr;
+
+  // MFMAs over one LDS stage, with the operands of the next k16 step read
+  // while the current step's MFMAs run.
+  // Every k step, fragment slot and accumulator is visited with compile-time
+  // indices (StaticFor): left to the loop unroller, a body this large can
+  // stay rolled, and a runtime index would move acc and the fragments to
+  // scratch memory.
+  auto compute = [&](auto stagec) {
+    constexpr int st = decltype(stagec)::value;
+    const lds_ptr la = (lds_ptr)(st ? As1 : As0);
+    const lds_ptr lb = (lds_ptr)(st ? Bs1 : Bs0);
     bf16x8 af[2][TM], bfr[2][TN];
     auto read_frags = [&](auto kkc, auto slotc) {
       constexpr int kk = decltype(kkc)::value, slot = decltype(slotc)::value;
-      const int chunk = kk * 2 + (lane >> 5);
       auto ra = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
         if constexpr (A_KMAJOR) {
-          const int row = wm * WM + i * 32 + (lane & 31);
-          af[slot][i] = *reinterpret_cast<const bf16x8*>(as + swz(row, chunk));
+          af[slot][i] = *(const lds_bf16x8_t*)(la + a_reg[kk] + i * 32 * ROW_BYTES);
         } else {
-          af[slot][i] = MNMajorDirect<BM>::frag(as, wm * WM + i * 32, kk, lane);
+          constexpr uint32_t R = MNMajorDirect<BM>::ROWB;
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(la + a_reg[i] + kk * 16 * R));
+          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(la + a_reg[i] + kk * 16 * R + 4 * R));
+          af[slot][i] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
       };
       auto rb = [&](auto jc) {
         constexpr int j = decltype(jc)::value;
         if constexpr (B_KMAJOR) {
-          const int row = wn * WN + j * 32 + (lane & 31);
-          bfr[slot][j] = *reinterpret_cast<const bf16x8*>(bs + swz(row, chunk));
+          bfr[slot][j] = *(const lds_bf16x8_t*)(lb + b_reg[kk] + j * 32 * ROW_BYTES);
         } else {
-          bfr[slot][j] = MNMajorDirect<BN>::frag(bs, wn * WN + j * 32, kk, lane);
+          constexpr uint32_t R = MNMajorDirect<BN>::ROWB;
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(lb + b_reg[j] + kk * 16 * R));
+          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(lb + b_reg[j] + kk * 16 * R + 4 * R));
+          bfr[slot][j] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
       };
       StaticFor<0, TM>::run(ra);
@@ -266,6 +340,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       constexpr int kk = decltype(kkc)::value, cur = kk & 1;
       if constexpr (kk + 1 < BK / 16)
         read_frags(std::integral_constant<int, kk + 1>{}, std::integral_constant<int, cur ^ 1>{});
+      // The next step's reads stay in front of this step's MFMAs (otherwise
+      // the scheduler moves them behind and reuses the same registers).
+      __builtin_amdgcn_sched_barrier(0);
       auto mm = [&](auto ijc) {
         constexpr int i = decltype(ijc)::value / TN, j = decltype(ijc)::value % TN;
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
@@ -275,16 +352,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
     StaticFor<0, BK / 16>::run(kstep);
   };
 
-  // One pipeline step: compute on stage (cur_a, cur_b) while tile kt + 1
-  // moves into the other stage, then a barrier.
-  auto step = [&](int kt, int KT, const uint8_t* cur_a, const uint8_t* cur_b, uint8_t* nxt_a,
-                  uint8_t* nxt_b) {
-    if (kt + 1 < KT) issue_loads(kt + 1, nxt_a, nxt_b);
+  // One pipeline step: compute on stage `cur` while tile kt + 1 moves into
+  // the other stage, then a barrier.
+  auto step = [&](int kt, int KT, auto curc) {
+    constexpr int cur = decltype(curc)::value;
+    if (kt + 1 < KT) issue_loads(kt + 1, cur ? As0 : As1, cur ? Bs0 : Bs1);
     // Keep the loads of the next tile ahead of this tile's MFMAs: left to
     // itself the scheduler sinks them to the end of the step, right in front
     // of the wait for them, and the whole memory latency is exposed.
     __builtin_amdgcn_sched_barrier(0);
-    compute(cur_a, cur_b);
+    compute(curc);
     // The direct loads of the next tile and every read of this one are done
     // before any wave moves on.
     __builtin_amdgcn_s_waitcnt(0);
@@ -297,10 +374,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   __syncthreads();
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
-    step(kt, KT, As0, Bs0, As1, Bs1);
-    step(kt + 1, KT, As1, Bs1, As0, Bs0);
+    step(kt, KT, std::integral_constant<int, 0>{});
+    step(kt + 1, KT, std::integral_constant<int, 1>{});
   }
-  if (kt < KT) step(kt, KT, As0, Bs0, As1, Bs1);
+  if (kt < KT) step(kt, KT, std::integral_constant<int, 0>{});
 
   // ---- epilogue ----
   const int lrow = (lane >> 5) * 4;
@@ -422,6 +499,9 @@ int dispatch(GemmParams p, hipStream_t s) {
   return launch<128, 128, AK, BKM, EPI, OB>(p, s);
 }
 
+// Load offsets are 32-bit: 256 rows of a K-major tile span 256 * ld * 2 bytes.
+constexpr int kMaxLd = 1 << 22;
+
 bool ok16(const void* p, int64_t ld) {
   return aligned16(p) && (ld % 8) == 0;
 }
@@ -443,6 +523,8 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
     return fail(MR_EINVAL, "mr_gemm: M and N must be multiples of 8 and K a positive multiple of %d "
                 "(M=%lld N=%lld K=%lld)", BK, (long long)M, (long long)N, (long long)K);
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return fail(MR_EINVAL, "mr_gemm: too large");
+  if (lda > kMaxLd || ldb > kMaxLd)
+    return fail(MR_EINVAL, "mr_gemm: leading dimensions above %d are not supported", kMaxLd);
   if (!ok16(A, lda) || !ok16(B, ldb))
     return fail(MR_EINVAL, "mr_gemm: operands must be 16-byte aligned with ld a multiple of 8");
   if (c_dtype != MR_F32 && c_dtype != MR_BF16) return fail(MR_EINVAL, "mr_gemm: C must be fp32 or bf16");
@@ -491,6 +573,8 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
     return fail(MR_EINVAL, "mr_gemm_swiglu: M %% 8, N %% 32 and K %% %d must be 0", BK);
   if (!ok16(X, ldx) || !ok16(Wgu, ldw))
     return fail(MR_EINVAL, "mr_gemm_swiglu: operands must be 16-byte aligned");
+  if (ldx < K || ldw < K || ldact < N || (gu && ldgu < 2 * N) || ldx > kMaxLd || ldw > kMaxLd)
+    return fail(MR_EINVAL, "mr_gemm_swiglu: bad leading dimension");
   GemmParams p{};
   p.M = static_cast<int>(M);
   p.N = static_cast<int>(2 * N);
@@ -518,6 +602,8 @@ int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t 
     return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: M %% 8, N %% 32 and K %% %d must be 0", BK);
   if (!ok16(dd, ldd) || !ok16(Wd, ldw))
     return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: operands must be 16-byte aligned");
+  if (ldd < K || ldw < N || lddgu < 2 * N || ldd > kMaxLd || ldw > kMaxLd)
+    return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: bad leading dimension");
   if (ldgu != lddgu) return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: gu and dgu must share a layout");
   GemmParams p{};
   p.M = static_cast<int>(M);

@@ -64,6 +64,8 @@ __device__ __forceinline__ bf16x8 frag_row(const uint8_t* lds, int r, int s, int
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8_t;
+typedef const __attribute__((address_space(3))) uint8_t* lds_cptr;
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
 
@@ -334,8 +336,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
   __shared__ __attribute__((aligned(1024))) uint8_t O0[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t Q1[TILE];
   __shared__ __attribute__((aligned(1024))) uint8_t O1[TILE];
-  __shared__ float LD0[128];  // lse (log2 domain) then rowsum(dO O) of the tile's 64 queries
-  __shared__ float LD1[128];
+  __shared__ __attribute__((aligned(16))) float LD0[128];  // lse (log2 domain) then rowsum(dO O) of the tile's 64 queries
+  __shared__ __attribute__((aligned(16))) float LD1[128];
   const int kb = blockIdx.z, g = blockIdx.x, b = blockIdx.y;
   const int G = Hq / Hkv;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
@@ -378,6 +380,102 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
   issue(0, Q0, O0);
   if (threadIdx.x < 128) LD0[threadIdx.x] = fetch_ld(0);
 
+  // One query tile (two 32-query halves) as a software pipeline. The S^T and
+  // dP^T MFMAs of both halves go first (their LDS operands read one step
+  // ahead), then each half's softmax and dS run while the MFMA pipe still
+  // works on earlier products, and each half's dV, dK MFMAs take their
+  // transposed operands one step ahead. sched_barrier pins the order the
+  // compiler would otherwise collapse. The first two tiles of every head
+  // cross the block's keys (DIAG): there P is zeroed for keys after the
+  // query; a half entirely before the wave's keys contributes zeros.
+  // Lane-dependent LDS offsets of the tile reads, computed once and hidden
+  // from the optimizer, so that every read is its tile plus one of these
+  // registers plus an immediate (32-row half, k16 step). Row reads: row l32
+  // at chunk 2 s + h. Transposing reads: k-rows 4 h + i / 4 (+ 8), column
+  // block dt; the swizzle of those rows does not depend on the k16 step.
+  uint32_t row_off[NS], tr_off[2][ND];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    row_off[s] = rowtile_off<D>(l32, 2 * s + h);
+    asm volatile("" : "+v"(row_off[s]));
+  }
+#pragma unroll
+  for (int hv = 0; hv < 2; ++hv)
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      const int q = (lane >> 4) & 1, li = lane & 15;
+      tr_off[hv][dt] = rowtile_off<D>(4 * h + (li >> 2) + 8 * hv, (dt * 32 + q * 16) / 8 + ((li & 3) >> 1)) +
+                       (li & 1) * 8;
+      asm volatile("" : "+v"(tr_off[hv][dt]));
+    }
+  auto rd_row = [&](const uint8_t* t, int mq, int s) -> bf16x8 {
+    return *(const lds_bf16x8_t*)((lds_cptr)t + row_off[s] + mq * 32 * (2 * D));
+  };
+  auto rd_tr = [&](const uint8_t* t, int dt, int s) -> bf16x8 {
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((lds_cptr)t + tr_off[0][dt] + s * 16 * (2 * D)));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((lds_cptr)t + tr_off[1][dt] + s * 16 * (2 * D)));
+    typedef short v8i16 __attribute__((ext_vector_type(8)));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  auto tile = [&](auto diagc, int qt0, const uint8_t* Qc, const uint8_t* Oc, const float* LDc) {
+    constexpr bool DIAG = decltype(diagc)::value;
+    f32x16 sacc[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+    bf16x8 qa[2], oa[2];
+    qa[0] = rd_row(Qc, 0, 0);
+    oa[0] = rd_row(Oc, 0, 0);
+    auto sdp = [&](auto idxc) {
+      constexpr int idx = decltype(idxc)::value, mq = idx / NS, s = idx % NS;
+      if constexpr (idx + 1 < 2 * NS) {
+        constexpr int n = idx + 1;
+        qa[n & 1] = rd_row(Qc, n / NS, n % NS);
+        oa[n & 1] = rd_row(Oc, n / NS, n % NS);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      sacc[mq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[idx & 1], kf[s], sacc[mq], 0, 0, 0);
+      dp[mq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[idx & 1], vf[s], dp[mq], 0, 0, 0);
+    };
+    StaticFor<0, 2 * NS>::run(sdp);
+    auto half = [&](auto mqc) {
+      constexpr int mq = decltype(mqc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      bf16x8 ta[2], tb[2];  // dO^T and Q^T operands, one step ahead
+      ta[0] = rd_tr(Oc, 0, 2 * mq);
+      tb[0] = rd_tr(Qc, 0, 2 * mq);
+      const float4* l4 = reinterpret_cast<const float4*>(LDc + mq * 32 + 4 * h);
+      const float4* d4 = reinterpret_cast<const float4*>(LDc + 64 + mq * 32 + 4 * h);
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {  // rows 8 gq + 4 h + 0..3 of the half: acc registers 4 gq..
+        const float4 lv = l4[2 * gq], dv4 = d4[2 * gq];
+        const float lq[4] = {lv.x, lv.y, lv.z, lv.w}, dq[4] = {dv4.x, dv4.y, dv4.z, dv4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * gq + j;
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[mq][r], scale_log2, -lq[j]));
+          if (DIAG && kj > qt0 + mq * 32 + acc_row(r, h)) p = 0.0f;
+          sacc[mq][r] = p;
+          dp[mq][r] = p * (dp[mq][r] - dq[j]);
+        }
+      }
+      const bf16x8 pa[2] = {cvt8(sacc[mq], 0), cvt8(sacc[mq], 8)};
+      const bf16x8 da[2] = {cvt8(dp[mq], 0), cvt8(dp[mq], 8)};
+      auto acc = [&](auto idxc) {
+        constexpr int idx = decltype(idxc)::value, ss = idx / ND, dt = idx % ND;
+        if constexpr (idx + 1 < 2 * ND) {
+          constexpr int n = idx + 1;
+          ta[n & 1] = rd_tr(Oc, n % ND, 2 * mq + n / ND);
+          tb[n & 1] = rd_tr(Qc, n % ND, 2 * mq + n / ND);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[ss], ta[idx & 1], dv[dt], 0, 0, 0);
+        dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da[ss], tb[idx & 1], dk[dt], 0, 0, 0);
+      };
+      StaticFor<0, 2 * ND>::run(acc);
+    };
+    half(std::integral_constant<int, 0>{});
+    half(std::integral_constant<int, 1>{});
+  };
+
   auto step = [&](int i, const uint8_t* Qc, const uint8_t* Oc, const float* LDc, uint8_t* Qn,
                   uint8_t* On, float* LDn) {
     __builtin_amdgcn_s_waitcnt(0);
@@ -388,41 +486,9 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
       issue(i + 1, Qn, On);
       if (threadIdx.x < 128) next_ld = fetch_ld(i + 1);
     }
-    const int qt0 = first_q + (i % nqt) * 64;
-#pragma unroll
-    for (int mq = 0; mq < 2; ++mq) {
-      const int qs0 = qt0 + mq * 32;
-      if (qs0 + 31 < k0w) continue;  // every query of the half before every key of the wave
-      const bool diag = qs0 < k0w + 31;
-      f32x16 sacc = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Qc, mq * 32 + l32, s, h), kf[s],
-                                                       sacc, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Oc, mq * 32 + l32, s, h), vf[s], dp,
-                                                     0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {  // P and dS overwrite S and dP in place
-        const int qrow = mq * 32 + acc_row(r, h);
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale_log2, -LDc[qrow]));
-        if (diag && kj > qt0 + qrow) p = 0.0f;
-        sacc[r] = p;
-        dp[r] = p * (dp[r] - LDc[64 + qrow]);
-      }
-#pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
-        const bf16x8 pa = cvt8(sacc, 8 * ss);
-        const bf16x8 da = cvt8(dp, 8 * ss);
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt) {
-          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa, frag_tr<D>(Oc, dt * 32, 2 * mq + ss, lane),
-                                                           dv[dt], 0, 0, 0);
-          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, frag_tr<D>(Qc, dt * 32, 2 * mq + ss, lane),
-                                                           dk[dt], 0, 0, 0);
-        }
-      }
-    }
+    const int t = i % nqt;
+    if (t < 2) tile(std::true_type{}, first_q + t * 64, Qc, Oc, LDc);
+    else tile(std::false_type{}, first_q + t * 64, Qc, Oc, LDc);
     if (more && threadIdx.x < 128) LDn[threadIdx.x] = next_ld;
   };
 

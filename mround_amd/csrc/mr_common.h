@@ -9,6 +9,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/mround_hip.h"
 
 namespace mr {
@@ -156,5 +158,17 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) {
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled by the front end.
+template <int B, int E>
+struct StaticFor {
+  template <typename F>
+  __device__ __forceinline__ static void run(F& f) {
+    if constexpr (B < E) {
+      f(std::integral_constant<int, B>{});
+      StaticFor<B + 1, E>::run(f);
+    }
+  }
+};
 
 }  // namespace mr

@@ -199,18 +199,6 @@ struct MNMajorDirect {
 __device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
 
-// f(integral_constant<int, I>) for I = B .. E-1, unrolled by the front end.
-template <int B, int E>
-struct StaticFor {
-  template <typename F>
-  __device__ __forceinline__ static void run(F& f) {
-    if constexpr (B < E) {
-      f(std::integral_constant<int, B>{});
-      StaticFor<B + 1, E>::run(f);
-    }
-  }
-};
-
 template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int WM = BM / kWaveRows, WN = BN / (kWaves / kWaveRows);

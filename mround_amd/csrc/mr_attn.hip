@@ -299,22 +299,37 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 
 // ---- backward ---------------------------------------------------------------
 
-// D[b, h, q] = sum_d dO[q, h d] * O[q, h d]: one wave per (token, head).
+// D[b, h, q] = sum_d dO[q, h d] * O[q, h d]: D / 8 lanes per (token, head),
+// each with one 16-byte load of dO and of O; the group's partial sums meet by
+// lane exchanges inside the group.
 template <int D>
 __global__ __launch_bounds__(kThreads) void attn_bwd_dot(const uint16_t* __restrict__ dout,
                                                          const uint16_t* __restrict__ out,
                                                          int64_t ldo, int64_t T, int S, int Hq,
                                                          float* __restrict__ dsum) {
-  const int64_t w = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (w >= T * Hq) return;
-  const int64_t t = w / Hq;
-  const int hq = static_cast<int>(w % Hq);
+  constexpr int L = D / 8;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t pair = gid / L;
+  const int sub = static_cast<int>(gid % L);
+  const bool valid = pair < T * Hq;
   float acc = 0.0f;
-  for (int d = lane; d < D; d += 64)
-    acc += bf16_to_f32(dout[t * ldo + hq * D + d]) * bf16_to_f32(out[t * ldo + hq * D + d]);
-  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (lane == 0) {
+  int64_t t = 0;
+  int hq = 0;
+  if (valid) {
+    t = pair / Hq;
+    hq = static_cast<int>(pair % Hq);
+    const uint4 a = *reinterpret_cast<const uint4*>(dout + t * ldo + hq * D + sub * 8);
+    const uint4 o = *reinterpret_cast<const uint4*>(out + t * ldo + hq * D + sub * 8);
+    const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, ow[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc += __uint_as_float(aw[k] << 16) * __uint_as_float(ow[k] << 16);
+      acc += __uint_as_float(aw[k] & 0xffff0000u) * __uint_as_float(ow[k] & 0xffff0000u);
+    }
+  }
+#pragma unroll
+  for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (valid && sub == 0) {
     const int64_t b = t / S, s = t % S;
     dsum[(b * Hq + hq) * S + s] = acc;
   }
@@ -620,9 +635,9 @@ int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint1
                int64_t ldo, const float* lse, float* dsum, int B, int S, int Hq, int Hkv,
                float scale, uint16_t* dqkv, hipStream_t s) {
   const int64_t T = static_cast<int64_t>(B) * S;
-  const int64_t waves = T * Hq;
-  hipLaunchKernelGGL(attn_bwd_dot<D>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(kThreads), 0,
-                     s, dout, out, ldo, T, S, Hq, dsum);
+  const int64_t lanes = T * Hq * (D / 8);
+  hipLaunchKernelGGL(attn_bwd_dot<D>, dim3(static_cast<unsigned>((lanes + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, s, dout, out, ldo, T, S, Hq, dsum);
   hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
                      lse, dsum, S, Hq, Hkv, scale, dqkv);
   hipLaunchKernelGGL(attn_bwd_dq<D>, dim3(Hq, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
@@ -671,7 +686,8 @@ int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, 
   clear_error();
   int rc = check("mr_attn_bwd", qkv, ld, B, S, Hq, Hkv, head_dim, ldo);
   if (rc) return rc;
-  if (!out || !dout || !lse || !dsum_ws || !dqkv || !aligned16(dout) || !aligned16(dqkv))
+  if (!out || !dout || !lse || !dsum_ws || !dqkv || !aligned16(out) || !aligned16(dout) ||
+      !aligned16(dqkv))
     return fail(MR_EINVAL, "mr_attn_bwd: bad argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* q = static_cast<const uint16_t*>(qkv);

@@ -114,6 +114,154 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ 
     y[i] = f32_to_bf16(x[i]);
 }
 
+
+// ---- vectorized forms (16-byte loads, rows held in registers) ---------------
+// Used when every row starts 16-byte aligned and H is a multiple of 4: a
+// thread owns float4 columns tid, tid + kBlock, ... of its row (NV of them),
+// so each row is read from HBM once.
+
+__device__ __forceinline__ uint2 pack4_bf16(float a, float b, float c, float d) {
+  return make_uint2(static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16),
+                    static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16));
+}
+
+template <int NV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_fwd_v(const float* __restrict__ h,
+                                                        const float* __restrict__ w, int64_t H,
+                                                        float eps, uint16_t* __restrict__ y,
+                                                        float* __restrict__ rstd) {
+  __shared__ float smem[kBlock / 64];
+  const int64_t row = blockIdx.x;
+  const int n4 = static_cast<int>(H / 4);
+  const float4* hr = reinterpret_cast<const float4*>(h + row * H);
+  float4 v[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    v[k] = i < n4 ? hr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+  }
+  ss = block_sum_f32(ss, smem);
+  const float r = rsqrtf(ss / static_cast<float>(H) + eps);
+  if (threadIdx.x == 0 && rstd) rstd[row] = r;
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  uint2* yr = reinterpret_cast<uint2*>(y + row * H);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (i < n4) {
+      const float4 g = w4[i];
+      yr[i] = pack4_bf16(v[k].x * r * g.x, v[k].y * r * g.y, v[k].z * r * g.z, v[k].w * r * g.w);
+    }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_bwd_v(const float* __restrict__ dy,
+                                                        const float* __restrict__ h,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ rstd,
+                                                        const float* __restrict__ dres, int64_t H,
+                                                        uint16_t* __restrict__ dh_bf16,
+                                                        float* __restrict__ dh_f32) {
+  __shared__ float smem[kBlock / 64];
+  const int64_t row = blockIdx.x;
+  const int n4 = static_cast<int>(H / 4);
+  const float4* dyr = reinterpret_cast<const float4*>(dy + row * H);
+  const float4* hr = reinterpret_cast<const float4*>(h + row * H);
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  float4 gy[NV], hv[NV];
+  float dot = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    hv[k] = i < n4 ? hr[i] : z;
+    const float4 d = i < n4 ? dyr[i] : z;
+    const float4 g = i < n4 ? w4[i] : z;
+    gy[k] = make_float4(d.x * g.x, d.y * g.y, d.z * g.z, d.w * g.w);  // dy w
+    dot += gy[k].x * hv[k].x + gy[k].y * hv[k].y + gy[k].z * hv[k].z + gy[k].w * hv[k].w;
+  }
+  dot = block_sum_f32(dot, smem);
+  const float r = rstd[row];
+  const float c = r * r * r * dot / static_cast<float>(H);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (i >= n4) continue;
+    float4 g = make_float4(r * gy[k].x - c * hv[k].x, r * gy[k].y - c * hv[k].y,
+                           r * gy[k].z - c * hv[k].z, r * gy[k].w - c * hv[k].w);
+    if (dres) {
+      const float4 q = reinterpret_cast<const float4*>(dres + row * H)[i];
+      g.x += q.x; g.y += q.y; g.z += q.z; g.w += q.w;
+    }
+    if (dh_bf16) reinterpret_cast<uint2*>(dh_bf16 + row * H)[i] = pack4_bf16(g.x, g.y, g.z, g.w);
+    if (dh_f32) reinterpret_cast<float4*>(dh_f32 + row * H)[i] = g;
+  }
+}
+
+// Rotary embedding, 8 pairs per thread: 16-byte loads of x_i.. and
+// x_{i+d/2}.., 64 bytes of the cos/sin table. Needs d % 16 == 0 and 16-byte
+// aligned rows.
+template <bool BWD>
+__global__ __launch_bounds__(kBlock) void rope_v(uint16_t* __restrict__ x, int64_t ld, int64_t T,
+                                                 int S, int n_heads, int d,
+                                                 const float* __restrict__ cs) {
+  const int half = d / 2, groups = half / 8;
+  const int64_t total = T * n_heads * groups;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (idx >= total) return;
+  const int gi = static_cast<int>(idx % groups);
+  const int64_t th = idx / groups;
+  const int hd = static_cast<int>(th % n_heads);
+  const int64_t t = th / n_heads;
+  const int pos = static_cast<int>(t % S);
+  uint16_t* p = x + t * ld + static_cast<int64_t>(hd) * d + gi * 8;
+  const uint4 av = *reinterpret_cast<const uint4*>(p);
+  const uint4 bv = *reinterpret_cast<const uint4*>(p + half);
+  const float4* c4 = reinterpret_cast<const float4*>(cs + (static_cast<int64_t>(pos) * half + gi * 8) * 2);
+  const uint32_t aw[4] = {av.x, av.y, av.z, av.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+  uint32_t ow_a[4], ow_b[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // pairs 2k, 2k + 1
+    const float4 t4 = c4[k];      // cos, sin of pair 2k; cos, sin of pair 2k + 1
+    const float a0 = __uint_as_float(aw[k] << 16), a1 = __uint_as_float(aw[k] & 0xffff0000u);
+    const float b0 = __uint_as_float(bw[k] << 16), b1 = __uint_as_float(bw[k] & 0xffff0000u);
+    float ya0, yb0, ya1, yb1;
+    if constexpr (BWD) {
+      ya0 = a0 * t4.x + b0 * t4.y; yb0 = b0 * t4.x - a0 * t4.y;
+      ya1 = a1 * t4.z + b1 * t4.w; yb1 = b1 * t4.z - a1 * t4.w;
+    } else {
+      ya0 = a0 * t4.x - b0 * t4.y; yb0 = b0 * t4.x + a0 * t4.y;
+      ya1 = a1 * t4.z - b1 * t4.w; yb1 = b1 * t4.z + a1 * t4.w;
+    }
+    ow_a[k] = static_cast<uint32_t>(f32_to_bf16(ya0)) | (static_cast<uint32_t>(f32_to_bf16(ya1)) << 16);
+    ow_b[k] = static_cast<uint32_t>(f32_to_bf16(yb0)) | (static_cast<uint32_t>(f32_to_bf16(yb1)) << 16);
+  }
+  *reinterpret_cast<uint4*>(p) = make_uint4(ow_a[0], ow_a[1], ow_a[2], ow_a[3]);
+  *reinterpret_cast<uint4*>(p + half) = make_uint4(ow_b[0], ow_b[1], ow_b[2], ow_b[3]);
+}
+
+__global__ __launch_bounds__(kBlock) void cast_v(const float4* __restrict__ x, uint2* __restrict__ y,
+                                                 int64_t n4) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4; i += stride) {
+    const float4 v = x[i];
+    y[i] = pack4_bf16(v.x, v.y, v.z, v.w);
+  }
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// float4 columns per thread for a row of H floats, or 0 when H is too wide.
+int row_nv(int64_t H) {
+  const int64_t n4 = H / 4;
+  for (int nv : {1, 2, 4, 8, 16})
+    if (n4 <= static_cast<int64_t>(nv) * kBlock) return nv;
+  return 0;
+}
+
 }  // namespace
 }  // namespace mr
 
@@ -124,6 +272,15 @@ int mr_cast_f32_bf16(const float* x, void* y, int64_t n, void* stream) {
   clear_error();
   if (n <= 0) return MR_OK;
   if (!x || !y) return fail(MR_EINVAL, "mr_cast_f32_bf16: null pointer");
+  if (n % 4 == 0 && al16(x) && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) {
+    int64_t blocks = (n / 4 + kBlock - 1) / kBlock;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(cast_v, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), reinterpret_cast<const float4*>(x),
+                       static_cast<uint2*>(y), n / 4);
+    MR_LAUNCH_CHECK("mr_cast_f32_bf16");
+    return MR_OK;
+  }
   int64_t blocks = (n + kBlock - 1) / kBlock;
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(cast_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
@@ -139,9 +296,23 @@ int mr_rmsnorm_fwd(const float* h, const float* w, int64_t T, int64_t H, float e
   if (T <= 0 || H <= 0) return MR_OK;
   if (!h || !w || !y_bf16) return fail(MR_EINVAL, "mr_rmsnorm_fwd: null pointer");
   if (T > 0x7fffffff) return fail(MR_EINVAL, "mr_rmsnorm_fwd: too many rows");
-  hipLaunchKernelGGL(rmsnorm_fwd, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0,
-                     static_cast<hipStream_t>(stream), h, w, H, eps,
-                     static_cast<uint16_t*>(y_bf16), rstd_out);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* y = static_cast<uint16_t*>(y_bf16);
+  const int nv = row_nv(H);
+  if (H % 4 == 0 && nv && al16(h) && al16(w) && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) {
+    const dim3 g(static_cast<unsigned>(T));
+    switch (nv) {
+      case 1: hipLaunchKernelGGL(rmsnorm_fwd_v<1>, g, dim3(kBlock), 0, s, h, w, H, eps, y, rstd_out); break;
+      case 2: hipLaunchKernelGGL(rmsnorm_fwd_v<2>, g, dim3(kBlock), 0, s, h, w, H, eps, y, rstd_out); break;
+      case 4: hipLaunchKernelGGL(rmsnorm_fwd_v<4>, g, dim3(kBlock), 0, s, h, w, H, eps, y, rstd_out); break;
+      case 8: hipLaunchKernelGGL(rmsnorm_fwd_v<8>, g, dim3(kBlock), 0, s, h, w, H, eps, y, rstd_out); break;
+      default: hipLaunchKernelGGL(rmsnorm_fwd_v<16>, g, dim3(kBlock), 0, s, h, w, H, eps, y, rstd_out); break;
+    }
+    MR_LAUNCH_CHECK("mr_rmsnorm_fwd");
+    return MR_OK;
+  }
+  hipLaunchKernelGGL(rmsnorm_fwd, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0, s, h, w, H, eps,
+                     y, rstd_out);
   MR_LAUNCH_CHECK("mr_rmsnorm_fwd");
   return MR_OK;
 }
@@ -155,9 +326,24 @@ int mr_rmsnorm_bwd(const float* dy, const float* h, const float* w, const float*
   if (!dy || !h || !w || !rstd || (!dh_bf16 && !dh_f32))
     return fail(MR_EINVAL, "mr_rmsnorm_bwd: null pointer");
   if (T > 0x7fffffff) return fail(MR_EINVAL, "mr_rmsnorm_bwd: too many rows");
-  hipLaunchKernelGGL(rmsnorm_bwd, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0,
-                     static_cast<hipStream_t>(stream), dy, h, w, rstd, dres, H,
-                     static_cast<uint16_t*>(dh_bf16), dh_f32);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* db = static_cast<uint16_t*>(dh_bf16);
+  const int nv = row_nv(H);
+  if (H % 4 == 0 && nv && al16(dy) && al16(h) && al16(w) && (!dres || al16(dres)) &&
+      (!dh_f32 || al16(dh_f32)) && (reinterpret_cast<uintptr_t>(db) & 7u) == 0) {
+    const dim3 g(static_cast<unsigned>(T));
+    switch (nv) {
+      case 1: hipLaunchKernelGGL(rmsnorm_bwd_v<1>, g, dim3(kBlock), 0, s, dy, h, w, rstd, dres, H, db, dh_f32); break;
+      case 2: hipLaunchKernelGGL(rmsnorm_bwd_v<2>, g, dim3(kBlock), 0, s, dy, h, w, rstd, dres, H, db, dh_f32); break;
+      case 4: hipLaunchKernelGGL(rmsnorm_bwd_v<4>, g, dim3(kBlock), 0, s, dy, h, w, rstd, dres, H, db, dh_f32); break;
+      case 8: hipLaunchKernelGGL(rmsnorm_bwd_v<8>, g, dim3(kBlock), 0, s, dy, h, w, rstd, dres, H, db, dh_f32); break;
+      default: hipLaunchKernelGGL(rmsnorm_bwd_v<16>, g, dim3(kBlock), 0, s, dy, h, w, rstd, dres, H, db, dh_f32); break;
+    }
+    MR_LAUNCH_CHECK("mr_rmsnorm_bwd");
+    return MR_OK;
+  }
+  hipLaunchKernelGGL(rmsnorm_bwd, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0, s, dy, h, w,
+                     rstd, dres, H, db, dh_f32);
   MR_LAUNCH_CHECK("mr_rmsnorm_bwd");
   return MR_OK;
 }
@@ -170,11 +356,24 @@ int mr_rope(void* x_bf16, int64_t ld, int64_t T, int S, int n_heads, int head_di
   if (!x_bf16 || !cos_sin) return fail(MR_EINVAL, "mr_rope: null pointer");
   if (head_dim <= 0 || head_dim % 2 || S <= 0 || ld < static_cast<int64_t>(n_heads) * head_dim)
     return fail(MR_EINVAL, "mr_rope: bad shape");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* x = static_cast<uint16_t*>(x_bf16);
+  if (head_dim % 16 == 0 && ld % 8 == 0 && al16(x) && al16(cos_sin)) {
+    const int64_t total_v = T * n_heads * (head_dim / 16);
+    const int64_t blocks_v = (total_v + kBlock - 1) / kBlock;
+    if (blocks_v > 0x7fffffff) return fail(MR_EINVAL, "mr_rope: too large");
+    if (backward)
+      hipLaunchKernelGGL(rope_v<true>, dim3(static_cast<unsigned>(blocks_v)), dim3(kBlock), 0, s, x,
+                         ld, T, S, n_heads, head_dim, cos_sin);
+    else
+      hipLaunchKernelGGL(rope_v<false>, dim3(static_cast<unsigned>(blocks_v)), dim3(kBlock), 0, s, x,
+                         ld, T, S, n_heads, head_dim, cos_sin);
+    MR_LAUNCH_CHECK("mr_rope");
+    return MR_OK;
+  }
   const int64_t total = T * n_heads * (head_dim / 2);
   const int64_t blocks = (total + kBlock - 1) / kBlock;
   if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_rope: too large");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  uint16_t* x = static_cast<uint16_t*>(x_bf16);
   if (backward)
     hipLaunchKernelGGL(rope_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x,
                        ld, T, S, n_heads, head_dim, cos_sin);

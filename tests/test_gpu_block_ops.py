@@ -166,7 +166,9 @@ def rmsnorm_ref(h, w, eps):
     return h64 * r * w.double(), r
 
 
-@pytest.mark.parametrize("shape", [(300, 896), (64, 3584), (8, 128), (17, 4096)])
+# rows of width % 4 == 0 take the vectorized kernels (row held in registers);
+# 130 and 9 take the scalar ones
+@pytest.mark.parametrize("shape", [(300, 896), (64, 3584), (8, 128), (17, 4096), (5, 130), (3, 9)])
 def test_rmsnorm_forward(shape):
     T, H = shape
     h = torch.randn(T, H, generator=_gen(31)) * 3
@@ -180,7 +182,7 @@ def test_rmsnorm_forward(shape):
     assert torch.allclose(rstd.double().cpu(), r_ref[:, 0], rtol=1e-5, atol=0)
 
 
-@pytest.mark.parametrize("shape", [(300, 896), (64, 3584)])
+@pytest.mark.parametrize("shape", [(300, 896), (64, 3584), (7, 130)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_rmsnorm_backward(shape, with_res):
     T, H = shape
@@ -236,7 +238,9 @@ def rope_ref(x, S, n_heads, d, cs, backward):
     return y, mag
 
 
-@pytest.mark.parametrize("cfg", [(2, 128, 6, 2, 64), (1, 256, 16, 4, 128), (3, 40, 2, 1, 128)])
+# head_dim % 16 == 0 with 16-byte rows takes the 8-pair kernel; 40 the scalar one
+@pytest.mark.parametrize("cfg", [(2, 128, 6, 2, 64), (1, 256, 16, 4, 128), (3, 40, 2, 1, 128),
+                                 (2, 24, 3, 1, 40)])
 @pytest.mark.parametrize("backward", [False, True])
 def test_rope(cfg, backward):
     B, S, Hq, Hkv, d = cfg
@@ -252,6 +256,19 @@ def test_rope(cfg, backward):
     assert torch.all((got - y_ref).abs() <= tol)
     # v heads and padding untouched
     assert torch.equal(got[:, (Hq + Hkv) * d:], x.double()[:, (Hq + Hkv) * d:])
+
+
+# ---------------------------------------------------------------------- cast --
+
+@pytest.mark.parametrize("n,offset", [(4096, 0), (1000, 0), (1001, 0), (1000, 1)])
+def test_cast_bf16(n, offset):
+    """fp32 -> bf16, round to nearest even (vectorized when n % 4 == 0 and aligned)."""
+    x = torch.randn(n + offset, generator=_gen(47)) * 100
+    x[offset + 3] = 1.0 + 2.0 ** -8  # a tie: rounds to even (1.0)
+    xd = x.to(dev())[offset:]
+    y = torch.empty(n + offset, dtype=torch.bfloat16, device=dev())[offset:]
+    K.cast_bf16(xd, y)
+    assert torch.equal(y.cpu(), x[offset:].to(torch.bfloat16))
 
 
 # -------------------------------------------------------------- SwiGLU bwd --

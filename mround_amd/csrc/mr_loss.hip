@@ -5,11 +5,13 @@
 // |r| of the whole batch (sort(|r|)[n - k]); every element tied at t is
 // excluded. loss = sum(r_kept^2) / denom and dL/dpred = 2 r_kept / denom.
 //
-// The threshold is found exactly by a three-pass radix select on the bit
-// pattern of |r| (non-negative floats order like their bit patterns): 11, 11
-// and 10 bits from the top, each pass a histogram of the next digit among
-// the elements that share the digits chosen so far, followed by a one-block
-// select. Everything stays on the device; no host synchronisation.
+// The threshold is found exactly by a two-pass radix select on the bit
+// pattern of |r| (non-negative floats order like their bit patterns, and the
+// sign bit is dropped): a histogram of the top 15 bits (30..16) built in LDS
+// per block, a one-block select of the bin holding the k-th largest, then a
+// histogram of the low 16 bits among the elements of that bin only (global
+// atomics, few elements), and a second select. Everything stays on the
+// device; no host synchronisation.
 //
 // Sums are deterministic: a fixed grid of kBlocks blocks, fp64 accumulation
 // per thread, a fixed-order block reduction, then one block adding the block
@@ -21,12 +23,16 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kBlocks = 1024;
-constexpr int kBins = 2048;
+constexpr int kHiBits = 15, kLoBits = 16;
+constexpr int kHiBins = 1 << kHiBits, kLoBins = 1 << kLoBits;
+constexpr int kSelThreads = 1024;
+constexpr int kHistThreads = 1024;
 
 struct Workspace {
   double partial[kBlocks];
-  uint32_t hist[kBins];
-  uint32_t state[4];  // [0] key prefix, [1] remaining rank k, [2] final key
+  uint32_t hist_hi[kHiBins];
+  uint32_t hist_lo[kLoBins];
+  uint32_t state[4];  // [0] top-15-bit digit, [1] remaining rank k, [2] final key
 };
 
 __device__ __forceinline__ double block_sum(double x, double* smem) {
@@ -41,82 +47,138 @@ __device__ __forceinline__ double block_sum(double x, double* smem) {
   return total;  // valid in thread 0
 }
 
-__global__ __launch_bounds__(kBlock) void zero_hist(Workspace* ws) {
-  for (int i = threadIdx.x; i < kBins; i += kBlock) ws->hist[i] = 0;
-}
+__device__ __forceinline__ uint32_t abs_key(float r) { return __float_as_uint(r) & 0x7fffffffu; }
 
-__global__ void set_rank(Workspace* ws, uint32_t k) {
-  ws->state[0] = 0;
-  ws->state[1] = k;
-}
-
-// Histogram of digit (key >> shift) & (nbins-1) among keys whose bits above
-// `shift + digit_bits` equal the prefix chosen so far.
-__global__ __launch_bounds__(kBlock) void radix_hist(const float* __restrict__ pred,
-                                                     const float* __restrict__ target, int64_t n,
-                                                     int shift, int nbits, int prefix_shift,
-                                                     Workspace* __restrict__ ws) {
-  __shared__ uint32_t h[kBins];
-  for (int i = threadIdx.x; i < kBins; i += kBlock) h[i] = 0;
-  __syncthreads();
-  const uint32_t prefix = ws->state[0];
-  const uint32_t dmask = (1u << nbits) - 1u;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
-    const float r = pred[i] - target[i];
-    const uint32_t key = __float_as_uint(r) & 0x7fffffffu;
-    const bool match = prefix_shift >= 32 || (key >> prefix_shift) == prefix;
-    if (match) atomicAdd(&h[(key >> shift) & dmask], 1u);
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < kBins; i += kBlock) {
-    if (h[i]) atomicAdd(&ws->hist[i], h[i]);
+__global__ __launch_bounds__(kBlock) void zero_hist(Workspace* ws, uint32_t k) {
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i < kHiBins) ws->hist_hi[i] = 0;
+  if (i < kLoBins) ws->hist_lo[i] = 0;
+  if (i == 0) {
+    ws->state[0] = 0;
+    ws->state[1] = k;
   }
 }
 
-// Finds the digit holding the k-th largest key: the largest d with
-// count(digit > d) < k <= count(digit >= d). Appends d to the prefix and
-// subtracts the count above from k. One block; each thread owns 8 bins.
-__global__ __launch_bounds__(kBlock) void radix_select(int nbits, int last, Workspace* ws,
-                                                       float* __restrict__ threshold_out) {
-  __shared__ uint32_t totals[kBlock];
-  __shared__ uint32_t above[kBlock];
-  const int nb = 1 << nbits;
-  const int per = (nb + kBlock - 1) / kBlock;
-  const int t = threadIdx.x;
-  uint32_t mine = 0;
-  for (int j = 0; j < per; ++j) {
-    int b = t * per + j;
-    if (b < nb) mine += ws->hist[b];
-  }
-  totals[t] = mine;
+// Pass 1: histogram of key >> 16 over every element, per block in LDS
+// (128 KB), then the block's non-empty bins added to the global histogram.
+__global__ __launch_bounds__(kHistThreads) void radix_hist_hi(const float* __restrict__ pred,
+                                                              const float* __restrict__ target,
+                                                              int64_t n, Workspace* __restrict__ ws) {
+  __shared__ uint32_t h[kHiBins];
+  for (int i = threadIdx.x; i < kHiBins; i += kHistThreads) h[i] = 0;
   __syncthreads();
-  if (t == 0) {
-    uint32_t run = 0;
-    for (int i = kBlock - 1; i >= 0; --i) {
-      above[i] = run;  // count in bins owned by threads > i
-      run += totals[i];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kHistThreads;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kHistThreads + threadIdx.x;
+  if ((n & 3) == 0) {
+    const float4* p4 = reinterpret_cast<const float4*>(pred);
+    const float4* t4 = reinterpret_cast<const float4*>(target);
+    for (int64_t i = first; i < n / 4; i += stride) {
+      const float4 p = p4[i], q = t4[i];
+      atomicAdd(&h[abs_key(p.x - q.x) >> kLoBits], 1u);
+      atomicAdd(&h[abs_key(p.y - q.y) >> kLoBits], 1u);
+      atomicAdd(&h[abs_key(p.z - q.z) >> kLoBits], 1u);
+      atomicAdd(&h[abs_key(p.w - q.w) >> kLoBits], 1u);
     }
+  } else {
+    for (int64_t i = first; i < n; i += stride) atomicAdd(&h[abs_key(pred[i] - target[i]) >> kLoBits], 1u);
   }
   __syncthreads();
-  const uint32_t k = ws->state[1];
-  uint32_t run = above[t];
-  if (run < k && k <= run + totals[t]) {
-    for (int j = per - 1; j >= 0; --j) {
-      int b = t * per + j;
-      if (b >= nb) continue;
-      uint32_t c = ws->hist[b];
-      if (run < k && k <= run + c) {
-        const uint32_t prefix = (ws->state[0] << nbits) | static_cast<uint32_t>(b);
-        ws->state[0] = prefix;
-        ws->state[1] = k - run;
-        if (last) {
-          ws->state[2] = prefix;
-          if (threshold_out) *threshold_out = __uint_as_float(prefix);
-        }
-        break;
+  for (int i = threadIdx.x; i < kHiBins; i += kHistThreads)
+    if (h[i]) atomicAdd(&ws->hist_hi[i], h[i]);
+}
+
+// Pass 2: histogram of the low 16 bits among the elements whose top 15 bits
+// are the chosen digit, straight into global memory.
+__global__ __launch_bounds__(kHistThreads) void radix_hist_lo(const float* __restrict__ pred,
+                                                              const float* __restrict__ target,
+                                                              int64_t n, Workspace* __restrict__ ws) {
+  const uint32_t digit = ws->state[0];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kHistThreads;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kHistThreads + threadIdx.x;
+  auto one = [&](float r) {
+    const uint32_t key = abs_key(r);
+    if ((key >> kLoBits) == digit) {
+      // lanes sharing one key (ties, the common case among few matches)
+      // add once: keeps a degenerate input from serialising on one address
+      const uint32_t k0 = __builtin_amdgcn_readfirstlane(key);
+      const uint64_t same = __ballot(key == k0), all = __ballot(1);
+      if (same == all) {
+        if (__lane_id() == static_cast<unsigned>(__builtin_ctzll(all)))
+          atomicAdd(&ws->hist_lo[k0 & (kLoBins - 1)], static_cast<uint32_t>(__popcll(all)));
+      } else {
+        atomicAdd(&ws->hist_lo[key & (kLoBins - 1)], 1u);
       }
-      run += c;
+    }
+  };
+  if ((n & 3) == 0) {
+    const float4* p4 = reinterpret_cast<const float4*>(pred);
+    const float4* t4 = reinterpret_cast<const float4*>(target);
+    for (int64_t i = first; i < n / 4; i += stride) {
+      const float4 p = p4[i], q = t4[i];
+      one(p.x - q.x);
+      one(p.y - q.y);
+      one(p.z - q.z);
+      one(p.w - q.w);
+    }
+  } else {
+    for (int64_t i = first; i < n; i += stride) one(pred[i] - target[i]);
+  }
+}
+
+// The bin holding the k-th largest key: the largest b with
+// count(bins > b) < k <= count(bins >= b). One block; thread t owns the
+// per = nbins / kSelThreads consecutive bins starting at t * per (read as
+// 16-byte vectors). A suffix sum over the threads finds the owner of that
+// bin; one wave then scans the owner's bins, a lane per bin. Pass 1 records
+// the digit and the rank left inside its bin; pass 2 forms the final key.
+__global__ __launch_bounds__(kSelThreads) void radix_select(int hi, Workspace* ws,
+                                                            float* __restrict__ threshold_out) {
+  __shared__ uint32_t above[kSelThreads];
+  __shared__ uint32_t win[2];  // owner thread, count strictly above its bins
+  const uint32_t* hist = hi ? ws->hist_hi : ws->hist_lo;
+  const int per = (hi ? kHiBins : kLoBins) / kSelThreads;  // 32 or 64
+  const int t = threadIdx.x;
+  const uint4* h4 = reinterpret_cast<const uint4*>(hist + t * per);
+  uint32_t mine = 0;
+  for (int j = 0; j < per / 4; ++j) {
+    const uint4 v = h4[j];
+    mine += v.x + v.y + v.z + v.w;
+  }
+  // suffix sums over threads, by doubling
+  above[t] = mine;
+  __syncthreads();
+  for (int off = 1; off < kSelThreads; off <<= 1) {
+    const uint32_t add = t + off < kSelThreads ? above[t + off] : 0u;
+    __syncthreads();
+    above[t] += add;
+    __syncthreads();
+  }
+  const uint32_t k = ws->state[1];
+  const uint32_t run0 = above[t] - mine;  // strictly above thread t's bins
+  if (run0 < k && k <= run0 + mine) {
+    win[0] = static_cast<uint32_t>(t);
+    win[1] = run0;
+  }
+  __syncthreads();
+  if (t >= 64) return;
+  // wave 0: lane l holds bin win[0] * per + l; suffix sums over the lanes
+  const int lane = t;
+  const int b = static_cast<int>(win[0]) * per + lane;
+  const uint32_t c = lane < per ? hist[b] : 0u;
+  uint32_t suf = c;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t v = __shfl_down(suf, off, 64);
+    if (lane + off < 64) suf += v;
+  }
+  const uint32_t above_b = win[1] + suf - c;  // count in bins > b
+  if (lane < per && above_b < k && k <= above_b + c) {
+    if (hi) {
+      ws->state[0] = static_cast<uint32_t>(b);
+      ws->state[1] = k - above_b;
+    } else {
+      const uint32_t key = (ws->state[0] << kLoBits) | static_cast<uint32_t>(b);
+      ws->state[2] = key;
+      if (threshold_out) *threshold_out = __uint_as_float(key);
     }
   }
 }
@@ -235,20 +297,14 @@ int mr_loss_outlier(const float* pred, const float* target, int64_t n, int64_t k
   hipStream_t s = static_cast<hipStream_t>(stream);
   Workspace* ws = static_cast<Workspace*>(workspace);
   const int grid = grid_for(n);
-  const int hist_grid = grid;
   if (!threshold_in) {
-    hipLaunchKernelGGL(set_rank, dim3(1), dim3(1), 0, s, ws, static_cast<uint32_t>(k));
-    // digits: bits [21, 32) then [10, 21) then [0, 10)
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
-    const int pshift[3] = {32, 21, 10};
-    for (int pass = 0; pass < 3; ++pass) {
-      hipLaunchKernelGGL(zero_hist, dim3(1), dim3(kBlock), 0, s, ws);
-      hipLaunchKernelGGL(radix_hist, dim3(hist_grid), dim3(kBlock), 0, s, pred, target, n,
-                         shifts[pass], widths[pass], pshift[pass], ws);
-      hipLaunchKernelGGL(radix_select, dim3(1), dim3(kBlock), 0, s, widths[pass], pass == 2 ? 1 : 0,
-                         ws, threshold_out);
-    }
+    int64_t hg = ((n & 3) == 0 ? n / 4 : n) / kHistThreads + 1;
+    const int hist_grid = static_cast<int>(hg < 256 ? hg : 256);
+    hipLaunchKernelGGL(zero_hist, dim3(kLoBins / kBlock), dim3(kBlock), 0, s, ws, static_cast<uint32_t>(k));
+    hipLaunchKernelGGL(radix_hist_hi, dim3(hist_grid), dim3(kHistThreads), 0, s, pred, target, n, ws);
+    hipLaunchKernelGGL(radix_select, dim3(1), dim3(kSelThreads), 0, s, 1, ws, threshold_out);
+    hipLaunchKernelGGL(radix_hist_lo, dim3(hist_grid), dim3(kHistThreads), 0, s, pred, target, n, ws);
+    hipLaunchKernelGGL(radix_select, dim3(1), dim3(kSelThreads), 0, s, 0, ws, threshold_out);
   } else if (threshold_out) {
     return fail(MR_EINVAL, "mr_loss_outlier: threshold_out is only written when it is computed");
   }

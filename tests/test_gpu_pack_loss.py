@@ -110,7 +110,7 @@ def test_mse_loss_and_grad(n):
     np.testing.assert_array_equal(to_np(grad), r * np.float32(2.0 / n))
 
 
-@pytest.mark.parametrize("n", [2000, 1 << 20, 2_359_296, 58_720_256 // 8])
+@pytest.mark.parametrize("n", [2000, 2001, 4097, 1 << 20, 2_359_296, 58_720_256 // 8])
 def test_outlier_threshold_exact(n):
     _note("outlier", n)
     gen = torch.Generator().manual_seed(n + 1)
@@ -126,6 +126,20 @@ def test_outlier_threshold_exact(n):
     assert float(loss) == pytest.approx(ref_loss, rel=1e-6)
     keep = np.abs(r) < ref_thr
     np.testing.assert_array_equal(to_np(grad), np.where(keep, r, 0).astype(np.float32) * np.float32(2.0 / n))
+
+
+@pytest.mark.parametrize("n", [4096, 4099, 1 << 20])
+def test_outlier_threshold_constant_residual(n):
+    """Every residual equal: the k-th largest is that value and every element
+    is tied with it, so the loss and gradient are zero."""
+    _note("outlier constant", n)
+    pred = torch.full((n,), 0.75)
+    thr = torch.empty((), device=dev())
+    loss, grad = LS.outlier_suppressed_loss(pred.to(dev()), torch.zeros(n, device=dev()),
+                                            with_grad=True, threshold_out=thr)
+    assert float(thr) == 0.75
+    assert float(loss) == 0.0
+    assert not torch.any(grad.cpu())
 
 
 def test_outlier_ties_all_excluded_and_pieces():

@@ -26,6 +26,7 @@
 // Blocks are renumbered so that each XCD (blocks are dealt to the 8 XCDs
 // round-robin) receives a contiguous run of tiles, grouped along M so that a
 // run shares B panels in that XCD's L2.
+#include <mutex>
 #include <type_traits>
 
 #include "mr_common.h"
@@ -72,7 +73,25 @@ struct GemmParams {
   uint16_t* gu;        // SWIGLU: gate/up copy, [M, 2 * n_out] bf16, interleaved like B
   int64_t ldgu;        // (SWIGLU_BWD reads the saved gate/up from gu and writes dgu to C)
   int grid_m, grid_n;
+  // Tiles of this launch: logical tiles tile0 .. tile0 + n_tiles - 1 of the
+  // grouped order. ksplit > 1: each tile's k steps are cut into ksplit runs
+  // of kt_per steps (one block each), whose raw fp32 accumulators go to
+  // ws[(tile - tile0) * ksplit + split] as BM x BN row-major partial tiles.
+  int tile0, n_tiles, ksplit, kt_per;
+  float* ws;
 };
+
+// Logical tile -> (tile row, tile column): groups of 8 tile rows, column by
+// column within a group, so that consecutive tiles share B panels.
+__device__ __forceinline__ void tile_coords(int lt, int grid_m, int grid_n, int& bm, int& bn) {
+  constexpr int GROUP_M = 8;
+  const int per_group = GROUP_M * grid_n;
+  const int group = lt / per_group;
+  const int first_m = group * GROUP_M;
+  const int gm = min(grid_m - first_m, GROUP_M);
+  bm = first_m + (lt % per_group) % gm;
+  bn = (lt % per_group) / gm;
+}
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -212,17 +231,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t Bs0[BN * ROW_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t Bs1[BN * ROW_BYTES];
 
-  // XCD-aware renumbering, then grouped order along M.
-  const int nblk = p.grid_m * p.grid_n;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  constexpr int GROUP_M = 8;
-  const int per_group = GROUP_M * p.grid_n;
-  const int group = bid / per_group;
-  const int first_m = group * GROUP_M;
-  const int gm = min(p.grid_m - first_m, GROUP_M);
-  const int bm = first_m + (bid % per_group) % gm;
-  const int bn = (bid % per_group) / gm;
+  // XCD-aware renumbering (each XCD gets a contiguous run of the launch's
+  // tiles), then the grouped order along M. Split launches take the splits
+  // of one tile as consecutive blocks.
+  int bid = blockIdx.x, split = 0;
+  if (p.ksplit > 1) {
+    split = bid % p.ksplit;
+    bid /= p.ksplit;
+  } else if ((p.n_tiles & 7) == 0) {
+    bid = (bid & 7) * (p.n_tiles >> 3) + (bid >> 3);
+  }
+  int bm, bn;
+  tile_coords(p.tile0 + bid, p.grid_m, p.grid_n, bm, bn);
   const int m0 = bm * BM;
   const int n0 = bn * BN;
 
@@ -356,20 +376,35 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
     __syncthreads();
   };
 
-  const int KT = p.K / BK;
-  issue_loads(0, As0, Bs0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  int kt = 0;
-  for (; kt + 1 < KT; kt += 2) {
-    step(kt, KT, std::integral_constant<int, 0>{});
-    step(kt + 1, KT, std::integral_constant<int, 1>{});
+  const int kt_begin = split * p.kt_per;
+  const int KT = min(p.K / BK, kt_begin + p.kt_per);
+  if (kt_begin < KT) {
+    issue_loads(kt_begin, As0, Bs0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int kt = kt_begin;
+    for (; kt + 1 < KT; kt += 2) {
+      step(kt, KT, std::integral_constant<int, 0>{});
+      step(kt + 1, KT, std::integral_constant<int, 1>{});
+    }
+    if (kt < KT) step(kt, KT, std::integral_constant<int, 0>{});
   }
-  if (kt < KT) step(kt, KT, std::integral_constant<int, 0>{});
 
   // ---- epilogue ----
   const int lrow = (lane >> 5) * 4;
   const int lcol = lane & 31;
+  if (p.ksplit > 1) {  // raw partial tile; the reduce kernel applies the epilogue
+    float* out = p.ws + (static_cast<int64_t>(bid) * p.ksplit + split) * (BM * BN);
+    auto tile = [&](auto ij) {
+      constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        out[(wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3)) * BN + wn * WN + j * 32 + lcol] =
+            acc[i][j][r];
+    };
+    StaticFor<0, TM * TN>::run(tile);
+    return;
+  }
   if constexpr (EPI == EPI_SWIGLU) {
     // B rows interleave 32 gate rows and 32 up rows, and a wave's column
     // range starts on a multiple of 64: tile j = 2q holds gate columns and
@@ -466,14 +501,153 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   }
 }
 
+// Sums the k-split partial tiles of a launch in split order and applies the
+// epilogue the whole-K kernel would have: one thread per 4 columns of a tile
+// row (for SwiGLU, per 4 act columns: gate and up sit 32 columns apart).
+template <int BM, int BN, int EPI, bool OUT_BF16>
+__global__ __launch_bounds__(256) void gemm_reduce(GemmParams p) {
+  constexpr int CW = EPI == EPI_SWIGLU ? BN / 2 : BN;  // output columns per tile
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t per_tile = static_cast<int64_t>(BM) * (CW / 4);
+  if (idx >= per_tile * p.n_tiles) return;
+  const int t = static_cast<int>(idx / per_tile);
+  const int rem = static_cast<int>(idx % per_tile);
+  const int r = rem / (CW / 4), c4 = (rem % (CW / 4)) * 4;
+  int bm, bn;
+  tile_coords(p.tile0 + t, p.grid_m, p.grid_n, bm, bn);
+  const int row = bm * BM + r;
+  if (row >= p.M) return;
+  const float* part = p.ws + static_cast<int64_t>(t) * p.ksplit * (BM * BN) + r * BN;
+  auto sum4 = [&](int c) {  // columns c .. c + 3 of the tile, splits in order
+    float4 a = *reinterpret_cast<const float4*>(part + c);
+    for (int sp = 1; sp < p.ksplit; ++sp) {
+      const float4 b = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(sp) * (BM * BN) + c);
+      a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    }
+    return a;
+  };
+  if constexpr (EPI == EPI_SWIGLU) {
+    const int gc = (c4 / 32) * 64 + c4 % 32;  // tile column of the gate
+    const float4 g4 = sum4(gc), u4 = sum4(gc + 32);
+    const float gs[4] = {g4.x, g4.y, g4.z, g4.w}, us[4] = {u4.x, u4.y, u4.z, u4.w};
+    uint16_t* act = static_cast<uint16_t*>(p.C);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int col = (bn * BN) / 2 + c4 + k;
+      const int gcol = bn * BN + gc + k;
+      if (col >= p.n_out) continue;
+      act[static_cast<int64_t>(row) * p.ldc + col] = f32_to_bf16(silu(gs[k]) * us[k]);
+      if (p.gu) {
+        p.gu[static_cast<int64_t>(row) * p.ldgu + gcol] = f32_to_bf16(gs[k]);
+        p.gu[static_cast<int64_t>(row) * p.ldgu + gcol + 32] = f32_to_bf16(us[k]);
+      }
+    }
+  } else {
+    const float4 v4 = sum4(c4);
+    const float vs[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int col = bn * BN + c4 + k;
+      if (col >= p.N) continue;
+      if constexpr (EPI == EPI_SWIGLU_BWD) {
+        const int gcol = (col >> 5) * 64 + (col & 31);
+        const int64_t o = static_cast<int64_t>(row) * p.ldgu + gcol;
+        const float g = bf16_to_f32(p.gu[o]), u = bf16_to_f32(p.gu[o + 32]);
+        const float sg = sigmoid(g);
+        const float dsilu = sg * (1.0f + g * (1.0f - sg));
+        uint16_t* dgu = static_cast<uint16_t*>(p.C);
+        const int64_t od = static_cast<int64_t>(row) * p.ldc + gcol;
+        dgu[od] = f32_to_bf16(vs[k] * u * dsilu);
+        dgu[od + 32] = f32_to_bf16(vs[k] * g * sg);
+      } else {
+        float x = vs[k] + (p.bias ? p.bias[col] : 0.0f);
+        if constexpr (EPI == EPI_RESID) x = p.resid[static_cast<int64_t>(row) * p.ldr + col] + x;
+        const int64_t o = static_cast<int64_t>(row) * p.ldc + col;
+        if constexpr (OUT_BF16) static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(x);
+        else static_cast<float*>(p.C)[o] = x;
+      }
+    }
+  }
+}
+
+// Partial-tile workspace for the k-split tails, one per device, allocated
+// on first use and kept for the life of the process.
+constexpr int64_t kSplitWsBytes = 128ll << 20;
+constexpr int kSplitMinKt = 96;
+float* split_workspace() {
+  static std::mutex mu;
+  static float* ws[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ws[dev]) {
+    void* q = nullptr;
+    if (hipMalloc(&q, kSplitWsBytes) != hipSuccess) return nullptr;
+    ws[dev] = static_cast<float*>(q);
+  }
+  return ws[dev];
+}
+
+// Large tiles go out in whole waves of 256 (one per CU). When K is long (at
+// least kSplitMinKt steps, so a tile takes far longer than the partial-tile
+// round trip), a remainder that would leave CUs idle in a last, partial wave
+// is cut along K instead: ksplit blocks per tile, chosen (up to 16) to
+// minimise the remainder's time in tile units, ceil(tail * ksplit / 256) /
+// ksplit, within the workspace. (Small tiles run two per CU and are not
+// split: measured, the split did not pay for them.)
 template <int BM, int BN, bool AK, bool BKM, int EPI, bool OB>
 int launch(GemmParams p, hipStream_t s) {
   p.grid_m = (p.M + BM - 1) / BM;
   p.grid_n = (p.N + BN - 1) / BN;
-  const int64_t blocks = static_cast<int64_t>(p.grid_m) * p.grid_n;
-  if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_gemm: problem too large");
+  const int64_t tiles = static_cast<int64_t>(p.grid_m) * p.grid_n;
+  if (tiles > 0x7fffffff) return fail(MR_EINVAL, "mr_gemm: problem too large");
+  const int KT = p.K / BK;
+  constexpr int64_t wave = 256;
+  const int64_t tail = tiles % wave, full = tiles - tail;
+  int split = 1;
+  if (BM == 256 && tail && KT >= kSplitMinKt) {
+    double best = 1.0;
+    for (int sp = 2; sp <= 16 && sp <= KT; ++sp) {
+      if (tail * sp * BM * BN * 4 > kSplitWsBytes) break;
+      const double t = static_cast<double>((tail * sp + wave - 1) / wave) / sp;
+      if (t < best - 1e-9) {
+        best = t;
+        split = sp;
+      }
+    }
+  }
+  float* ws = split > 1 ? split_workspace() : nullptr;
+  if (split > 1 && !ws) split = 1;
+  if (split == 1) {
+    p.tile0 = 0;
+    p.n_tiles = static_cast<int>(tiles);
+    p.ksplit = 1;
+    p.kt_per = KT;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BKM, EPI, OB>), dim3(static_cast<unsigned>(tiles)),
+                       dim3(kThreads), 0, s, p);
+    MR_LAUNCH_CHECK("mr_gemm");
+    return MR_OK;
+  }
+  if (full) {
+    GemmParams q = p;
+    q.tile0 = 0;
+    q.n_tiles = static_cast<int>(full);
+    q.ksplit = 1;
+    q.kt_per = KT;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BKM, EPI, OB>), dim3(static_cast<unsigned>(full)),
+                       dim3(kThreads), 0, s, q);
+  }
+  p.tile0 = static_cast<int>(full);
+  p.n_tiles = static_cast<int>(tail);
+  p.kt_per = (KT + split - 1) / split;
+  p.ksplit = (KT + p.kt_per - 1) / p.kt_per;  // no empty split
+  p.ws = ws;
   hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BKM, EPI, OB>),
-                     dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s, p);
+                     dim3(static_cast<unsigned>(tail * p.ksplit)), dim3(kThreads), 0, s, p);
+  constexpr int CW = EPI == EPI_SWIGLU ? BN / 2 : BN;
+  const int64_t threads = tail * BM * (CW / 4);
+  hipLaunchKernelGGL((gemm_reduce<BM, BN, EPI, OB>), dim3(static_cast<unsigned>((threads + 255) / 256)),
+                     dim3(256), 0, s, p);
   MR_LAUNCH_CHECK("mr_gemm");
   return MR_OK;
 }

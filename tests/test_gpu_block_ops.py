@@ -273,7 +273,9 @@ def test_cast_bf16(n, offset):
 
 # -------------------------------------------------------------- SwiGLU bwd --
 
-@pytest.mark.parametrize("mnk", [(256, 192, 128), (200, 96, 64), (1024, 4864, 896)])
+# 4096 x 4352 x 6144: 272 large tiles, the 16 past the wave take the k-split tail
+# (partials summed in order by the reduce kernel, which applies the SwiGLU backward)
+@pytest.mark.parametrize("mnk", [(256, 192, 128), (200, 96, 64), (1024, 4864, 896), (4096, 4352, 6144)])
 def test_swiglu_backward(mnk):
     M, N, Kd = mnk  # rows, intermediate, hidden
     dd = torch.randn(M, Kd, generator=_gen(51)).to(torch.bfloat16)
@@ -281,7 +283,13 @@ def test_swiglu_backward(mnk):
     g = (torch.randn(M, N, generator=_gen(53)) * 3).to(torch.bfloat16)
     u = torch.randn(M, N, generator=_gen(54)).to(torch.bfloat16)
     gu = torch.stack([g.reshape(M, N // 32, 32), u.reshape(M, N // 32, 32)], 2).reshape(M, 2 * N)
-    dact = dd.double() @ wd.double()
+    if M * N * Kd > 5e9:  # large case: float32 products on the GPU (their error counted twice)
+        ddf, wdf = dd.to(dev()).float(), wd.to(dev()).float()
+        dact = (ddf @ wdf).double().cpu()
+        abs_prod = (ddf.abs() @ wdf.abs()).double().cpu() * 2
+    else:
+        dact = dd.double() @ wd.double()
+        abs_prod = dd.double().abs() @ wd.double().abs()
     g64, u64 = g.double(), u.double()
     sg = torch.sigmoid(g64)
     dg_ref = dact * u64 * sg * (1 + g64 * (1 - sg))
@@ -291,7 +299,7 @@ def test_swiglu_backward(mnk):
     out = dgu.double().cpu().reshape(M, N // 32, 2, 32)
     got_g = out[:, :, 0, :].reshape(M, N)
     got_u = out[:, :, 1, :].reshape(M, N)
-    e_act = (dd.double().abs() @ wd.double().abs()) * Kd * 2.0**-23
+    e_act = abs_prod * Kd * 2.0**-23
     tol_g = 1.1 * e_act * u64.abs() + 1e-5 * (dact * u64).abs() + U * dg_ref.abs() + 1e-30
     tol_u = e_act * (g64 * sg).abs() + 1e-5 * du_ref.abs() + U * du_ref.abs() + 1e-30
     assert torch.all((got_g - dg_ref).abs() <= tol_g)

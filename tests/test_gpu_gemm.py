@@ -53,6 +53,95 @@ def test_gemm_layouts(layout, mnk, out):
     assert torch.all((got - ref).abs() <= tol), float(((got - ref).abs() / tol).max())
 
 
+# Large tiles: 4096 x 4096 is exactly one wave of 256 x 256 tiles (one launch).
+# 4352 x 4096 leaves a partial wave with a short K (not split); 256 x 384 and
+# 200 x 136 are small tiles over a long K (not split either). The k-split of
+# large tiles is covered below and by the SwiGLU and residual cases.
+@pytest.mark.parametrize("mnk", [(4096, 4096, 64), (4352, 4096, 640), (256, 384, 6144), (200, 136, 6208)])
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+def test_gemm_large_tiles_and_split_tail(mnk, layout):
+    M, N, Kd = mnk
+    print("case gemm large", layout, mnk, flush=True, file=sys.stderr)
+    if layout == "nt":
+        a, b = _rand(M, Kd, seed=21), _rand(N, Kd, seed=22)
+        a64, b64 = a.double(), b.double().t()
+    elif layout == "nn":
+        a, b = _rand(M, Kd, seed=25), _rand(Kd, N, seed=26)
+        a64, b64 = a.double(), b.double()
+    else:
+        a, b = _rand(Kd, M, seed=23), _rand(Kd, N, seed=24)
+        a64, b64 = a.double().t(), b.double()
+    ref = a64 @ b64
+    c = torch.empty(M, N, device=dev())
+    K.gemm(layout, a.to(dev()), b.to(dev()), c, M=M, N=N, K=Kd)
+    assert torch.all((c.double().cpu() - ref).abs() <= _bound(a64, b64, Kd))
+
+
+# The k-split tail of large tiles: 4096 x 4352 (or 4352 x 4096) x 6144 has 272
+# tiles of 256 x 256; the 16 past the wave are cut along K and their partials
+# summed in order by the reduce kernel, which also applies the epilogue.
+# References: float32 PyTorch products of the same bf16 inputs on the GPU
+# (their own accumulation error is within the K 2^-23 |A||B| bound used).
+SPLIT_M, SPLIT_N, SPLIT_K = 4096, 4352, 6144
+
+
+def _gpu_ref(a, b):
+    """float32 product and the bound 2 K 2^-23 |A||B| (a: [M, K], b: [K, N], on the GPU)."""
+    ref = a.float() @ b.float()
+    bound = (a.float().abs() @ b.float().abs()) * (2 * a.shape[1] * 2.0**-23) + 1e-30
+    return ref, bound
+
+
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_gemm_split_tail_large_tiles(layout, out):
+    M, N, Kd = (SPLIT_N, SPLIT_M, SPLIT_K) if layout == "tn" else (SPLIT_M, SPLIT_N, SPLIT_K)
+    print("case gemm split", layout, (M, N, Kd), out, flush=True, file=sys.stderr)
+    if layout == "nt":
+        a, b = _rand(M, Kd, seed=27).to(dev()), _rand(N, Kd, seed=28).to(dev())
+        ref, bound = _gpu_ref(a, b.t().contiguous())
+    elif layout == "nn":
+        a, b = _rand(M, Kd, seed=29).to(dev()), _rand(Kd, N, seed=30).to(dev())
+        ref, bound = _gpu_ref(a, b)
+    else:
+        a, b = _rand(Kd, M, seed=31).to(dev()), _rand(Kd, N, seed=32).to(dev())
+        ref, bound = _gpu_ref(a.t().contiguous(), b)
+    c = torch.empty(M, N, dtype=out, device=dev())
+    K.gemm(layout, a, b, c, M=M, N=N, K=Kd)
+    tol = bound + (ref.abs() * 2.0**-8 if out == torch.bfloat16 else 0)
+    assert bool(torch.all((c.float() - ref).abs() <= tol))
+
+
+def test_gemm_split_tail_bias_residual():
+    M, N, Kd = SPLIT_M, SPLIT_N, SPLIT_K
+    a, b = _rand(M, Kd, seed=33).to(dev()), _rand(N, Kd, seed=34).to(dev())
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(35)).to(dev())
+    resid = torch.randn(M, N, generator=torch.Generator().manual_seed(36)).to(dev())
+    prod, bound = _gpu_ref(a, b.t().contiguous())
+    ref = resid + (prod + bias)
+    c = torch.empty(M, N, device=dev())
+    K.gemm("nt", a, b, c, M=M, N=N, K=Kd, bias=bias, resid=resid)
+    assert bool(torch.all((c - ref).abs() <= bound + ref.abs() * 2.0**-22))
+
+
+def test_swiglu_split_tail():
+    M, N, Kd = SPLIT_M, SPLIT_N // 2, SPLIT_K
+    x = _rand(M, Kd, seed=37).to(dev())
+    wg, wu = _rand(N, Kd, seed=38), _rand(N, Kd, seed=39)
+    g, tg = _gpu_ref(x, wg.to(dev()).t().contiguous())
+    u, tu = _gpu_ref(x, wu.to(dev()).t().contiguous())
+    act = torch.empty(M, N, dtype=torch.bfloat16, device=dev())
+    gu = torch.empty(M, 2 * N, dtype=torch.bfloat16, device=dev())
+    K.gemm_swiglu(x, interleave_gate_up(wg, wu).to(dev()), act, gu)
+    gu_c = gu.float().reshape(M, N // 32, 2, 32)
+    got_g, got_u = gu_c[:, :, 0, :].reshape(M, N), gu_c[:, :, 1, :].reshape(M, N)
+    assert bool(torch.all((got_g - g).abs() <= tg + g.abs() * 2.0**-8))
+    assert bool(torch.all((got_u - u).abs() <= tu + u.abs() * 2.0**-8))
+    act_ref = torch.nn.functional.silu(g) * u
+    tol = 1.1 * tg * u.abs() + tu * torch.nn.functional.silu(g).abs() + act_ref.abs() * 2.0**-7 + 1e-6
+    assert bool(torch.all((act.float() - act_ref).abs() <= tol))
+
+
 def test_gemm_bias_and_residual():
     M, N, Kd = 304, 264, 128
     a, b = _rand(M, Kd, seed=7), _rand(N, Kd, seed=8)

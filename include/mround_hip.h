@@ -168,8 +168,12 @@ int mr_delta_loss(const void* w, int w_dtype, const float* g, int64_t rows, int6
  *        MR_NN: A = dY [M, K], B = W [K, N] (input gradient, dx = dy W)
  *        MR_TN: A = dY [K, M], B = X [K, N] (weight gradient, dW = dy^T x)
  * All row-major with leading dimensions lda/ldb/ldc/ldr in elements; M, N
- * multiples of 8, K a multiple of 32, operands 16-byte aligned. C is fp32 or
- * bf16; with resid (fp32) C is fp32. Replaces the matmul of the reference's
+ * multiples of 8, K a multiple of 64, operands 16-byte aligned. C is fp32 or
+ * bf16; with resid (fp32) C is fp32. Long-K problems whose 256 x 256 tiles
+ * leave a partial last wave sum that remainder from k-split partial tiles in
+ * a 128 MB device workspace the library allocates on the first such call on
+ * each GPU and keeps (the same for mr_gemm_swiglu and mr_gemm_swiglu_bwd);
+ * calls that overlap on one GPU share it, so issue them on one stream. Replaces the matmul of the reference's
  * tunable linear, `x @ weight.T` (mround/pipeline/runner.py:364-368), and the
  * two products MLX autodiff forms for its backward.
  */

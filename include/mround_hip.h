@@ -162,6 +162,45 @@ int mr_delta_loss(const void* w, int w_dtype, const float* g, int64_t rows, int6
                   double* scores_out, void* workspace, void* stream);
 
 /*
+ * The same accumulation with the gradient read through a row placement (as in
+ * mr_fq_forward_mapped: gradient row r at (r / block) * stride + offset +
+ * r % block; block 0 is the identity), and with MR_SYM_SEARCHED allowed:
+ * init_scales is then a host array of n_bits device pointers, each width's
+ * searched scale grid (rows, n_groups) fp32, and rtn_i quantizes with that
+ * scale (mround/pipeline/scoring.py:196-221, the searched grid at scoring
+ * time). init_scales may be NULL for the other modes.
+ */
+int mr_delta_loss_mapped(const void* w, int w_dtype, const float* g, int64_t rows, int64_t cols,
+                         int group_size, const int* bits_list, int n_bits, int mode, float eps,
+                         const float* const* init_scales, int64_t g_row_block,
+                         int64_t g_row_stride, int64_t g_row_offset, double* scores_out,
+                         void* workspace, void* stream);
+
+/*
+ * Causal-LM cross-entropy over bf16 logits rows (T, V) with leading dimension
+ * ld: row_loss[t] = logsumexp(logits[t]) - logits[t, labels[t]] (0 for a
+ * negative label, NaN for a label >= V), and, if loss_out is non-NULL,
+ * loss_out = scale * sum_t row_loss[t] (fixed-order fp64 sum). If dlogits is
+ * non-NULL it receives scale * (softmax(logits[t]) - onehot(labels[t])) as
+ * bf16 (zero rows for negative labels); dlogits may be the logits buffer.
+ * Replaces _causal_loss and its autodiff (mround/pipeline/scoring.py:183-192,
+ * 507-514): scale = 1 / number of labelled positions gives the mean.
+ */
+int mr_cross_entropy(const void* logits, int64_t ld, int64_t T, int64_t V, const int32_t* labels,
+                     float scale, float* row_loss, float* loss_out, void* dlogits, int64_t ldd,
+                     void* stream);
+
+/*
+ * Embedding lookup into the fp32 residual stream: out[t, :] = table[ids[t], :]
+ * (table (V, H) in dtype, leading dimension ldt; out leading dimension ldo).
+ * An id outside [0, V) yields a NaN row. Replaces the model's embedding
+ * lookup at the head of the scoring forward (mround/pipeline/scoring.py:190)
+ * and of the captured block-0 inputs (mround/pipeline/blocks.py:444-520).
+ */
+int mr_embed_rows(const void* table, int dtype, int64_t V, int64_t H, int64_t ldt,
+                  const int32_t* ids, int64_t T, float* out, int64_t ldo, void* stream);
+
+/*
  * bf16 GEMM on the MFMA cores, fp32 accumulation:
  *   C[m, n] = sum_k A(m, k) B(n, k) (+ bias[n]) (+ resid[m, n])
  * layout MR_NT: A = X [M, K], B = W [N, K]  (forward, y = x W^T)

@@ -1,20 +1,24 @@
-"""Public entry point: quantize a model and write an MLX checkpoint.
+"""Public entry points: quantize a model and write an MLX checkpoint, or plan
+a mixed-precision allocation.
 
-The surface of ``mround.api.quantize`` (mround/api.py:366-794) for local
-checkpoints on one MI355X: resolve the scheme, load the model onto the GPU,
-embed the calibration tokens into the block-0 input stream, tune every block
+The surface of ``mround.api.quantize`` (mround/api.py:366-794) and
+``plan_mixed_precision`` (api.py:943-1085) for local checkpoints on one
+MI355X: resolve the scheme, load the model onto the GPU, embed the
+calibration tokens into the block-0 input stream, tune every block
 (``QuantizationRunner``), round the tensors outside the blocks to nearest,
 write the MLX checkpoint (packed codes, scales, biases, config, index) and
-the run record. Mixed precision takes a ready ``plan`` (per-layer widths,
-e.g. from ``mround_amd.planner.allocator.allocate_bits``); the whole-model
-sensitivity pass that would produce one from ``average_bits`` is not part of
-this build and is refused with that reason.
+the run record. With ``average_bits`` a mixed run first scores every block
+layer at every candidate width with whole-model causal-LM gradients
+(``mround_amd.pipeline.scoring``) and allocates widths exactly under the
+budget the average implies (api.py:1471-1695), or checks and costs a given
+``plan`` (api.py:1698-1802).
 """
 
 from __future__ import annotations
 
 import dataclasses
 import json
+import math
 import time
 from collections.abc import Mapping, Sequence
 from pathlib import Path
@@ -24,15 +28,21 @@ import torch
 
 from mround_amd.core.quantizer import quantize_codes
 from mround_amd.core.scale_search import search_scales
-from mround_amd.exceptions import ArchitectureError, CalibrationError, UnsupportedSchemeError
+from mround_amd.exceptions import (ArchitectureError, CalibrationError, SchemeError,
+                                   UnsupportedSchemeError)
 from mround_amd.formats.mlx_export import (QuantizedLayer, export_mlx, narrow_codes,
                                            require_mlx_representable)
 from mround_amd.pipeline.checkpoint import DecoderModel, dense_tensors, load_model
 from mround_amd.pipeline.runner import QuantizationRunner, RunSummary
+from mround_amd.planner.allocator import allocate_bits
+from mround_amd.planner.sensitivity import (gradient_source_for, mixed_budget_bits,
+                                            score_layer_options, scoring_batch_size, storage_bits)
 from mround_amd.schemes import (LOW_BIT_THRESHOLD, QuantScheme, ScaleInit, Symmetry,
                                 TuningConfig)
 
 RUN_RECORD = "mround_run.json"
+SENSITIVITY_SAMPLES = 128  # mround/planner/sensitivity.py:91-92
+SENSITIVITY_SEQ_LEN = 1024
 
 
 @dataclasses.dataclass(frozen=True)
@@ -80,14 +90,160 @@ def default_scale_init(narrowest_width: int, symmetry: Symmetry) -> ScaleInit:
     return ScaleInit.SEARCHED if narrowest_width < LOW_BIT_THRESHOLD else ScaleInit.OBSERVED_RANGE
 
 
-def _resolve_scheme(*, bits, group_size, symmetry, plan, scheme, scale_init) -> tuple[QuantScheme, set[int]]:
+def _resolve_scheme(*, bits, group_size, symmetry, average_bits, candidate_bits, remainder_bits,
+                    scheme, scale_init) -> tuple[QuantScheme, set[int]]:
+    """The scheme a run resolves to and every width it can assign: the
+    candidates and the remainder's too when mixed (mround/api.py:1253-1288)."""
     widths = {scheme.bits if scheme is not None else bits}
-    if plan:
-        widths.update(int(b) for b in plan.values())
+    if average_bits is not None:
+        widths.update(int(b) for b in candidate_bits)
+        if remainder_bits is not None:
+            widths.add(int(remainder_bits))
     resolved = scheme or QuantScheme(
         bits=bits, group_size=group_size, symmetry=symmetry,
         scale_init=default_scale_init(min(widths), symmetry) if scale_init is None else ScaleInit(scale_init))
     return resolved, widths
+
+
+def _refuse_unusable_plan(plan, average_bits, candidate_bits) -> None:
+    """A given plan needs its average and widths on the menu (mround/api.py:311-346)."""
+    if plan is None:
+        return
+    if average_bits is None:
+        raise SchemeError("a given plan is a mixed run's allocation; pass average_bits too, which the "
+                          "plan is reported against and which sets the remainder's width")
+    if not plan:
+        raise SchemeError("a given plan must assign a width to every block layer; this one is empty")
+    menu = sorted({int(b) for b in candidate_bits})
+    off = sorted({(path, int(b)) for path, b in plan.items() if int(b) not in menu})
+    if off:
+        shown = ", ".join(f"{path} at {b}" for path, b in off[:4])
+        more = f" and {len(off) - 4} more" if len(off) > 4 else ""
+        raise SchemeError(f"a given plan may assign only widths in candidate_bits={menu}; it has {shown}{more}")
+
+
+def _remainder_width(average_bits: float, remainder_bits: int | None, base: QuantScheme) -> int:
+    """Nearest supported width to the average, ties toward more bits, unless
+    given (mround/api.py:1659-1667)."""
+    if remainder_bits is None:
+        return min(8, max(2, math.floor(average_bits + 0.5)))
+    base.with_bits(int(remainder_bits))  # validates
+    return int(remainder_bits)
+
+
+def _dtype_bits(model: DecoderModel) -> int:
+    return 16 if model.dtype in (torch.bfloat16, torch.float16) else 32
+
+
+def _plan_info(shapes, by_layer, widths, base, average_bits, remainder, dtype_bits, cost, budget):
+    elements = sum(o * i for o, i in shapes.values())
+    metadata = sum(2 * o * base.groups_per_row(i) * dtype_bits for o, i in shapes.values())
+    counts = {w: sum(1 for b in by_layer.values() if b == w) for w in widths}
+    return {
+        "average_bits": average_bits,
+        "candidate_bits": list(widths),
+        "achieved_code_bits": (cost - metadata) / elements,
+        "layers_by_width": {str(w): c for w, c in counts.items()},
+        "remainder_bits": remainder,
+        "budget_bits": budget,
+        "allocated_cost_bits": cost,
+        "assignments": {p: int(b) for p, b in sorted(by_layer.items())},
+    }
+
+
+def _given_plan(model: DecoderModel, base: QuantScheme, average_bits: float, candidate_bits, plan,
+                *, remainder_bits: int | None) -> tuple[dict[str, QuantScheme], dict[str, Any]]:
+    """Check a given plan against the layers a scored one would cover and cost
+    it (mround/api.py:1698-1802)."""
+    from mround_amd.pipeline.scoring import eligible_block_layers
+
+    widths = sorted({int(b) for b in candidate_bits})
+    eligible, _, _ = eligible_block_layers(model, base.group_size)
+    unknown = sorted(set(plan) - set(eligible))
+    missing = sorted(set(eligible) - set(plan))
+    if unknown or missing:
+        parts = []
+        if unknown:
+            parts.append(f"{len(unknown)} the run does not plan over, the first {unknown[0]}")
+        if missing:
+            parts.append(f"{len(missing)} left out, the first {missing[0]}")
+        raise SchemeError("a given plan must name exactly the block layers a scored plan would cover; "
+                          "this one names " + " and ".join(parts))
+    shapes = {p: (int(w.shape[0]), int(w.shape[1])) for p, w in eligible.items()}
+    dtype_bits = _dtype_bits(model)
+    by_layer = {p: int(plan[p]) for p in eligible}
+    cost = sum(storage_bits(shapes[p], b, base.group_size, dtype_bits=dtype_bits) for p, b in by_layer.items())
+    budget = mixed_budget_bits(shapes, average_bits, base.group_size, dtype_bits=dtype_bits)
+    remainder = _remainder_width(average_bits, remainder_bits, base)
+    info = _plan_info(shapes, by_layer, widths, base, average_bits, remainder, dtype_bits, cost, budget)
+    over = "" if cost <= budget else f", {cost - budget} bits over the budget"
+    summary = ", ".join(f"{c} layers at {w} bits" for w, c in info["layers_by_width"].items())
+    info.update(source="given", describe=f"given plan: {summary}; {info['achieved_code_bits']:.3f} code bits "
+                f"per weight against a target of {average_bits:g}{over}, remainder at {remainder} bits")
+    return {p: base.with_bits(b) for p, b in by_layer.items()}, info
+
+
+def _scoring_tokens(calibration, vocab: int, samples: int, sequence: int, *, seed: int, device):
+    if isinstance(calibration, torch.Tensor):
+        t = calibration.to(device=device, dtype=torch.int64)
+        if t.dim() != 2 or t.shape[0] < samples or t.shape[1] < sequence:
+            raise CalibrationError(f"scoring draws {samples} sequences of {sequence} tokens from the "
+                                   f"calibration ids, which are {tuple(t.shape)}; pass scoring_samples "
+                                   "and scoring_seq_len that fit")
+        return t[:samples, :sequence]
+    return calibration_tokens(vocab, samples, sequence, seed=seed, device=device)
+
+
+def _plan_mixed(model: DecoderModel, base: QuantScheme, average_bits: float, candidate_bits, calibration,
+                *, gradient_source: str = "auto", remainder_bits: int | None = None,
+                scoring_samples: int | None = None, scoring_seq_len: int | None = None,
+                scoring_batch: int | None = None, seed: int = 0, device="cuda",
+                progress=None) -> tuple[dict[str, QuantScheme], dict[str, Any]]:
+    """Score, allocate, and return per-layer schemes plus what was decided
+    (mround/api.py:1471-1695)."""
+    from mround_amd.pipeline.scoring import eligible_block_layers, score_widths
+
+    widths = sorted({int(b) for b in candidate_bits})
+    if not widths:
+        raise SchemeError("mixed precision needs at least one candidate width")
+    for w in widths:
+        base.with_bits(w)
+    if not widths[0] <= average_bits <= widths[-1]:
+        raise SchemeError(f"average_bits={average_bits} is outside the achievable range "
+                          f"[{widths[0]}, {widths[-1]}] for candidate_bits={widths}")
+    if scoring_batch is not None and int(scoring_batch) < 1:
+        raise SchemeError(f"scoring_batch_size must be at least 1, or None; got {scoring_batch}")
+    eligible, _, _ = eligible_block_layers(model, base.group_size)
+    scored_weights = sum(int(w.numel()) for w in eligible.values())
+    requested = gradient_source
+    gradient_source = gradient_source_for(requested, scored_weights)
+    samples = SENSITIVITY_SAMPLES if scoring_samples is None else int(scoring_samples)
+    sequence = SENSITIVITY_SEQ_LEN if scoring_seq_len is None else int(scoring_seq_len)
+    batch = (scoring_batch_size(samples, sequence) if scoring_batch is None
+             else max(1, min(samples, int(scoring_batch))))
+    tokens = _scoring_tokens(calibration, int(model.config["vocab_size"]), samples, sequence, seed=seed,
+                             device=device)
+    batches = [tokens[i:i + batch] for i in range(0, samples, batch)]
+    scored = score_widths(model, batches, widths, base, gradient_source=gradient_source, progress=progress)
+    dtype_bits = _dtype_bits(model)
+    options = score_layer_options(scored.scores, scored.shapes, base, dtype_bits=dtype_bits)
+    budget = mixed_budget_bits(scored.shapes, average_bits, base.group_size, dtype_bits=dtype_bits)
+    allocation = allocate_bits(options, budget_bits=budget)
+    remainder = _remainder_width(average_bits, remainder_bits, base)
+    info = _plan_info(scored.shapes, allocation.by_layer, widths, base, average_bits, remainder, dtype_bits,
+                      allocation.total_cost_bits, budget)
+    summary = ", ".join(f"{c} layers at {w} bits" for w, c in info["layers_by_width"].items())
+    info.update(
+        source="scored", predicted_loss=allocation.predicted_loss, scoring_seconds=round(scored.seconds, 1),
+        scoring_samples=samples, scoring_seq_len=sequence, scoring_batch_size=batch,
+        gradient_source=gradient_source, gradient_source_requested=requested,
+        scored_weights=scored_weights,
+        describe=(f"planned {summary}; {info['achieved_code_bits']:.3f} code bits per weight against a "
+                  f"target of {average_bits:g}, remainder at {remainder} bits, scored {samples}x{sequence} "
+                  f"in {scored.seconds:.1f}s with gradients at "
+                  f"{'the widest width' if gradient_source == 'widest' else 'each own width'}"
+                  + (f", by size at {scored_weights / 1e9:.2f} billion weights" if requested == "auto" else "")))
+    return {p: base.with_bits(b) for p, b in allocation.by_layer.items()}, info
 
 
 def calibration_tokens(vocab: int, n_samples: int, seq_len: int, *, seed: int, device) -> torch.Tensor:
@@ -139,38 +295,7 @@ def _storage(model: DecoderModel, quantized: Mapping[str, QuantizedLayer]) -> St
     return Storage(total, params, float(dtype_bits))
 
 
-def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_size: int = 64,
-             symmetry: Symmetry = Symmetry.SYMMETRIC, average_bits: float | None = None,
-             dense_remainder: bool = False, scheme: QuantScheme | None = None,
-             tuning: TuningConfig | None = None, calibration: str | torch.Tensor = "random",
-             export_format: str = "mlx", quantized_inputs: bool = True, holdout_batches: int = 0,
-             per_layer_recipe: bool = False, plan: Mapping[str, int] | None = None,
-             scale_init: ScaleInit | str | None = None, seed: int | None = None,
-             device: str = "cuda", progress=None) -> QuantizeResult:
-    """Quantize the local checkpoint ``model`` into ``output_dir``.
-
-    ``calibration`` is ``"random"`` (token ids uniform over the vocabulary) or
-    a ``[n_samples, seq_len]`` tensor of token ids; ``plan`` maps block layer
-    paths to widths. Raises the reference's exceptions for unrepresentable
-    schemes, bad calibration and unsupported architectures.
-    """
-    started = time.perf_counter()
-    if export_format != "mlx":
-        raise UnsupportedSchemeError(f"export format {export_format!r} is not supported; only 'mlx'")
-    if average_bits is not None:
-        raise UnsupportedSchemeError(
-            "average_bits needs the whole-model sensitivity scoring pass, which this build does not "
-            "include; pass plan= (layer path -> width, e.g. from planner.allocator.allocate_bits)")
-    resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry, plan=plan,
-                                       scheme=scheme, scale_init=scale_init)
-    for w in sorted(widths):
-        require_mlx_representable(resolved.with_bits(w))
-    tuning = tuning or TuningConfig()
-    seed = 0 if seed is None else int(seed)
-    t0 = time.perf_counter()
-    m = load_model(model, device=device)
-    load_s = time.perf_counter() - t0
-
+def _load_tokens(m: DecoderModel, calibration, tuning: TuningConfig, seed: int, device) -> torch.Tensor:
     vocab = int(m.config["vocab_size"])
     if isinstance(calibration, torch.Tensor):
         tokens = calibration.to(device=device, dtype=torch.int64)
@@ -178,11 +303,54 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
             raise CalibrationError("calibration token ids must be [n_samples, seq_len]")
         if tokens.numel() and (int(tokens.min()) < 0 or int(tokens.max()) >= vocab):
             raise CalibrationError(f"calibration token ids must lie in [0, {vocab})")
-    elif calibration == "random":
+    elif calibration in ("random", "auto"):
         tokens = calibration_tokens(vocab, tuning.n_samples, tuning.seq_len, seed=seed, device=device)
     else:
         raise CalibrationError(f"calibration {calibration!r} needs a text corpus, which is not "
                                "available offline; pass 'random' or a tensor of token ids")
+    return tokens
+
+
+def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_size: int = 64,
+             symmetry: Symmetry = Symmetry.SYMMETRIC, average_bits: float | None = None,
+             candidate_bits: Sequence[int] = (2, 3, 4), sensitivity_gradients: str = "auto",
+             remainder_bits: int | None = None, dense_remainder: bool = False,
+             scoring_samples: int | None = None, scoring_seq_len: int | None = None,
+             scoring_batch_size: int | None = None, scheme: QuantScheme | None = None,
+             tuning: TuningConfig | None = None, calibration: str | torch.Tensor = "random",
+             export_format: str = "mlx", quantized_inputs: bool = True, holdout_batches: int = 0,
+             per_layer_recipe: bool = False, plan: Mapping[str, int] | None = None,
+             scale_init: ScaleInit | str | None = None, seed: int | None = None,
+             device: str = "cuda", progress=None, scoring_progress=None) -> QuantizeResult:
+    """Quantize the local checkpoint ``model`` into ``output_dir``.
+
+    ``calibration`` is ``"random"`` (``"auto"`` is the same here: token ids
+    uniform over the vocabulary, since no text corpus is available offline)
+    or a ``[n_samples, seq_len]`` tensor of token ids. ``average_bits``
+    engages the planner: a whole-model scoring pass over ``candidate_bits``
+    and an exact allocation (or, with ``plan``, the given per-layer widths),
+    the block layers tuned at their assigned widths and the remainder at
+    ``remainder_bits`` (default: the width nearest the average, ties up).
+    Raises the reference's exceptions for unrepresentable schemes, bad
+    calibration, unusable plans and unsupported architectures.
+    """
+    started = time.perf_counter()
+    if export_format != "mlx":
+        raise UnsupportedSchemeError(f"export format {export_format!r} is not supported; only 'mlx'")
+    if holdout_batches < 0:
+        raise CalibrationError(f"holdout_batches must be zero or more, got {holdout_batches}")
+    _refuse_unusable_plan(plan, average_bits, candidate_bits)
+    resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry,
+                                       average_bits=average_bits, candidate_bits=candidate_bits,
+                                       remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
+    for w in sorted(widths):
+        require_mlx_representable(resolved.with_bits(w))
+    tuning = tuning or TuningConfig()
+    seed = 0 if seed is None else int(seed)
+    t0 = time.perf_counter()
+    m = load_model(model, device=device)
+    load_s = time.perf_counter() - t0
+    tokens = _load_tokens(m, calibration, tuning, seed, device)
     if tokens.shape[1] != tuning.seq_len:
         raise CalibrationError(f"calibration sequences have {tokens.shape[1]} tokens, tuning.seq_len "
                                f"is {tuning.seq_len}")
@@ -191,15 +359,29 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
                                f"{tuning.batch_size}")
 
     schemes_by_layer = None
-    if plan:
-        schemes_by_layer = {p: resolved.with_bits(int(b)) for p, b in plan.items()}
+    mixed = None
+    remainder_scheme = resolved
+    plan_s = 0.0
+    if average_bits is not None:
+        tp = time.perf_counter()
+        if plan is not None:
+            schemes_by_layer, mixed = _given_plan(m, resolved, average_bits, candidate_bits, plan,
+                                                  remainder_bits=remainder_bits)
+        else:
+            schemes_by_layer, mixed = _plan_mixed(
+                m, resolved, average_bits, candidate_bits, calibration,
+                gradient_source=sensitivity_gradients, remainder_bits=remainder_bits,
+                scoring_samples=scoring_samples, scoring_seq_len=scoring_seq_len,
+                scoring_batch=scoring_batch_size, seed=seed, device=device, progress=scoring_progress)
+        remainder_scheme = resolved.with_bits(int(mixed["remainder_bits"]))
+        plan_s = time.perf_counter() - tp
     runner = QuantizationRunner(resolved, tuning, progress=progress, quantized_inputs=quantized_inputs,
                                 holdout_batches=holdout_batches, per_layer_recipe=per_layer_recipe)
     entrance = _entrance(m, tokens, tuning.batch_size)
     summary, quantized = runner.run(m.blocks, entrance, scheme_by_layer=schemes_by_layer)
     del entrance
     t1 = time.perf_counter()
-    remainder, skipped = _round_to_nearest(m, resolved, dense=dense_remainder)
+    remainder, skipped = _round_to_nearest(m, remainder_scheme, dense=dense_remainder)
     quantized.update(remainder)
     if not quantized:
         raise ArchitectureError(f"nothing in {model!r} could be quantized at group_size={group_size}")
@@ -211,8 +393,8 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     export_mlx(out, dense_weights=dense, quantized=quantized, config=m.config, dtype=dtype_name)
     t3 = time.perf_counter()
     storage = _storage(m, quantized)
-    seconds = {"load": load_s, "blocks": summary.total_seconds, "remainder": t2 - t1, "export": t3 - t2,
-               "total": t3 - started}
+    seconds = {"load": load_s, "plan": plan_s, "blocks": summary.total_seconds, "remainder": t2 - t1,
+               "export": t3 - t2, "total": t3 - started}
     record = {
         "model": str(model),
         "scheme": {"bits": resolved.bits, "group_size": resolved.group_size,
@@ -220,7 +402,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         "tuning": dataclasses.asdict(tuning),
         "calibration": "random" if not isinstance(calibration, torch.Tensor) else "tokens",
         "seed": seed,
-        "plan": dict(plan) if plan else None,
+        "mixed": mixed,
         "quantized_inputs": quantized_inputs,
         "holdout_batches": holdout_batches,
         "blocks": [{"index": b.index, "name": b.name, "initial_loss": b.initial_loss,
@@ -233,4 +415,31 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     config_path = out / RUN_RECORD
     config_path.write_text(json.dumps(record, indent=2) + "\n")
     return QuantizeResult(out, summary, dict(summary.scheme_by_layer), config_path, storage,
-                          tuple(skipped), None, seconds)
+                          tuple(skipped), mixed, seconds)
+
+
+def plan_mixed_precision(model: str | Path, average_bits: float, candidate_bits: Sequence[int] = (2, 3, 4),
+                         *, bits: int = 4, group_size: int = 64, symmetry: Symmetry = Symmetry.SYMMETRIC,
+                         scale_init: ScaleInit | str | None = None, scheme: QuantScheme | None = None,
+                         calibration: str | torch.Tensor = "random", sensitivity_gradients: str = "auto",
+                         remainder_bits: int | None = None, scoring_samples: int | None = None,
+                         scoring_seq_len: int | None = None, scoring_batch_size: int | None = None,
+                         seed: int | None = None, device: str = "cuda", progress=None) -> dict[str, Any]:
+    """Score and allocate, and stop there: nothing is tuned or written
+    (mround/api.py:943-1085). Returns the plan summary, whose
+    ``assignments`` map each block layer path to its width."""
+    resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry,
+                                       average_bits=average_bits, candidate_bits=candidate_bits,
+                                       remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
+    for w in sorted(widths):
+        require_mlx_representable(resolved.with_bits(w))
+    if isinstance(calibration, str) and calibration not in ("random", "auto"):
+        raise CalibrationError(f"calibration {calibration!r} needs a text corpus, which is not "
+                               "available offline; pass 'random' or a tensor of token ids")
+    m = load_model(model, device=device)
+    _, info = _plan_mixed(m, resolved, average_bits, candidate_bits, calibration,
+                          gradient_source=sensitivity_gradients, remainder_bits=remainder_bits,
+                          scoring_samples=scoring_samples, scoring_seq_len=scoring_seq_len,
+                          scoring_batch=scoring_batch_size, seed=0 if seed is None else int(seed),
+                          device=device, progress=progress)
+    return info

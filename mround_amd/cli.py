@@ -36,6 +36,10 @@ def _parser() -> argparse.ArgumentParser:
     q.add_argument("-g", "--group-size", type=int, default=64)
     q.add_argument("--asym", action="store_true", help="asymmetric codes with a zero point")
     q.add_argument("--average-bits", type=float, default=None)
+    q.add_argument("--options", default="2,3,4",
+                   help="candidate widths for --average-bits, comma separated (default: 2,3,4)")
+    q.add_argument("--remainder-bits", type=int, default=None,
+                   help="width for the tensors outside the block stack (default: nearest the average)")
     q.add_argument("--plan", default=None, help="JSON file mapping layer paths to widths")
     q.add_argument("--format", default="mlx")
     q.add_argument("--iters", type=int, default=None)
@@ -53,6 +57,14 @@ def _parser() -> argparse.ArgumentParser:
     r.add_argument("--seed", type=int, default=0)
     r.add_argument("--device", default="cuda")
     return p
+
+
+def _widths(options: str) -> tuple[int, ...]:
+    """``--options`` as candidate widths (mround/cli/main.py:439-451)."""
+    try:
+        return tuple(int(piece) for piece in options.split(",") if piece.strip())
+    except ValueError:
+        raise ValueError(f"--options must be comma separated integers, not {options!r}") from None
 
 
 def _tuning(args):
@@ -90,14 +102,18 @@ def main(argv=None) -> int:
         result = api.quantize(args.model, output_dir=args.output_dir, bits=args.bits,
                               group_size=args.group_size,
                               symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
-                              average_bits=args.average_bits, plan=plan, tuning=_tuning(args),
+                              average_bits=args.average_bits, candidate_bits=_widths(args.options),
+                              remainder_bits=args.remainder_bits, plan=plan, tuning=_tuning(args),
                               calibration=args.calibration, export_format=args.format,
                               dense_remainder=args.allow_dense, seed=args.seed,
                               progress=lambda b: print(f"  block {b.index}: loss {b.initial_loss:.4g} -> "
-                                                       f"{b.final_loss:.4g} in {b.seconds:.2f} s", flush=True))
+                                                       f"{b.final_loss:.4g} in {b.seconds:.2f} s", flush=True),
+                              scoring_progress=lambda step: print(step.describe(), flush=True))
     except (MRoundError, ValueError) as exc:
         print(f"mround: {exc}", file=sys.stderr)
         return 1
+    if result.mixed:
+        print(f"  {result.mixed['describe']}")
     print(f"  {result.describe()}")
     for path, reason in result.skipped:
         print(f"  left dense  {path}: {reason}")

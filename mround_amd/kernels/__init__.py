@@ -25,8 +25,11 @@ from mround_amd.exceptions import KernelError, KernelUnavailableError
 __all__ = [
     "MODE",
     "copy_bytes",
+    "cross_entropy",
     "delta_loss",
+    "delta_loss_mapped",
     "dtype_code",
+    "embed_rows",
     "fq_backward_signsgd",
     "fq_forward",
     "lib",
@@ -88,6 +91,10 @@ _SIGNATURES = {
                                   _L, _P]),
     "mr_fq_backward_signsgd_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F,
                                            _F, _F, _F, _F, _L, _L, _L, _P]),
+    "mr_delta_loss_mapped": (_I, [_P, _I, _P, _L, _L, _I, _P, _I, _I, _F, _P, _L, _L, _L, _P, _P,
+                                  _P]),
+    "mr_cross_entropy": (_I, [_P, _L, _L, _L, _P, _F, _P, _P, _P, _L, _P]),
+    "mr_embed_rows": (_I, [_P, _I, _L, _L, _L, _P, _L, _P, _L, _P]),
 }
 
 
@@ -245,10 +252,8 @@ def loss_outlier(pred, target, *, k, denom, loss_out, threshold_in=None, thresho
 
 # ------------------------------------------------------------- sensitivity --
 
-def delta_loss(weight, grad, *, group_size, bits_list, mode, eps, scores_out, workspace=None) -> None:
+def _delta_workspace(weight, n_bits: int, workspace):
     rows, cols = weight.shape
-    n_bits = len(bits_list)
-    arr = (ctypes.c_int * n_bits)(*bits_list)
     nbytes = int(lib().mr_delta_loss_workspace_bytes(rows, cols, n_bits))
     if workspace is None:
         key = (weight.device.index or 0, "delta")
@@ -256,12 +261,79 @@ def delta_loss(weight, grad, *, group_size, bits_list, mode, eps, scores_out, wo
         if workspace is None or workspace.numel() < nbytes:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
             _workspaces[key] = workspace
+    return workspace
+
+
+def delta_loss(weight, grad, *, group_size, bits_list, mode, eps, scores_out, workspace=None) -> None:
+    rows, cols = weight.shape
+    n_bits = len(bits_list)
+    arr = (ctypes.c_int * n_bits)(*bits_list)
+    workspace = _delta_workspace(weight, n_bits, workspace)
     if scores_out.dtype != torch.float64:
         raise KernelError("scores_out must be float64")
     rc = lib().mr_delta_loss(_ptr(weight), dtype_code(weight.dtype), _ptr(_f32(grad, "grad")), rows,
                              cols, group_size, arr, n_bits, MODE[mode], eps, _ptr(scores_out),
                              _ptr(workspace), _stream(weight))
     _check(rc, "mr_delta_loss")
+
+
+def delta_loss_mapped(weight, grad, *, group_size, bits_list, mode, eps, scores_out, grids=None,
+                      row_block=0, row_stride=0, row_offset=0, workspace=None) -> None:
+    """``mr_delta_loss_mapped``: ``grad`` is the placed gradient buffer (its rows
+    at the placement), ``grids`` one (rows, n_groups) fp32 scale grid per width
+    for the searched mode."""
+    rows, cols = weight.shape
+    n_bits = len(bits_list)
+    arr = (ctypes.c_int * n_bits)(*bits_list)
+    grid_arr = None
+    if grids is not None:
+        if len(grids) != n_bits:
+            raise KernelError("one scale grid per width")
+        grid_arr = (ctypes.c_void_p * n_bits)(*[_ptr(_f32(g, "grid")) for g in grids])
+    if grad.shape[1] != cols or not grad.is_contiguous():
+        raise KernelError("the placed gradient must be contiguous with the weight's column count")
+    last = ((rows - 1) // row_block) * row_stride + row_offset + (rows - 1) % row_block if row_block else rows - 1
+    if last >= grad.shape[0]:
+        raise KernelError(f"the placement reaches gradient row {last}, past the {grad.shape[0]} rows given")
+    if scores_out.dtype != torch.float64:
+        raise KernelError("scores_out must be float64")
+    workspace = _delta_workspace(weight, n_bits, workspace)
+    rc = lib().mr_delta_loss_mapped(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(grad, "grad")), rows, cols, group_size, arr,
+        n_bits, MODE[mode], eps, grid_arr, row_block, row_stride, row_offset, _ptr(scores_out),
+        _ptr(workspace), _stream(weight))
+    _check(rc, "mr_delta_loss_mapped")
+
+
+# ------------------------------------------------------------- LM head ends --
+
+def cross_entropy(logits, labels, *, V, scale, row_loss, loss_out=None, dlogits=None) -> None:
+    """``mr_cross_entropy`` over bf16 logits rows ``[T, >=V]``; int32 labels."""
+    if logits.dtype != torch.bfloat16 or (dlogits is not None and dlogits.dtype != torch.bfloat16):
+        raise KernelError("cross-entropy logits and their gradient are bf16")
+    if labels.dtype != torch.int32:
+        raise KernelError("labels must be int32")
+    T = logits.shape[0]
+    if labels.numel() != T or row_loss.numel() < T:
+        raise KernelError("one label and one row loss per logits row")
+    rc = lib().mr_cross_entropy(_ptr(logits), logits.stride(0), T, V, _ptr(labels), scale,
+                                _ptr(_f32(row_loss, "row_loss")), _ptr(_f32(loss_out, "loss")),
+                                _ptr(dlogits), dlogits.stride(0) if dlogits is not None else 0,
+                                _stream(logits))
+    _check(rc, "mr_cross_entropy")
+
+
+def embed_rows(table, ids, out) -> None:
+    """``mr_embed_rows``: ``out[t] = table[ids[t]]`` as fp32; int32 ids."""
+    if ids.dtype != torch.int32:
+        raise KernelError("token ids must be int32")
+    V, H = table.shape
+    T = ids.numel()
+    if out.shape[0] < T or out.shape[1] != H:
+        raise KernelError(f"embedding output must be [{T}, {H}]")
+    rc = lib().mr_embed_rows(_ptr(table), dtype_code(table.dtype), V, H, table.stride(0), _ptr(ids), T,
+                             _ptr(_f32(out, "out")), out.stride(0), _stream(table))
+    _check(rc, "mr_embed_rows")
 
 
 # -------------------------------------------------------------------- GEMM --

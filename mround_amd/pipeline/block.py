@@ -205,8 +205,26 @@ class BlockEngine:
         self.scale = 1.0 / math.sqrt(shape.head_dim)
         self.place = placements(shape)
         self.loss_ws = K.loss_workspace(self.device, T * h)
+        self.x_in: torch.Tensor | None = None  # block input of the last saving forward
+        self.dh32: torch.Tensor | None = None  # fp32 residual gradient, for input gradients
         # name -> [(start, end) HIP events] for the launches being timed, or None
         self.timers: dict[str, list] | None = None
+
+    # What a forward(save=True) leaves for the backward, besides its input.
+    ACTIVATIONS = ("x1", "rstd1", "qkv", "attn", "lse", "h2", "x2", "rstd2", "act", "gu")
+
+    def new_activations(self) -> dict[str, torch.Tensor]:
+        """A fresh set of the saved-activation buffers, for keeping several
+        blocks' activations at once (see ``bind``)."""
+        return {n: torch.empty_like(getattr(self, n)) for n in self.ACTIVATIONS}
+
+    def bind(self, acts: dict[str, torch.Tensor], x_in: torch.Tensor | None = None) -> None:
+        """Make ``acts`` the saved-activation buffers that the next forward
+        writes and the next backward reads, and ``x_in`` the block input that
+        they were saved from (kept unchanged by the caller)."""
+        for n in self.ACTIVATIONS:
+            setattr(self, n, acts[n])
+        self.x_in = x_in
 
     def _run(self, name: str, fn) -> None:
         """Launch ``fn``; bracket it with events on the current stream when timed."""
@@ -242,7 +260,7 @@ class BlockEngine:
             "gemm_dact": 2.0 * T * mlp * h, "gemm_dw_down": 2.0 * h * mlp * T,
             "gemm_dx_gate_up": 2.0 * T * h * 2 * mlp, "gemm_dw_gate_up": 2.0 * 2 * mlp * h * T,
             "gemm_dattn": 2.0 * T * hq_d * h, "gemm_dw_o": 2.0 * h * hq_d * T,
-            "gemm_dw_qkv": 2.0 * q * h * T,
+            "gemm_dw_qkv": 2.0 * q * h * T, "gemm_dx_qkv": 2.0 * T * h * q,
         }
 
     # ---------------------------------------------------------------- weights --
@@ -272,6 +290,10 @@ class BlockEngine:
         if x.shape != (T, s.hidden) or out.shape != (T, s.hidden):
             raise ArchitectureError(f"block input must be [{T}, {s.hidden}]")
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
+        if save:
+            if out.data_ptr() == x.data_ptr():
+                raise ArchitectureError("a saving forward needs its input kept: out must not be x")
+            self.x_in = x
         K.rmsnorm_fwd(x, self.norm_in, s.norm_eps, self.x1, self.rstd1)
         self._run("gemm_qkv", lambda: K.gemm("nt", self.x1, self.wq["qkv"], self.qkv, M=T, N=s.qkv_rows,
                                              K=h, bias=self.bias_qkv))
@@ -303,10 +325,21 @@ class BlockEngine:
         return self.loss_val
 
     # --------------------------------------------------------------- backward --
-    def backward(self) -> None:
+    def backward(self, dx_out: torch.Tensor | None = None) -> None:
         """dL/dW' of all seven layers into ``self.dw`` from ``self.grad_out``
-        (after ``forward(save=True)`` and ``loss(with_grad=True)``)."""
+        (after ``forward(save=True)`` and ``loss(with_grad=True)``, or with
+        ``grad_out`` filled by the caller). With ``dx_out`` (float32 ``[T, h]``,
+        not ``grad_out``) also the gradient with respect to the block input."""
         s, T = self.shape, self.tokens
+        if dx_out is not None:
+            if self.x_in is None:
+                raise ArchitectureError("the input gradient needs a saving forward first")
+            if dx_out.shape != (T, s.hidden) or dx_out.dtype != torch.float32:
+                raise ArchitectureError(f"dx_out must be float32 [{T}, {s.hidden}]")
+            if dx_out.data_ptr() == self.grad_out.data_ptr():
+                raise ArchitectureError("dx_out must not be the output gradient buffer")
+            if self.dh32 is None:
+                self.dh32 = torch.empty(T, s.hidden, dtype=torch.float32, device=self.device)
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
         K.cast_bf16(self.grad_out, self.grad_out16)
         # MLP: dgu from dact = dout Wd'; dWd' = dout^T act; dx2 = dgu Wgu'; dWgu' = dgu^T x2
@@ -319,7 +352,8 @@ class BlockEngine:
         self._run("gemm_dw_gate_up", lambda: K.gemm("tn", self.dgu, self.x2, self.dw["gu"], M=2 * mlp,
                                                     N=h, K=T))
         # dh = dout + rmsnorm'(dx2)
-        K.rmsnorm_bwd(self.dx2, self.h2, self.norm_post, self.rstd2, self.grad_out, dh_bf16=self.dh2)
+        K.rmsnorm_bwd(self.dx2, self.h2, self.norm_post, self.rstd2, self.grad_out, dh_bf16=self.dh2,
+                      dh_f32=self.dh32 if dx_out is not None else None)
         # attention output projection
         self._run("gemm_dattn", lambda: K.gemm("nn", self.dh2, self.wq["o"], self.dattn, M=T, N=hq_d,
                                                K=h))
@@ -333,3 +367,9 @@ class BlockEngine:
                head_dim=s.head_dim, cos_sin=self.cos_sin, backward=True)
         self._run("gemm_dw_qkv", lambda: K.gemm("tn", self.dqkv, self.x1, self.dw["qkv"], M=s.qkv_rows,
                                                 N=h, K=T))
+        if dx_out is None:
+            return
+        # dx = dh + rmsnorm'(dqkv Wqkv'); dx2 is free again and holds dx1.
+        self._run("gemm_dx_qkv", lambda: K.gemm("nn", self.dqkv, self.wq["qkv"], self.dx2, M=T, N=h,
+                                                K=s.qkv_rows))
+        K.rmsnorm_bwd(self.dx2, self.x_in, self.norm_in, self.rstd1, self.dh32, dh_f32=dx_out)

@@ -8,9 +8,9 @@ import torch
 
 from mround_amd import api
 from mround_amd.cli import GEOMETRIES, main
-from mround_amd.exceptions import ArchitectureError, CalibrationError, UnsupportedSchemeError
+from mround_amd.exceptions import ArchitectureError, CalibrationError, SchemeError, UnsupportedSchemeError
 from mround_amd.pipeline.checkpoint import block_shape, dense_tensors, load_model, write_random_checkpoint
-from mround_amd.schemes import ScaleInit, Symmetry
+from mround_amd.schemes import ScaleInit, Symmetry, TuningConfig
 
 TINY = dict(model_type="qwen2", hidden_size=128, num_attention_heads=2, num_key_value_heads=1,
             intermediate_size=256, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=2,
@@ -54,8 +54,18 @@ def test_default_scale_init_rule():
 
 def test_quantize_refusals(tmp_path):
     write_random_checkpoint(tmp_path / "m", TINY)
-    with pytest.raises(UnsupportedSchemeError, match="sensitivity"):
-        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", average_bits=2.5, device="cpu")
+    with pytest.raises(SchemeError, match="pass average_bits too"):
+        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", plan={"a": 2}, device="cpu")
+    with pytest.raises(SchemeError, match="empty"):
+        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", average_bits=3, plan={}, device="cpu")
+    with pytest.raises(SchemeError, match="candidate_bits"):
+        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", average_bits=3, plan={"a": 5}, device="cpu")
+    with pytest.raises(SchemeError, match="outside the achievable range"):
+        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", average_bits=4.5, device="cpu",
+                     tuning=TuningConfig(n_samples=2, batch_size=2, seq_len=128))
+    with pytest.raises(UnsupportedSchemeError):
+        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", average_bits=3, candidate_bits=(2, 7),
+                     device="cpu")
     with pytest.raises(UnsupportedSchemeError, match="format"):
         api.quantize(tmp_path / "m", output_dir=tmp_path / "o", export_format="gguf", device="cpu")
     with pytest.raises(UnsupportedSchemeError):
@@ -68,5 +78,6 @@ def test_cli_random_model_and_errors(tmp_path, capsys):
     assert main(["random-model", "smollm2-135m", str(tmp_path / "s"), "--layers", "1", "--device", "cpu"]) == 0
     m = load_model(tmp_path / "s", device="cpu")
     assert len(m.blocks) == 1 and m.blocks[0].shape.n_heads == 9
-    assert main(["quantize", str(tmp_path / "s"), "-o", str(tmp_path / "o"), "--average-bits", "2.5"]) == 1
-    assert "sensitivity" in capsys.readouterr().err
+    assert main(["quantize", str(tmp_path / "s"), "-o", str(tmp_path / "o"), "--average-bits", "2.5",
+                 "--options", "2,x"]) == 1
+    assert "--options must be comma separated" in capsys.readouterr().err

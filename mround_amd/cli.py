@@ -1,7 +1,8 @@
 """Command line: ``python -m mround_amd quantize MODEL -o OUT ...`` (the
 ``mround quantize`` subcommand of mround/cli/main.py:66-200, for local
-checkpoints), and ``random-model`` to write a random-initialised checkpoint
-of a named geometry."""
+checkpoints), ``plan`` (``mround.api.plan_mixed_precision``, api.py:943-1085:
+score and allocate only), and ``random-model`` to write a random-initialised
+checkpoint of a named geometry."""
 
 from __future__ import annotations
 
@@ -50,6 +51,20 @@ def _parser() -> argparse.ArgumentParser:
     q.add_argument("--calibration", default="random")
     q.add_argument("--seed", type=int, default=None)
     q.add_argument("--allow-dense", action="store_true", help="leave embedding/head dense")
+    pl = sub.add_parser("plan", help="score and allocate a mixed-precision plan; nothing is tuned")
+    pl.add_argument("model", help="local checkpoint directory (config.json + *.safetensors)")
+    pl.add_argument("--average-bits", type=float, required=True)
+    pl.add_argument("--options", default="2,3,4", help="candidate widths, comma separated")
+    pl.add_argument("-b", "--bits", type=int, default=4)
+    pl.add_argument("-g", "--group-size", type=int, default=64)
+    pl.add_argument("--asym", action="store_true")
+    pl.add_argument("--remainder-bits", type=int, default=None)
+    pl.add_argument("--gradients", default="auto", help="auto, own_width or widest")
+    pl.add_argument("--scoring-samples", type=int, default=None)
+    pl.add_argument("--scoring-seq-len", type=int, default=None)
+    pl.add_argument("--scoring-batch-size", type=int, default=None)
+    pl.add_argument("--seed", type=int, default=None)
+    pl.add_argument("--write", default=None, help="write the per-layer widths as JSON (for --plan)")
     r = sub.add_parser("random-model", help="write a random-initialised checkpoint")
     r.add_argument("geometry", choices=sorted(GEOMETRIES))
     r.add_argument("output_dir")
@@ -94,6 +109,21 @@ def main(argv=None) -> int:
             return 0
         from mround_amd import api
         from mround_amd.schemes import Symmetry
+
+        if args.command == "plan":
+            info = api.plan_mixed_precision(
+                args.model, args.average_bits, _widths(args.options), bits=args.bits,
+                group_size=args.group_size, symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
+                sensitivity_gradients=args.gradients, remainder_bits=args.remainder_bits,
+                scoring_samples=args.scoring_samples, scoring_seq_len=args.scoring_seq_len,
+                scoring_batch_size=args.scoring_batch_size, seed=args.seed,
+                progress=lambda step: print(step.describe(), flush=True))
+            print(f"  {info['describe']}")
+            if args.write:
+                with open(args.write, "w") as f:
+                    json.dump(info["assignments"], f, indent=1)
+                print(f"  wrote {args.write}")
+            return 0
 
         plan = None
         if args.plan:

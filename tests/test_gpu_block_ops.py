@@ -275,7 +275,9 @@ def test_cast_bf16(n, offset):
 
 # 4096 x 4352 x 6144: 272 large tiles, the 16 past the wave take the k-split tail
 # (partials summed in order by the reduce kernel, which applies the SwiGLU backward)
-@pytest.mark.parametrize("mnk", [(256, 192, 128), (200, 96, 64), (1024, 4864, 896), (4096, 4352, 6144)])
+# 200 x 128 x 6144: 1 large tile, the whole grid cut along K
+@pytest.mark.parametrize("mnk", [(256, 192, 128), (200, 96, 64), (1024, 4864, 896), (4096, 4352, 6144),
+                                 (200, 128, 6144)])
 def test_swiglu_backward(mnk):
     M, N, Kd = mnk  # rows, intermediate, hidden
     dd = torch.randn(M, Kd, generator=_gen(51)).to(torch.bfloat16)

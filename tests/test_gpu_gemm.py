@@ -142,6 +142,56 @@ def test_swiglu_split_tail():
     assert bool(torch.all((act.float() - act_ref).abs() <= tol))
 
 
+# Under one wave of large tiles with a long K (at least 96 steps of 64) the whole
+# grid is cut along K: ragged 296 x 200 (2 tiles) and 904 x 696 (12 tiles).
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mn", [(296, 200), (904, 696)])
+def test_gemm_small_grid_long_k(layout, out, mn):
+    M, N = mn
+    Kd = 6400
+    print("case gemm small grid", layout, (M, N, Kd), out, flush=True, file=sys.stderr)
+    if layout == "nt":
+        a, b = _rand(M, Kd, seed=41).to(dev()), _rand(N, Kd, seed=42).to(dev())
+        ref, bound = _gpu_ref(a, b.t().contiguous())
+    elif layout == "nn":
+        a, b = _rand(M, Kd, seed=43).to(dev()), _rand(Kd, N, seed=44).to(dev())
+        ref, bound = _gpu_ref(a, b)
+    else:
+        a, b = _rand(Kd, M, seed=45).to(dev()), _rand(Kd, N, seed=46).to(dev())
+        ref, bound = _gpu_ref(a.t().contiguous(), b)
+    c = torch.full((M, N), 7.0, dtype=out, device=dev())
+    K.gemm(layout, a, b, c, M=M, N=N, K=Kd)
+    tol = bound + (ref.abs() * 2.0**-8 if out == torch.bfloat16 else 0)
+    assert bool(torch.all((c.float() - ref).abs() <= tol))
+
+
+def test_gemm_small_grid_bias_residual_and_swiglu():
+    M, N, Kd = 328, 256, 6144
+    print("case gemm small grid epilogues", flush=True, file=sys.stderr)
+    a, b = _rand(M, Kd, seed=47).to(dev()), _rand(N, Kd, seed=48).to(dev())
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(49)).to(dev())
+    resid = torch.randn(M, N, generator=torch.Generator().manual_seed(50)).to(dev())
+    prod, bound = _gpu_ref(a, b.t().contiguous())
+    ref = resid + (prod + bias)
+    c = torch.empty(M, N, device=dev())
+    K.gemm("nt", a, b, c, M=M, N=N, K=Kd, bias=bias, resid=resid)
+    assert bool(torch.all((c - ref).abs() <= bound + ref.abs() * 2.0**-22))
+    n = N // 2
+    wg, wu = _rand(n, Kd, seed=51), _rand(n, Kd, seed=52)
+    g, tg = _gpu_ref(a, wg.to(dev()).t().contiguous())
+    u, tu = _gpu_ref(a, wu.to(dev()).t().contiguous())
+    act = torch.empty(M, n, dtype=torch.bfloat16, device=dev())
+    gu = torch.empty(M, 2 * n, dtype=torch.bfloat16, device=dev())
+    K.gemm_swiglu(a, interleave_gate_up(wg, wu).to(dev()), act, gu)
+    gu_c = gu.float().reshape(M, n // 32, 2, 32)
+    assert bool(torch.all((gu_c[:, :, 0, :].reshape(M, n) - g).abs() <= tg + g.abs() * 2.0**-8))
+    assert bool(torch.all((gu_c[:, :, 1, :].reshape(M, n) - u).abs() <= tu + u.abs() * 2.0**-8))
+    act_ref = torch.nn.functional.silu(g) * u
+    tol = 1.1 * tg * u.abs() + tu * torch.nn.functional.silu(g).abs() + act_ref.abs() * 2.0**-7 + 1e-6
+    assert bool(torch.all((act.float() - act_ref).abs() <= tol))
+
+
 def test_gemm_bias_and_residual():
     M, N, Kd = 304, 264, 128
     a, b = _rand(M, Kd, seed=7), _rand(N, Kd, seed=8)

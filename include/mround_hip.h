@@ -273,9 +273,12 @@ int mr_rope(void* x_bf16, int64_t ld, int64_t T, int S, int n_heads, int head_di
  * writes out [B*S, Hq*head_dim] bf16 (leading dimension ldo) and the natural
  * log-sum-exp per (b, h, s) for the backward. The backward takes dout, writes
  * the gradient of the (post-rope) q/k/v into dqkv (same layout as qkv) and
- * uses dsum_ws (B*Hq*S floats) as workspace. The scaled-dot-product
- * attention of the mlx-lm block (mround/pipeline/blocks.py:605) and its
- * autodiff.
+ * uses dsum_ws (B*Hq*S floats) as workspace. When fewer than 512 blocks of
+ * 128 keys would run (Hkv * B * S / 128), the backward splits each kv head's
+ * query heads over several blocks and sums their fp32 dK/dV partials in a
+ * fixed order; those live in a 128 MB per-device buffer that the first such
+ * call allocates and the process keeps. The scaled-dot-product attention of
+ * the mlx-lm block (mround/pipeline/blocks.py:605) and its autodiff.
  */
 int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int head_dim,
                 float scale, void* out, int64_t ldo, float* lse, void* stream);

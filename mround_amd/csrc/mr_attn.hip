@@ -17,6 +17,8 @@
 // orientations. All sums are in a fixed order: no atomics, deterministic.
 #include <cmath>
 
+#include <mutex>
+
 #include "mr_common.h"
 
 namespace mr {
@@ -344,7 +346,7 @@ template <int D>
 __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
     const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
     const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
-    float scale, uint16_t* __restrict__ dqkv) {
+    float scale, uint16_t* __restrict__ dqkv, int hsplit, float* __restrict__ part) {
   constexpr int NS = D / 16, ND = D / 32;
   constexpr int TILE = 64 * D * 2;
   __shared__ __attribute__((aligned(1024))) uint8_t Q0[TILE];
@@ -353,8 +355,11 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
   __shared__ __attribute__((aligned(1024))) uint8_t O1[TILE];
   __shared__ __attribute__((aligned(16))) float LD0[128];  // lse (log2 domain) then rowsum(dO O) of the tile's 64 queries
   __shared__ __attribute__((aligned(16))) float LD1[128];
-  const int kb = blockIdx.z, g = blockIdx.x, b = blockIdx.y;
+  const int kb = blockIdx.z, g = blockIdx.x / hsplit, hs = blockIdx.x % hsplit, b = blockIdx.y;
   const int G = Hq / Hkv;
+  // This block's query heads of the group: [h_lo, h_hi) (all of them unless split).
+  const int h_lo = hs * G / hsplit, h_hi = (hs + 1) * G / hsplit;
+  const int hq0 = g * G + h_lo;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
   const int k0w = kb * QB + wave * 32;
   const int kj = k0w + l32;  // this lane's key
@@ -363,17 +368,17 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
   const float scale_log2 = scale * kLog2e;
   const int first_q = kb * QB;
   const int nqt = (S - first_q) / 64;  // query tiles per head
-  const int n_items = G * nqt;
+  const int n_items = (h_hi - h_lo) * nqt;
 
-  // item i: query head g G + i / nqt, query tile first_q + 64 (i % nqt)
+  // item i: query head hq0 + i / nqt, query tile first_q + 64 (i % nqt)
   auto issue = [&](int i, uint8_t* Qd, uint8_t* Od) {
-    const int hq = g * G + i / nqt;
+    const int hq = hq0 + i / nqt;
     const int64_t r0 = tok0 + first_q + (i % nqt) * 64;
     dma_rowtile<D>(qkv, ld, r0, hq * D, Qd);
     dma_rowtile<D>(dout, ldo, r0, hq * D, Od);
   };
   auto fetch_ld = [&](int i) -> float {  // threads 0..127: this item's lse / rowsum value
-    const int hq = g * G + i / nqt;
+    const int hq = hq0 + i / nqt;
     const int q = first_q + (i % nqt) * 64 + (threadIdx.x & 63);
     const int64_t at = (static_cast<int64_t>(b) * Hq + hq) * S + q;
     return threadIdx.x < 64 ? lse[at] * kLog2e : dsum[at];
@@ -514,7 +519,22 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
   }
   if (i < n_items) step(i, Q0, O0, LD0, Q1, O1, LD1);
 
-  // dk[dt][r]: key k0w + acc_row(r, h), d = dt * 32 + l32.
+  // dk[dt][r]: key k0w + acc_row(r, h), d = dt * 32 + l32. Split blocks
+  // write fp32 partials, [split][token][k heads | v heads][d], summed by
+  // attn_bwd_kv_reduce in split order.
+  if (part) {
+    const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
+    float* pb = part + static_cast<int64_t>(hs) * gridDim.y * S * W;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = tok0 + k0w + acc_row(r, h);
+        pb[row * W + g * D + dt * 32 + l32] = dk[dt][r] * scale;
+        pb[row * W + (Hkv + g) * D + dt * 32 + l32] = dv[dt][r];
+      }
+    return;
+  }
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
@@ -523,6 +543,25 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
       dqkv[row * ld + kcol + dt * 32 + l32] = f32_to_bf16(dk[dt][r] * scale);
       dqkv[row * ld + vcol + dt * 32 + l32] = f32_to_bf16(dv[dt][r]);
     }
+}
+
+// dK, dV of head-split blocks: the sum of the partials in split order, as
+// bf16 into the k and v columns of dqkv. One thread per 4 consecutive values.
+__global__ __launch_bounds__(kThreads) void attn_bwd_kv_reduce(const float* __restrict__ part,
+                                                              int hsplit, int64_t T, int64_t W,
+                                                              int64_t col0, uint16_t* __restrict__ dqkv,
+                                                              int64_t ld) {
+  const int64_t e = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4;
+  if (e >= T * W) return;
+  float4 acc = *reinterpret_cast<const float4*>(part + e);
+  for (int sp = 1; sp < hsplit; ++sp) {
+    const float4 v = *reinterpret_cast<const float4*>(part + sp * T * W + e);
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  const int64_t row = e / W, c = e % W;
+  const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc.x)) | (static_cast<uint32_t>(f32_to_bf16(acc.y)) << 16);
+  const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc.z)) | (static_cast<uint32_t>(f32_to_bf16(acc.w)) << 16);
+  *reinterpret_cast<uint2*>(dqkv + row * ld + col0 + c) = make_uint2(lo, hi);
 }
 
 // dQ: queries along lanes; a block owns 128 queries of one query head and
@@ -630,6 +669,29 @@ int launch_fwd(const uint16_t* qkv, int64_t ld, int B, int S, int Hq, int Hkv, f
   return MR_OK;
 }
 
+// Grids of few key blocks (short sequences, few kv heads, small batches)
+// leave CUs idle and put the long causal first blocks on the critical path:
+// then each kv head's query heads are split over several blocks, up to
+// kKvTargetBlocks blocks, whose fp32 dK/dV partials live in a per-device
+// workspace allocated on first use and kept for the life of the process.
+// Measured: 1.3x on 8 x 2048 tokens with 2 kv heads, 3.4x on 2 x 1024; a
+// grid already at 512 blocks (4 kv heads) loses to the partials' traffic.
+constexpr int64_t kKvTargetBlocks = 512;
+constexpr int64_t kKvPartBytes = 128ll << 20;
+float* kv_partials() {
+  static std::mutex mu;
+  static float* ws[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ws[dev]) {
+    void* q = nullptr;
+    if (hipMalloc(&q, kKvPartBytes) != hipSuccess) return nullptr;
+    ws[dev] = static_cast<float*>(q);
+  }
+  return ws[dev];
+}
+
 template <int D>
 int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint16_t* dout,
                int64_t ldo, const float* lse, float* dsum, int B, int S, int Hq, int Hkv,
@@ -638,8 +700,22 @@ int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint1
   const int64_t lanes = T * Hq * (D / 8);
   hipLaunchKernelGGL(attn_bwd_dot<D>, dim3(static_cast<unsigned>((lanes + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, s, dout, out, ldo, T, S, Hq, dsum);
-  hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
-                     lse, dsum, S, Hq, Hkv, scale, dqkv);
+  const int G = Hq / Hkv;
+  const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
+  int hsplit = 1;
+  const int64_t blocks = static_cast<int64_t>(Hkv) * B * (S / QB);
+  while (hsplit < G && blocks * hsplit < kKvTargetBlocks &&
+         (hsplit + 1) * T * W * 4 <= kKvPartBytes)
+    ++hsplit;
+  float* part = hsplit > 1 ? kv_partials() : nullptr;
+  if (!part) hsplit = 1;
+  hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv * hsplit, B, S / QB), dim3(kThreads), 0, s, qkv, ld,
+                     dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
+  if (part) {
+    const int64_t threads = T * W / 4;
+    hipLaunchKernelGGL(attn_bwd_kv_reduce, dim3(static_cast<unsigned>((threads + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, s, part, hsplit, T, W, static_cast<int64_t>(Hq) * D, dqkv, ld);
+  }
   hipLaunchKernelGGL(attn_bwd_dq<D>, dim3(Hq, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
                      lse, dsum, S, Hq, Hkv, scale, dqkv);
   MR_LAUNCH_CHECK("mr_attn_bwd");

@@ -148,6 +148,21 @@ __device__ __forceinline__ void store8_f32(float* p, int64_t i, const float (&x)
   store8<MR_F32>(p, i, x);
 }
 
+// Eight fp32 through the caches (plain 16-byte accesses). Measured on the
+// fake-quant passes over the learnable v (read, then rewritten in place by the
+// update): 8-10 % faster than the streaming forms above.
+__device__ __forceinline__ void load8_f32_cached(const float* p, int64_t i, float (&out)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p + i);
+  const float4 b = *reinterpret_cast<const float4*>(p + i + 4);
+  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+
+__device__ __forceinline__ void store8_f32_cached(float* p, int64_t i, const float (&x)[8]) {
+  *reinterpret_cast<float4*>(p + i) = make_float4(x[0], x[1], x[2], x[3]);
+  *reinterpret_cast<float4*>(p + i + 4) = make_float4(x[4], x[5], x[6], x[7]);
+}
+
 // sign(x) as numpy/MLX define it: -1, 0 or +1 (NaN propagates).
 __device__ __forceinline__ float signf(float x) {
   return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x * 0.0f);

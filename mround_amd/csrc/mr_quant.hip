@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
 
   float vv[8];
   if constexpr (HAS_V) {
-    load8_f32(v, e, vv);
+    load8_f32_cached(v, e, vv);
   } else {
 #pragma unroll
     for (int k = 0; k < 8; ++k) vv[k] = 0.0f;
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
 
   float x[8], vv[8], gg[8];
   load8<WT>(w, e, x);
-  load8_f32(v, e, vv);
+  load8_f32_cached(v, e, vv);
   load8<GT>(g, map.chunk_elem(chunk), gg);
   float mx = x[0], mn = x[0];
 #pragma unroll
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
     float nv[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) nv[k] = clampf(vv[k] - st.lr * signf(gv[k]), -st.vb, st.vb);
-    store8_f32(v, e, nv);
+    store8_f32_cached(v, e, nv);
     if (leader) {
       alpha[grp] = clampf(a - st.lr * signf(ga), st.lo, st.hi);
       beta[grp] = clampf(b - st.lr * signf(gb), st.lo, st.hi);

@@ -34,6 +34,8 @@ from mround_amd.formats.mlx_export import (QuantizedLayer, export_mlx, narrow_co
                                            require_mlx_representable)
 from mround_amd.pipeline.checkpoint import DecoderModel, dense_tensors, load_model
 from mround_amd.pipeline.runner import QuantizationRunner, RunSummary
+from mround_amd import kernels as K
+from mround_amd.planner import memory as M
 from mround_amd.planner.allocator import allocate_bits
 from mround_amd.planner.sensitivity import (gradient_source_for, mixed_budget_bits,
                                             score_layer_options, scoring_batch_size, storage_bits)
@@ -254,10 +256,15 @@ def calibration_tokens(vocab: int, n_samples: int, seq_len: int, *, seed: int, d
 
 
 def _entrance(model: DecoderModel, tokens: torch.Tensor, batch_size: int) -> list[torch.Tensor]:
-    """The block-0 input stream: embedding rows in float32, one
-    ``[batch * seq_len, hidden]`` tensor per batch."""
-    return [model.embed[tokens[i:i + batch_size].reshape(-1)].float()
-            for i in range(0, tokens.shape[0], batch_size)]
+    """The block-0 input stream: embedding rows in float32 (``mr_embed_rows``),
+    one ``[batch * seq_len, hidden]`` tensor per batch."""
+    out = []
+    for i in range(0, tokens.shape[0], batch_size):
+        ids = tokens[i:i + batch_size].reshape(-1).to(torch.int32)
+        x = torch.empty(ids.numel(), model.embed.shape[1], dtype=torch.float32, device=model.embed.device)
+        K.embed_rows(model.embed, ids, x)
+        out.append(x)
+    return out
 
 
 def _round_to_nearest(model: DecoderModel, scheme: QuantScheme, *, dense: bool):
@@ -295,6 +302,57 @@ def _storage(model: DecoderModel, quantized: Mapping[str, QuantizedLayer]) -> St
     return Storage(total, params, float(dtype_bits))
 
 
+def _read_config(model: str | Path) -> dict[str, Any]:
+    path = Path(model)
+    if not (path / "config.json").is_file():
+        raise ArchitectureError(f"{path} is not a local checkpoint directory (no config.json); "
+                                "hub downloads are not available")
+    return json.loads((path / "config.json").read_text())
+
+
+def _run_shape(config, resolved: QuantScheme, tuning: TuningConfig, *, average_bits, plan, widths,
+               gradient_source, scoring_samples, scoring_seq_len, scoring_batch, dense_remainder,
+               quantized_inputs) -> tuple[M.ModelShape, M.RunShape]:
+    shape = M.ModelShape.from_config(config)
+    mixed = average_bits is not None and plan is None
+    samples = SENSITIVITY_SAMPLES if scoring_samples is None else int(scoring_samples)
+    sequence = SENSITIVITY_SEQ_LEN if scoring_seq_len is None else int(scoring_seq_len)
+    batch = (scoring_batch_size(samples, sequence) if scoring_batch is None
+             else max(1, min(samples, int(scoring_batch))))
+    source = gradient_source_for(gradient_source, shape.layers * shape.block_weights) if mixed else "own_width"
+    run = M.RunShape(n_samples=tuning.n_samples, seq_len=tuning.seq_len, batch_size=tuning.batch_size,
+                     group_size=resolved.group_size, searched=resolved.scale_init is ScaleInit.SEARCHED,
+                     quantized_inputs=quantized_inputs, mixed=mixed, widths=len(widths),
+                     gradient_source=source, scoring_samples=samples, scoring_seq_len=sequence,
+                     scoring_batch=batch, dense_remainder=dense_remainder)
+    return shape, run
+
+
+def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
+                   symmetry: Symmetry = Symmetry.SYMMETRIC, average_bits: float | None = None,
+                   candidate_bits: Sequence[int] = (2, 3, 4), sensitivity_gradients: str = "auto",
+                   remainder_bits: int | None = None, dense_remainder: bool = False,
+                   scoring_samples: int | None = None, scoring_seq_len: int | None = None,
+                   scoring_batch_size: int | None = None, scheme: QuantScheme | None = None,
+                   tuning: TuningConfig | None = None, scale_init: ScaleInit | str | None = None,
+                   quantized_inputs: bool = True, memory_budget: int | None = None,
+                   device: str = "cuda") -> M.MemoryCheck:
+    """Predict the device memory of the run :func:`quantize` would make, and
+    stop (mround/api.py:1088-1192). Reads ``config.json`` and nothing else.
+    ``memory_budget`` defaults to 90 % of the device's memory."""
+    config = _read_config(model)
+    resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry,
+                                       average_bits=average_bits, candidate_bits=candidate_bits,
+                                       remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
+    shape, run = _run_shape(config, resolved, tuning or TuningConfig(), average_bits=average_bits, plan=None,
+                            widths=candidate_bits if average_bits is not None else (resolved.bits,),
+                            gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
+                            scoring_seq_len=scoring_seq_len, scoring_batch=scoring_batch_size,
+                            dense_remainder=dense_remainder, quantized_inputs=quantized_inputs)
+    budget = M.default_budget(device) if memory_budget is None else memory_budget
+    return M.check_memory(shape, run, budget=budget)
+
+
 def _load_tokens(m: DecoderModel, calibration, tuning: TuningConfig, seed: int, device) -> torch.Tensor:
     vocab = int(m.config["vocab_size"])
     if isinstance(calibration, torch.Tensor):
@@ -321,6 +379,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
              export_format: str = "mlx", quantized_inputs: bool = True, holdout_batches: int = 0,
              per_layer_recipe: bool = False, plan: Mapping[str, int] | None = None,
              scale_init: ScaleInit | str | None = None, seed: int | None = None,
+             memory_budget: int | None = None, memory_check: bool = True,
              device: str = "cuda", progress=None, scoring_progress=None) -> QuantizeResult:
     """Quantize the local checkpoint ``model`` into ``output_dir``.
 
@@ -331,8 +390,12 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     and an exact allocation (or, with ``plan``, the given per-layer widths),
     the block layers tuned at their assigned widths and the remainder at
     ``remainder_bits`` (default: the width nearest the average, ties up).
-    Raises the reference's exceptions for unrepresentable schemes, bad
-    calibration, unusable plans and unsupported architectures.
+    The run's device memory is predicted from ``config.json`` before anything
+    is loaded (``predict_memory``) and a run past ``memory_budget`` (default
+    90 % of the device's memory) is refused with ``MemoryBudgetError`` unless
+    ``memory_check`` is off. Raises the reference's exceptions for
+    unrepresentable schemes, bad calibration, unusable plans and unsupported
+    architectures.
     """
     started = time.perf_counter()
     if export_format != "mlx":
@@ -347,6 +410,17 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         require_mlx_representable(resolved.with_bits(w))
     tuning = tuning or TuningConfig()
     seed = 0 if seed is None else int(seed)
+    mshape, rshape = _run_shape(_read_config(model), resolved, tuning, average_bits=average_bits, plan=plan,
+                                widths=candidate_bits if average_bits is not None else (resolved.bits,),
+                                gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
+                                scoring_seq_len=scoring_seq_len, scoring_batch=scoring_batch_size,
+                                dense_remainder=dense_remainder, quantized_inputs=quantized_inputs)
+    budget = M.default_budget(device) if memory_budget is None else memory_budget
+    memory = M.check_memory(mshape, rshape, budget=budget)
+    if memory_check:
+        M.require_fits(memory)
+    if torch.cuda.is_available() and str(device).startswith("cuda"):
+        torch.cuda.reset_peak_memory_stats(device)
     t0 = time.perf_counter()
     m = load_model(model, device=device)
     load_s = time.perf_counter() - t0
@@ -411,6 +485,9 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         "skipped": skipped,
         "storage": {"bits_per_weight": storage.bits_per_weight, "compression": storage.compression},
         "seconds": seconds,
+        "memory": {**memory.record(), "library_workspaces": M.LIBRARY_WORKSPACES,
+                   "peak_allocated": int(torch.cuda.max_memory_allocated(device))
+                   if torch.cuda.is_available() and str(device).startswith("cuda") else None},
     }
     config_path = out / RUN_RECORD
     config_path.write_text(json.dumps(record, indent=2) + "\n")

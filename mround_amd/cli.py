@@ -51,6 +51,13 @@ def _parser() -> argparse.ArgumentParser:
     q.add_argument("--calibration", default="random")
     q.add_argument("--seed", type=int, default=None)
     q.add_argument("--allow-dense", action="store_true", help="leave embedding/head dense")
+    q.add_argument("--memory-budget", type=float, default=None,
+                   help="GB the run may use on the device (default: 90 %% of its memory)")
+    q.add_argument("--skip-memory-check", action="store_true",
+                   help="run even when the prediction exceeds the budget")
+    q.add_argument("--dry-run", action="store_true",
+                   help="predict the run's peak device memory against the budget and stop; "
+                        "exits 0 when it fits, 1 when the run would be refused")
     pl = sub.add_parser("plan", help="score and allocate a mixed-precision plan; nothing is tuned")
     pl.add_argument("model", help="local checkpoint directory (config.json + *.safetensors)")
     pl.add_argument("--average-bits", type=float, required=True)
@@ -125,6 +132,16 @@ def main(argv=None) -> int:
                 print(f"  wrote {args.write}")
             return 0
 
+        budget = None if args.memory_budget is None else int(args.memory_budget * 1e9)
+        if args.dry_run:
+            check = api.predict_memory(
+                args.model, bits=args.bits, group_size=args.group_size,
+                symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
+                average_bits=args.average_bits, candidate_bits=_widths(args.options),
+                remainder_bits=args.remainder_bits, dense_remainder=args.allow_dense,
+                tuning=_tuning(args), memory_budget=budget)
+            print(f"  {check.explain()}")
+            return 0 if check.fits else 1
         plan = None
         if args.plan:
             with open(args.plan) as f:
@@ -135,7 +152,8 @@ def main(argv=None) -> int:
                               average_bits=args.average_bits, candidate_bits=_widths(args.options),
                               remainder_bits=args.remainder_bits, plan=plan, tuning=_tuning(args),
                               calibration=args.calibration, export_format=args.format,
-                              dense_remainder=args.allow_dense, seed=args.seed,
+                              dense_remainder=args.allow_dense, seed=args.seed, memory_budget=budget,
+                              memory_check=not args.skip_memory_check,
                               progress=lambda b: print(f"  block {b.index}: loss {b.initial_loss:.4g} -> "
                                                        f"{b.final_loss:.4g} in {b.seconds:.2f} s", flush=True),
                               scoring_progress=lambda step: print(step.describe(), flush=True))

@@ -1,0 +1,38 @@
+"""The device-memory prediction against the peak a run actually allocates
+(``torch.cuda.max_memory_allocated``, which does not see the library's two
+internal workspaces, so they are taken out of the prediction here)."""
+
+from __future__ import annotations
+
+import json
+import sys
+
+import pytest
+
+from mround_amd import api
+from mround_amd.pipeline.checkpoint import write_random_checkpoint
+from mround_amd.planner import memory as M
+from mround_amd.schemes import Symmetry, TuningConfig
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(model_type="qwen2", hidden_size=512, num_attention_heads=8, num_key_value_heads=2,
+             intermediate_size=1536, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=3,
+             vocab_size=4096, tie_word_embeddings=True)
+
+
+@pytest.mark.parametrize("mixed", [False, True])
+def test_prediction_bounds_the_measured_peak(tmp_path, mixed):
+    print("case memory", mixed, flush=True, file=sys.stderr)
+    src = write_random_checkpoint(tmp_path / "m", SMALL, seed=1)
+    tuning = TuningConfig(iters=2, batch_size=4, n_samples=8, seq_len=256)
+    kw = dict(average_bits=3.0, candidate_bits=(2, 4), scoring_samples=8, scoring_seq_len=257) if mixed else {}
+    res = api.quantize(src, output_dir=tmp_path / "q", bits=4, symmetry=Symmetry.ASYMMETRIC, tuning=tuning,
+                       seed=2, **kw)
+    rec = json.loads(res.config_path.read_text())["memory"]
+    predicted = rec["peak"] - M.LIBRARY_WORKSPACES
+    measured = rec["peak_allocated"]
+    print(f"  predicted {predicted} measured {measured} ({measured / predicted:.3f}) in {rec['peak_stage']}",
+          file=sys.stderr)
+    assert rec["peak_stage"] == ("scoring" if mixed else "blocks")
+    assert 0.85 * predicted <= measured <= 1.05 * predicted

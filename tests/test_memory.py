@@ -1,0 +1,101 @@
+"""The device-memory prediction: the geometry's weight counts against the
+figures of the benchmark configurations, the block and causal-LM engines'
+formulas against the buffers the engines actually allocate (built on the CPU),
+and the budget refusals of the API and the CLI."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from mround_amd import api
+from mround_amd.cli import GEOMETRIES, main
+from mround_amd.exceptions import MemoryBudgetError
+from mround_amd.pipeline.block import BlockEngine
+from mround_amd.pipeline.causal_lm import CausalLM, padded_length
+from mround_amd.pipeline.checkpoint import block_shape, load_model, write_random_checkpoint
+from mround_amd.planner import memory as M
+
+TINY = dict(model_type="qwen2", hidden_size=128, num_attention_heads=2, num_key_value_heads=1,
+            intermediate_size=256, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=2,
+            vocab_size=250, tie_word_embeddings=True)
+
+
+def _bytes(*objs) -> int:
+    """Bytes of the distinct tensor storages the objects' attributes hold
+    (directly or in dicts, lists and tuples)."""
+    seen, total = set(), 0
+
+    def visit(v):
+        nonlocal total
+        if isinstance(v, torch.Tensor):
+            key = (v.untyped_storage().data_ptr(), v.untyped_storage().nbytes())
+            if key not in seen and v.untyped_storage().nbytes():
+                seen.add(key)
+                total += v.untyped_storage().nbytes()
+        elif isinstance(v, dict):
+            for x in v.values():
+                visit(x)
+        elif isinstance(v, (list, tuple)):
+            for x in v:
+                visit(x)
+
+    for obj in objs:
+        for v in vars(obj).values():
+            visit(v)
+    return total
+
+
+@pytest.mark.parametrize("geo,weights", [("qwen2.5-7b", 233_046_016), ("qwen2.5-3b", 77_070_336),
+                                         ("qwen2.5-0.5b", 14_909_440), ("smollm2-135m", 3_538_944)])
+def test_block_weights_match_the_configurations(geo, weights):
+    assert M.ModelShape.from_config(GEOMETRIES[geo]).block_weights == weights
+
+
+@pytest.mark.parametrize("geo", ["qwen2.5-0.5b", "smollm2-135m"])
+def test_engine_formula_is_the_engine(geo):
+    cfg = GEOMETRIES[geo]
+    eng = BlockEngine(block_shape(cfg), batch=2, seq_len=256, device="cpu")
+    assert _bytes(eng) == M.engine_bytes(M.ModelShape.from_config(cfg), 512, 256)
+    assert sum(t.nbytes for t in eng.new_activations().values()) == \
+        M.activation_bytes(M.ModelShape.from_config(cfg), 512)
+
+
+def test_scoring_formula_is_the_causal_lm(tmp_path):
+    write_random_checkpoint(tmp_path / "m", TINY)
+    model = load_model(tmp_path / "m", device="cpu")
+    lm = CausalLM(model, batch=2, seq_len=200, device="cpu", keep_activations=True)
+    m = M.ModelShape.from_config(TINY)
+    run = M.RunShape(n_samples=2, seq_len=128, batch_size=2, group_size=64, mixed=True, widths=2,
+                     scoring_samples=4, scoring_seq_len=200, scoring_batch=2)
+    pred = M.predict_memory(m, run)
+    formula = pred.stages["scoring"] - pred.stages["load"] - 4 * 200 * 8 - 2 * 128 * 8
+    # what the engine object owns (the blocks' norms and biases it points at are the model's),
+    # and the input-gradient buffer appears at the first backward
+    owned = _bytes(lm, lm.eng) + lm.tokens * m.hidden * 4
+    shared = sum(p.untyped_storage().nbytes() for t in lm.params for p in t if p is not None)
+    assert abs((owned - shared) - formula) <= 0.005 * formula, (owned - shared, formula)
+
+
+def test_api_refuses_a_run_past_the_budget(tmp_path):
+    write_random_checkpoint(tmp_path / "m", TINY)
+    check = api.predict_memory(tmp_path / "m", memory_budget=10 ** 12, device="cpu")
+    assert check.fits and check.prediction.peak > 0 and "blocks" in check.describe()
+    small = api.predict_memory(tmp_path / "m", memory_budget=1000, device="cpu")
+    assert not small.fits and "calibration streams" in small.explain()
+    with pytest.raises(MemoryBudgetError, match="predicted peak"):
+        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", memory_budget=1000, device="cpu")
+    with pytest.raises(ValueError, match="positive"):
+        api.predict_memory(tmp_path / "m", memory_budget=-5, device="cpu")
+    mixed = api.predict_memory(tmp_path / "m", average_bits=3, candidate_bits=(2, 4), device="cpu",
+                               memory_budget=10 ** 12)
+    assert "scoring" in mixed.prediction.stages
+
+
+def test_cli_dry_run(tmp_path, capsys):
+    write_random_checkpoint(tmp_path / "m", TINY)
+    assert main(["quantize", str(tmp_path / "m"), "-o", str(tmp_path / "o"), "--dry-run",
+                 "--memory-budget", "1000"]) == 0
+    assert "predicted peak" in capsys.readouterr().out
+    assert main(["quantize", str(tmp_path / "m"), "-o", str(tmp_path / "o"), "--dry-run",
+                 "--memory-budget", "0.000001"]) == 1

@@ -495,6 +495,63 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
                           tuple(skipped), mixed, seconds)
 
 
+@dataclasses.dataclass(frozen=True)
+class RoundToNearestResult:
+    """What a round-to-nearest run produced (mround/api.py:798-838)."""
+
+    output_dir: Path
+    scheme: QuantScheme
+    quantized: tuple[str, ...]
+    skipped: tuple[tuple[str, str], ...]
+    bits_per_weight: float
+    stored_bytes: int
+    original_bytes: int
+
+    @property
+    def compression(self) -> float:
+        return self.original_bytes / max(1, self.stored_bytes)
+
+    def describe(self) -> str:
+        return (f"{len(self.quantized)} modules at {self.scheme.bits} bits, {len(self.skipped)} left dense, "
+                f"{self.bits_per_weight:.2f} bits per weight overall ({self.compression:.2f}x smaller)")
+
+
+def quantize_round_to_nearest(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_size: int = 64,
+                              symmetry: Symmetry = Symmetry.SYMMETRIC, dense_remainder: bool = False,
+                              device: str = "cuda") -> RoundToNearestResult:
+    """Quantize every linear at round to nearest with the observed-range scale,
+    nothing learned and no calibration, and write the MLX checkpoint: the
+    baseline learned rounding has to beat (mround/api.py:841-940). With
+    ``dense_remainder`` only the block linears are rounded."""
+    scheme = QuantScheme(bits=bits, group_size=group_size, symmetry=symmetry)
+    require_mlx_representable(scheme)
+    m = load_model(model, device=device)
+    quantized: dict[str, QuantizedLayer] = {}
+    skipped: list[tuple[str, str]] = []
+    for blk in m.blocks:
+        for name, w in sorted(blk.weights.linears.items()):
+            path = f"{blk.name}.{name}"
+            if group_size != -1 and w.shape[-1] % group_size:
+                skipped.append((path, f"last dimension {w.shape[-1]} is not a multiple of {group_size}"))
+                continue
+            codes, scale, zp = quantize_codes(w, None, scheme, narrow=True)
+            quantized[path] = QuantizedLayer(narrow_codes(codes, scheme), scale, zp, scheme)
+    remainder, rem_skipped = _round_to_nearest(m, scheme, dense=dense_remainder)
+    quantized.update(remainder)
+    skipped.extend(rem_skipped)
+    if not quantized:
+        raise ArchitectureError(f"nothing in {model!r} could be quantized at group_size={group_size}")
+    dense = {k: v for k, v in dense_tensors(m).items() if k.removesuffix(".weight") not in quantized
+             or not k.endswith(".weight")}
+    dtype_name = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}[m.dtype]
+    out = Path(output_dir)
+    export_mlx(out, dense_weights=dense, quantized=quantized, config=m.config, dtype=dtype_name)
+    storage = _storage(m, quantized)
+    original = int(storage.parameters * storage.dense_bits_per_weight) // 8
+    return RoundToNearestResult(out, scheme, tuple(sorted(quantized)), tuple(skipped), storage.bits_per_weight,
+                                storage.total_bits // 8, original)
+
+
 def plan_mixed_precision(model: str | Path, average_bits: float, candidate_bits: Sequence[int] = (2, 3, 4),
                          *, bits: int = 4, group_size: int = 64, symmetry: Symmetry = Symmetry.SYMMETRIC,
                          scale_init: ScaleInit | str | None = None, scheme: QuantScheme | None = None,

@@ -93,3 +93,35 @@ def test_cli_quantize(tmp_path, capsys):
     assert rc == 0
     out = capsys.readouterr().out
     assert "modules tuned" in out and (tmp_path / "q" / "model.safetensors").exists()
+
+
+@pytest.mark.parametrize("asym,dense", [(True, False), (False, True)])
+def test_round_to_nearest_export(tmp_path, asym, dense):
+    """Every block linear (and, unless dense, the embedding) at round to nearest
+    with the observed-range scale: packed words, scales and biases bit-exact
+    with the oracle (mround/api.py:841-940)."""
+    print("case rtn", asym, dense, flush=True, file=sys.stderr)
+    src = write_random_checkpoint(tmp_path / "m", TINY, seed=4, std=0.05)
+    res = api.quantize_round_to_nearest(src, output_dir=tmp_path / "q", bits=3,
+                                        symmetry=Symmetry.ASYMMETRIC if asym else Symmetry.SYMMETRIC,
+                                        dense_remainder=dense)
+    assert len(res.quantized) == 14 + (0 if dense else 1)
+    assert ("model.embed_tokens" in dict(res.skipped)) == dense
+    assert 3 < res.bits_per_weight < 16 and res.compression > 1
+    cfg = json.loads((tmp_path / "q" / "config.json").read_text())
+    assert cfg["quantization"]["bits"] == 3
+    t = load_file(str(tmp_path / "q" / "model.safetensors"))
+    orig = load_model(src, device="cpu")
+    w = orig.blocks[1].weights.linears["self_attn.o_proj"].float().numpy()
+    mode = "asym" if asym else "sym"
+    _, codes, scale, zp = OQ.fake_quantize(w, None, None, None, bits=3, group_size=64, mode=mode)
+    rows, cols = w.shape
+    q = codes.reshape(rows, cols).astype(np.int64) + (0 if asym else 4)
+    assert np.array_equal(t["model.layers.1.self_attn.o_proj.weight"].numpy(), OP.pack_codes(q.astype(np.uint32), 3))
+    s_bf = _bf16(scale.reshape(rows, -1))
+    assert torch.equal(t["model.layers.1.self_attn.o_proj.scales"], s_bf)
+    zpv = zp.reshape(rows, -1) if asym else np.full((rows, cols // 64), 4, dtype=np.float32)
+    assert torch.equal(t["model.layers.1.self_attn.o_proj.biases"],
+                       (-(s_bf.float() * _bf16(zpv).float())).to(torch.bfloat16))
+    if dense:
+        assert t["model.embed_tokens.weight"].dtype == torch.bfloat16

@@ -154,6 +154,11 @@ def bwd_bytes(n, gs):
     return n * (2 + 4 + 4 + 4) + (n // gs) * 16
 
 
+def step_requant_bytes(n, gs):
+    """The fused step that also writes the next step's W' (2 B per weight more)."""
+    return bwd_bytes(n, gs) + n * 2
+
+
 def pack_bytes(n, bits):
     return n * (1 + bits / 8)
 
@@ -174,6 +179,10 @@ def fake_quant_microbench(torch, K, dev, bits, gs, steps):
         "bwd_update": lambda: K.fq_backward_signsgd(w, v, a, b, g, bits=bits, group_size=gs,
                                                     mode="asym", eps=1e-8, update=True, lr=0.005,
                                                     coef_lo=0.1, coef_hi=1.0, v_bound=0.5),
+        "step_requant": lambda: K.fq_step_requant_mapped(w, v, a, b, g, bits=bits, group_size=gs,
+                                                         mode="asym", eps=1e-8, lr=0.005, coef_lo=0.1,
+                                                         coef_hi=1.0, v_bound=0.5, row_block=0,
+                                                         row_stride=0, row_offset=0, wq_out=wq),
         "codes": lambda: K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8,
                                       codes_out=codes, scale_out=scale, zp_out=zp),
         "pack": lambda: K.pack_codes(codes, bits, signed=False, offset=0, packed_out=packed),
@@ -191,7 +200,8 @@ def fake_quant_microbench(torch, K, dev, bits, gs, steps):
         e.record(stream)
         e.synchronize()
         out[name] = s.elapsed_time(e) / steps
-    nbytes = {"fwd": fwd_bytes(n, gs), "bwd_update": bwd_bytes(n, gs), "pack": pack_bytes(n, bits)}
+    nbytes = {"fwd": fwd_bytes(n, gs), "bwd_update": bwd_bytes(n, gs),
+              "step_requant": step_requant_bytes(n, gs), "pack": pack_bytes(n, bits)}
     return {
         "workload": f"{ROWS}x{COLS} bf16 weight, {bits}-bit asym gs{gs}",
         **{k: {"ms": round(out[k], 5), "bytes": nbytes[k],

@@ -104,6 +104,21 @@ int mr_fq_backward_signsgd_mapped(const void* w, int w_dtype, float* v, float* a
                                   void* stream);
 
 /*
+ * The fused step, then W' of the updated parameters written to wq_out (in
+ * wq_dtype) through the same row placement: the next tuning step's operand,
+ * bit-identical to mr_fq_forward_mapped on the parameters just written, made
+ * while W and the new v are still in registers. Replaces the step's
+ * SignSGD.apply + project_params and the next step's fake_quantize
+ * (mround/pipeline/runner.py:920-935, mround/core/quantizer.py:287-347).
+ */
+int mr_fq_step_requant_mapped(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                              const float* init_scale, const void* g, int g_dtype, int64_t rows,
+                              int64_t cols, int group_size, int bits, int mode, float eps, float lr,
+                              float coef_lo, float coef_hi, float v_bound, int64_t row_block,
+                              int64_t row_stride, int64_t row_offset, void* wq_out, int wq_dtype,
+                              void* stream);
+
+/*
  * Pack one-byte codes into MLX uint32 words, element 0 in the least
  * significant bits; widths 3/5/6/7 use the cross-word bitstream.
  * Replaces mround/formats/packing.py:119-163 (pack_codes); oracle

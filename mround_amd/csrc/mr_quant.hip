@@ -353,6 +353,8 @@ __device__ __forceinline__ void coef_grads(const Group& p, float sum_s, float su
 
 struct StepArgs {
   float lr, lo, hi, vb;
+  void* wq;   // if non-null: W' of the updated parameters, through the placement
+  int wq_dt;  // its dtype
 };
 
 template <int WT, int GT, int MODE, bool UPDATE, int TPG>
@@ -415,9 +417,27 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
 #pragma unroll
     for (int k = 0; k < 8; ++k) nv[k] = clampf(vv[k] - st.lr * signf(gv[k]), -st.vb, st.vb);
     store8_f32_cached(v, e, nv);
+    // Every lane of the group holds the group sums, so each forms the new
+    // coefficients itself (the leader stores them).
+    const float na = clampf(a - st.lr * signf(ga), st.lo, st.hi);
+    const float nb = clampf(b - st.lr * signf(gb), st.lo, st.hi);
     if (leader) {
-      alpha[grp] = clampf(a - st.lr * signf(ga), st.lo, st.hi);
-      beta[grp] = clampf(b - st.lr * signf(gb), st.lo, st.hi);
+      alpha[grp] = na;
+      beta[grp] = nb;
+    }
+    if (st.wq) {
+      // The next step's W': the forward's arithmetic on the same group
+      // extremes and the parameters just written.
+      const Group p2 = group_params<MODE>(mx, mn, na, nb, base, maxq, eps);
+      float q[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float code, in;
+        q[k] = quant_one<MODE, true>(x[k], nv[k], p2, qmin, qmax, code, in);
+      }
+      if (st.wq_dt == MR_BF16) store8<MR_BF16>(st.wq, map.chunk_elem(chunk), q);
+      else if (st.wq_dt == MR_F16) store8<MR_F16>(st.wq, map.chunk_elem(chunk), q);
+      else store8<MR_F32>(st.wq, map.chunk_elem(chunk), q);
     }
   }
 }
@@ -474,6 +494,23 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
     if constexpr (UPDATE) {
       alpha[grp] = clampf(a - st.lr * signf(ga), st.lo, st.hi);
       beta[grp] = clampf(b - st.lr * signf(gb), st.lo, st.hi);
+    }
+  }
+  if constexpr (UPDATE) {
+    if (st.wq) {
+      // The next step's W' from the parameters just written (each lane
+      // rereads the v entries it wrote itself).
+      const float na = clampf(a - st.lr * signf(ga), st.lo, st.hi);
+      const float nb = clampf(b - st.lr * signf(gb), st.lo, st.hi);
+      const Group p2 = group_params<MODE>(mx, mn, na, nb, base, maxq, eps);
+      for (int t = lane; t < gs; t += 64) {
+        const int64_t c = c0 + t;
+        if (c >= cols) continue;
+        const float x = load_any(w, wt, r * cols + c);
+        float code, in;
+        const float q = quant_one<MODE, true>(x, v[grp * gs + t], p2, qmin, qmax, code, in);
+        store_any(st.wq, st.wq_dt, map.row(r) * cols + c, q);
+      }
     }
   }
 }
@@ -674,7 +711,8 @@ static int fq_backward_impl(const char* fn, const void* w, int w_dtype, float* v
                             int64_t rows, int64_t cols, int group_size, int bits, int mode,
                             float eps, int update, float lr, float coef_lo, float coef_hi,
                             float v_bound, float* grad_v_out, float* grad_alpha_out,
-                            float* grad_beta_out, mr::RowMap map, void* stream) {
+                            float* grad_beta_out, mr::RowMap map, void* stream,
+                            void* wq_out = nullptr, int wq_dtype = 0) {
   using namespace mr;
   clear_error();
   Shape sh;
@@ -691,8 +729,11 @@ static int fq_backward_impl(const char* fn, const void* w, int w_dtype, float* v
     return fail(MR_EINVAL, "%s: negative row placement", fn);
   if (map.blk && rows * cols / 8 > 0x7fffffffLL)
     return fail(MR_EINVAL, "%s: placed tensor too large", fn);
+  if (wq_out && !update) return fail(MR_EINVAL, "%s: W' is written only with the update", fn);
+  if (wq_out && !valid_dtype(wq_dtype)) return fail(MR_EINVAL, "%s: unknown W' dtype %d", fn, wq_dtype);
+  if (wq_out && !aligned16(wq_out)) return fail(MR_EINVAL, "%s: W' must be 16-byte aligned", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  StepArgs st{lr, coef_lo, coef_hi, v_bound};
+  StepArgs st{lr, coef_lo, coef_hi, v_bound, wq_out, wq_dtype};
 #define MR_BWD(MODE_)                                                                       \
   return update ? launch_bwd<MODE_, true>(sh, w, w_dtype, v, alpha, beta, init_scale, g,     \
                                           g_dtype, eps, st, grad_v_out, grad_alpha_out,      \
@@ -728,6 +769,22 @@ int mr_fq_backward_signsgd_mapped(const void* w, int w_dtype, float* v, float* a
                           g, g_dtype, rows, cols, group_size, bits, mode, eps, 1, lr, coef_lo,
                           coef_hi, v_bound, nullptr, nullptr, nullptr,
                           mr::RowMap{row_block, row_stride, row_offset, 0}, stream);
+}
+
+int mr_fq_step_requant_mapped(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                              const float* init_scale, const void* g, int g_dtype, int64_t rows,
+                              int64_t cols, int group_size, int bits, int mode, float eps, float lr,
+                              float coef_lo, float coef_hi, float v_bound, int64_t row_block,
+                              int64_t row_stride, int64_t row_offset, void* wq_out, int wq_dtype,
+                              void* stream) {
+  if (!wq_out) {
+    mr::clear_error();
+    return mr::fail(MR_EINVAL, "mr_fq_step_requant_mapped: W' output is null");
+  }
+  return fq_backward_impl("mr_fq_step_requant_mapped", w, w_dtype, v, alpha, beta, init_scale, g,
+                          g_dtype, rows, cols, group_size, bits, mode, eps, 1, lr, coef_lo, coef_hi,
+                          v_bound, nullptr, nullptr, nullptr,
+                          mr::RowMap{row_block, row_stride, row_offset, 0}, stream, wq_out, wq_dtype);
 }
 
 }  // extern "C"

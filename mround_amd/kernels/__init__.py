@@ -91,6 +91,8 @@ _SIGNATURES = {
                                   _L, _P]),
     "mr_fq_backward_signsgd_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F,
                                            _F, _F, _F, _F, _L, _L, _L, _P]),
+    "mr_fq_step_requant_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F, _F, _F,
+                                       _F, _F, _L, _L, _L, _P, _I, _P]),
     "mr_delta_loss_mapped": (_I, [_P, _I, _P, _L, _L, _I, _P, _I, _I, _F, _P, _L, _L, _L, _P, _P,
                                   _P]),
     "mr_cross_entropy": (_I, [_P, _L, _L, _L, _P, _F, _P, _P, _P, _L, _P]),
@@ -484,6 +486,22 @@ def fq_step_mapped(weight, v, alpha, beta, grad, *, bits, group_size, mode, eps,
         dtype_code(grad.dtype), rows, cols, group_size, bits, MODE[mode], eps, lr, coef_lo, coef_hi,
         v_bound, row_block, row_stride, row_offset, _stream(weight))
     _check(rc, "mr_fq_backward_signsgd_mapped")
+
+
+def fq_step_requant_mapped(weight, v, alpha, beta, grad, *, bits, group_size, mode, eps, lr, coef_lo,
+                           coef_hi, v_bound, row_block, row_stride, row_offset, wq_out,
+                           init_scale=None) -> None:
+    """``mr_fq_step_requant_mapped``: the fused step, then the new W' placed in ``wq_out``."""
+    rows, cols = weight.shape
+    if grad.shape[1] != cols or wq_out.shape[1] != cols:
+        raise KernelError("the placed gradient and W' must have the weight's column count")
+    rc = lib().mr_fq_step_requant_mapped(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(v, "v")), _ptr(_f32(alpha, "alpha")),
+        _ptr(_f32(beta, "beta")), _ptr(_f32(init_scale, "init_scale")), _ptr(grad),
+        dtype_code(grad.dtype), rows, cols, group_size, bits, MODE[mode], eps, lr, coef_lo, coef_hi,
+        v_bound, row_block, row_stride, row_offset, _ptr(wq_out), dtype_code(wq_out.dtype),
+        _stream(weight))
+    _check(rc, "mr_fq_step_requant_mapped")
 
 
 def copy_bytes(src, dst, nbytes: int) -> None:

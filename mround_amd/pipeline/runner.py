@@ -318,17 +318,25 @@ class QuantizationRunner:
                                 row_offset=p.row_offset, init_scale=layer.init_scale)
 
     def _step_all(self, eng: BlockEngine, layers: Mapping[str, _Layer], rates: Mapping[str, float],
-                  step: int) -> None:
+                  step: int, *, requant: bool = False) -> None:
+        """The fused sign-SGD step of every layer; with ``requant`` the same
+        kernels also write the new W' into the engine's fused operands (the
+        next step's forward, made without rereading W and v)."""
         iters = self.tuning.iters
         for name, layer in layers.items():
             p = layer.placement
             lo, hi = layer.scheme.coefficient_bounds
             lr = LinearDecay(rates[name], iters)(step)
-            K.fq_step_mapped(layer.weight, layer.v, layer.alpha, layer.beta, eng.dw[p.operand],
-                             bits=layer.scheme.bits, group_size=layer.scheme.group_size,
-                             mode=layer.mode, eps=self.eps, lr=lr, coef_lo=lo, coef_hi=hi,
-                             v_bound=V_BOUND, row_block=p.row_block, row_stride=p.row_stride,
-                             row_offset=p.row_offset, init_scale=layer.init_scale)
+            common = dict(bits=layer.scheme.bits, group_size=layer.scheme.group_size, mode=layer.mode,
+                          eps=self.eps, lr=lr, coef_lo=lo, coef_hi=hi, v_bound=V_BOUND,
+                          row_block=p.row_block, row_stride=p.row_stride, row_offset=p.row_offset,
+                          init_scale=layer.init_scale)
+            if requant:
+                K.fq_step_requant_mapped(layer.weight, layer.v, layer.alpha, layer.beta, eng.dw[p.operand],
+                                         wq_out=eng.wq[p.operand], **common)
+            else:
+                K.fq_step_mapped(layer.weight, layer.v, layer.alpha, layer.beta, eng.dw[p.operand],
+                                 **common)
 
     def _scores(self, eng, layers, inputs, targets, over, suppress, scratch) -> float:
         """Mean loss over batches ``over`` with the current parameters."""
@@ -361,14 +369,15 @@ class QuantizationRunner:
         t0 = time.perf_counter()
         iters = self.tuning.iters
         step_losses = torch.zeros(iters, dtype=torch.float32, device=eng.device)
+        self._quantize_all(eng, layers)
         for step in range(iters):
             b = tuning_batches[step % len(tuning_batches)]
-            self._quantize_all(eng, layers)
             eng.forward(inputs[b], scratch, save=True)
             step_losses[step:step + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress,
                                                       with_grad=True))
             eng.backward()
-            self._step_all(eng, layers, rates, step)
+            # the step also writes the next step's W'
+            self._step_all(eng, layers, rates, step, requant=True)
         torch.cuda.synchronize(eng.device)
         stages["tune"] = time.perf_counter() - t0
 

@@ -202,3 +202,46 @@ def test_mapped_placement(shape):
                          row_block=blk, row_stride=stride, row_offset=off)
         for k in p1:
             assert torch.equal(p1[k], p2[k]), k
+
+
+@pytest.mark.parametrize("shape", [(64, 512, 64), (96, 256, 32), (32, 200, -1)])
+@pytest.mark.parametrize("mode", ["asym", "sym", "searched"])
+def test_step_requant_writes_the_next_forward(shape, mode):
+    """The fused step that also writes W' leaves the parameters exactly as the
+    plain fused step does, and its W' (placed) is bit-identical to the forward
+    of the updated parameters; rows outside the placement are untouched."""
+    from mround_amd import kernels as K
+
+    rows, cols, gs = shape
+    print("case step requant", shape, mode, flush=True, file=sys.stderr)
+    w = weight(rows, cols, seed=rows + 1).to(dev())
+    v, a, b = params(rows, cols, gs, seed=4, coef_jitter=0.2)
+    ng = 1 if gs == -1 else cols // gs
+    init = None
+    if mode == "searched":
+        init = (torch.rand(rows, ng, generator=torch.Generator().manual_seed(6)) * 0.02 + 0.005).to(dev())
+    lo, hi = (0.5, 1.5) if mode == "searched" else (0.1, 1.0)
+    g = torch.randn(rows, cols, generator=torch.Generator().manual_seed(7)).to(dev()) * 1e-3
+    for blk, stride, off in ((rows, 0, 17), (32, 64, 32)):
+        if blk == 32 and rows % 32:
+            continue
+        idx = torch.tensor([(r // blk) * stride + off + r % blk for r in range(rows)]).to(dev())
+        gbig = torch.zeros(2 * rows + 64, cols, device=dev())
+        gbig[idx] = g
+        p1 = [t.clone().to(dev()).contiguous() for t in (v.reshape(rows, -1), a.reshape(rows, ng),
+                                                          b.reshape(rows, ng))]
+        p2 = [t.clone() for t in p1]
+        common = dict(bits=2, group_size=gs, mode=mode, eps=1e-8, lr=0.005, coef_lo=lo, coef_hi=hi,
+                      v_bound=0.5, row_block=blk, row_stride=stride, row_offset=off, init_scale=init)
+        K.fq_step_mapped(w, *p1, gbig, **common)
+        wbig = torch.full((2 * rows + 64, cols), 7.0, dtype=torch.bfloat16, device=dev())
+        K.fq_step_requant_mapped(w, *p2, gbig, wq_out=wbig, **common)
+        for x, y in zip(p1, p2):
+            assert torch.equal(x, y)
+        ref = torch.zeros_like(wbig)
+        K.fq_forward_mapped(w, *p1, bits=2, group_size=gs, mode=mode, eps=1e-8, wq_out=ref, row_block=blk,
+                            row_stride=stride, row_offset=off, init_scale=init)
+        assert torch.equal(wbig[idx], ref[idx])
+        mask = torch.ones(wbig.shape[0], dtype=torch.bool, device=dev())
+        mask[idx] = False
+        assert bool((wbig[mask] == 7.0).all())

@@ -419,8 +419,11 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     memory = M.check_memory(mshape, rshape, budget=budget)
     if memory_check:
         M.require_fits(memory)
-    if torch.cuda.is_available() and str(device).startswith("cuda"):
+    on_gpu = torch.cuda.is_available() and str(device).startswith("cuda")
+    held_before = 0
+    if on_gpu:  # the run's own peak: what the process already holds is left out
         torch.cuda.reset_peak_memory_stats(device)
+        held_before = torch.cuda.memory_allocated(device)
     t0 = time.perf_counter()
     m = load_model(model, device=device)
     load_s = time.perf_counter() - t0
@@ -486,8 +489,8 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         "storage": {"bits_per_weight": storage.bits_per_weight, "compression": storage.compression},
         "seconds": seconds,
         "memory": {**memory.record(), "library_workspaces": M.LIBRARY_WORKSPACES,
-                   "peak_allocated": int(torch.cuda.max_memory_allocated(device))
-                   if torch.cuda.is_available() and str(device).startswith("cuda") else None},
+                   "peak_allocated": int(torch.cuda.max_memory_allocated(device)) - held_before
+                   if on_gpu else None},
     }
     config_path = out / RUN_RECORD
     config_path.write_text(json.dumps(record, indent=2) + "\n")

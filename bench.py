@@ -20,12 +20,12 @@ Printed as one JSON line:
              timed region, against 2.5 PFLOP/s dense bf16;
   kernels    the same for every GEMM and attention launch of the block;
   fake_quant the kernel microbench: a bf16 18944 x 3584 weight (0.1 % of
-             entries x10), 2-bit gs64; forward, backward + update and packing
-             against 8 TB/s;
+             entries x10), 2-bit gs64; forward, backward + update, the update
+             that also writes the next W', and packing, against 8 TB/s;
   cpu_baseline  the oracle (float32 PyTorch block + NumPy fake quantization)
              timed on the host on a bounded sample, extrapolated to the tune.
 
-``--gpus N`` with N > 1 exits: this build runs on one GPU.
+``--gpus N`` with N > 1 exits: the benchmark runs on one GPU only.
 """
 
 from __future__ import annotations
@@ -362,8 +362,8 @@ def main(argv=None):
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs on one GPU; multi-GPU runs are not part of it "
-              "(how the path would shard is described in DESIGN.md)", file=sys.stderr)
+        print("bench.py: the benchmark runs on one GPU; a block tune is not sharded over "
+              "several GPUs here", file=sys.stderr)
         return 2
 
     import torch

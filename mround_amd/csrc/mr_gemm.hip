@@ -652,16 +652,31 @@ int launch(GemmParams p, hipStream_t s) {
   return MR_OK;
 }
 
-// Large problems use 256 x 256 tiles. Below one wave of them, a long K is
-// cut instead (the whole grid is then a k-split remainder): measured on the
-// weight-gradient shapes of the small models (M, N <= 3584, K = 16384) and the
-// short-sequence input gradients, 1.1-3.6x faster than 128 x 128 tiles, which
-// leave CUs idle when the output is small. Short K uses 128 x 128 tiles.
+// Large tiles unless small ones finish sooner. A long K (at least
+// kSplitMinKt steps) always takes 256 x 256 tiles: a remainder wave, or a
+// grid under one wave, is cut along K (measured on the weight gradients of the
+// small models, M, N <= 3584 and K = 16384, and the short-sequence input
+// gradients: 1.1-3.6x faster than small tiles, which leave CUs idle when the
+// output is small). Otherwise the two sizes are compared in whole waves: 256
+// large tiles per wave, 512 small ones (two per CU), a wave of small tiles
+// taking kSmallWave of a large one's time at the same K (0.58 measured with
+// K = 3584; 0.45 for K <= 1024, where the prologue and epilogue of the two
+// co-resident small tiles overlap each other's k loops). Small tiles win for
+// K = 896 (the 0.5B block: its qkv projection 1.6x faster) and when large
+// ones leave a last wave mostly idle (the 3B qkv projection: 2.5 waves). The
+// residual epilogue (an fp32 read and write per output) stays on large tiles:
+// measured, the 0.5B o projection ran 1.2x slower on small ones.
 template <bool AK, bool BKM, int EPI, bool OB>
 int dispatch(GemmParams p, hipStream_t s) {
+  const int KT = p.K / BK;
+  if (KT >= kSplitMinKt) return launch<256, 256, AK, BKM, EPI, OB>(p, s);
   const int64_t big = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
-  if (big >= 256 || p.K / BK >= kSplitMinKt) return launch<256, 256, AK, BKM, EPI, OB>(p, s);
-  return launch<128, 128, AK, BKM, EPI, OB>(p, s);
+  const int64_t small = static_cast<int64_t>((p.M + 127) / 128) * ((p.N + 127) / 128);
+  const double wave_small = KT <= 16 ? 0.45 : 0.58;
+  const double t_big = static_cast<double>((big + 255) / 256);
+  const double t_small = static_cast<double>((small + 511) / 512) * wave_small;
+  if (EPI != EPI_RESID && t_small < 0.97 * t_big) return launch<128, 128, AK, BKM, EPI, OB>(p, s);
+  return launch<256, 256, AK, BKM, EPI, OB>(p, s);
 }
 
 // Load offsets are 32-bit: 256 rows of a K-major tile span 256 * ld * 2 bytes.

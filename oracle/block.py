@@ -205,13 +205,15 @@ def mean_loss(inputs, targets, weights, biases, norms, params, shape, scheme, su
 
 
 def tune_block(inputs, targets, weights, biases, norms, shape: Shape, scheme: Scheme, *, iters: int,
-               lr: float, suppress: bool, eps: float = 1e-8):
-    """``QuantizationRunner._tune`` (``mround/pipeline/runner.py:790-953``) without holdout."""
+               lr: float, suppress: bool, eps: float = 1e-8, steps: int | None = None):
+    """``QuantizationRunner._tune`` (``mround/pipeline/runner.py:790-953``) without holdout.
+    ``steps`` stops after that many steps of the ``iters``-step schedule (the
+    final score and the revert rule then apply to the parameters reached)."""
     params = init_params(weights, scheme)
     start = {n: tuple(t.clone() for t in p) for n, p in params.items()}
     initial = mean_loss(inputs, targets, weights, biases, norms, start, shape, scheme, suppress, eps)
     losses = []
-    for step in range(iters):
+    for step in range(iters if steps is None else min(steps, iters)):
         b = step % len(inputs)
         loss, grads = step_grads(inputs[b], targets[b], weights, biases, norms, params, shape,
                                  scheme, suppress, eps)

@@ -119,6 +119,23 @@ int mr_fq_step_requant_mapped(const void* w, int w_dtype, float* v, float* alpha
                               void* stream);
 
 /*
+ * The same with the rate read on the device: lr = lr_table[*step] (the index
+ * clamped to [0, lr_len)), both device pointers, so that a recorded sequence
+ * of launches (a HIP graph of one tuning step) replays with each step's rate
+ * of the LinearDecay schedule (mround/core/signsgd.py:23-40). mr_counter_add
+ * advances the step index inside the same sequence.
+ */
+int mr_fq_step_requant_mapped_sched(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                                    const float* init_scale, const void* g, int g_dtype,
+                                    int64_t rows, int64_t cols, int group_size, int bits, int mode,
+                                    float eps, const float* lr_table, int lr_len, const int* step,
+                                    float coef_lo, float coef_hi, float v_bound, int64_t row_block,
+                                    int64_t row_stride, int64_t row_offset, void* wq_out,
+                                    int wq_dtype, void* stream);
+/* counter[0] += delta on the stream (device int). No counterpart in the reference. */
+int mr_counter_add(int* counter, int delta, void* stream);
+
+/*
  * Pack one-byte codes into MLX uint32 words, element 0 in the least
  * significant bits; widths 3/5/6/7 use the cross-word bitstream.
  * Replaces mround/formats/packing.py:119-163 (pack_codes); oracle

@@ -39,11 +39,25 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src
   }
 }
 
+// counter[0] += delta, one lane (a vector store).
+__global__ void counter_add_kernel(int* counter, int delta) {
+  if (threadIdx.x == 0) counter[0] = counter[0] + delta;
+}
+
 }  // namespace mr
 
 extern "C" {
 
 const char* mr_last_error(void) { return mr::g_last_error; }
+
+int mr_counter_add(int* counter, int delta, void* stream) {
+  mr::clear_error();
+  if (!counter) return mr::fail(MR_EINVAL, "mr_counter_add: null counter");
+  hipLaunchKernelGGL(mr::counter_add_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     counter, delta);
+  MR_LAUNCH_CHECK("mr_counter_add");
+  return MR_OK;
+}
 
 int mr_abi_version(void) { return 1; }
 

@@ -355,6 +355,16 @@ struct StepArgs {
   float lr, lo, hi, vb;
   void* wq;   // if non-null: W' of the updated parameters, through the placement
   int wq_dt;  // its dtype
+  // If non-null, the rate is lr_tab[clamp(*step, 0, lr_len - 1)] (a schedule
+  // in device memory, for launches recorded once and replayed every step).
+  const float* lr_tab;
+  const int* step;
+  int lr_len;
+  __device__ __forceinline__ float rate() const {
+    if (!lr_tab) return lr;
+    const int i = min(max(*step, 0), lr_len - 1);
+    return lr_tab[i];
+  }
 };
 
 template <int WT, int GT, int MODE, bool UPDATE, int TPG>
@@ -364,6 +374,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
     int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps,
     StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
     float* __restrict__ gb_out, RowMap map) {
+  if constexpr (UPDATE) st.lr = st.rate();
   int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const bool active = chunk < n_chunks;
   if (!active) chunk = n_chunks - 1;
@@ -449,6 +460,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
     int gt, int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float qmin, float qmax,
     float eps, StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
     float* __restrict__ gb_out, RowMap map) {
+  if constexpr (UPDATE) st.lr = st.rate();
   const int64_t grp = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   if (grp >= rows * ng) return;
@@ -712,7 +724,9 @@ static int fq_backward_impl(const char* fn, const void* w, int w_dtype, float* v
                             float eps, int update, float lr, float coef_lo, float coef_hi,
                             float v_bound, float* grad_v_out, float* grad_alpha_out,
                             float* grad_beta_out, mr::RowMap map, void* stream,
-                            void* wq_out = nullptr, int wq_dtype = 0) {
+                            void* wq_out = nullptr, int wq_dtype = 0,
+                            const float* lr_tab = nullptr, const int* step = nullptr,
+                            int lr_len = 0) {
   using namespace mr;
   clear_error();
   Shape sh;
@@ -730,10 +744,12 @@ static int fq_backward_impl(const char* fn, const void* w, int w_dtype, float* v
   if (map.blk && rows * cols / 8 > 0x7fffffffLL)
     return fail(MR_EINVAL, "%s: placed tensor too large", fn);
   if (wq_out && !update) return fail(MR_EINVAL, "%s: W' is written only with the update", fn);
+  if (lr_tab && (!step || lr_len < 1 || !update))
+    return fail(MR_EINVAL, "%s: a rate schedule needs the step counter, its length and the update", fn);
   if (wq_out && !valid_dtype(wq_dtype)) return fail(MR_EINVAL, "%s: unknown W' dtype %d", fn, wq_dtype);
   if (wq_out && !aligned16(wq_out)) return fail(MR_EINVAL, "%s: W' must be 16-byte aligned", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  StepArgs st{lr, coef_lo, coef_hi, v_bound, wq_out, wq_dtype};
+  StepArgs st{lr, coef_lo, coef_hi, v_bound, wq_out, wq_dtype, lr_tab, step, lr_len};
 #define MR_BWD(MODE_)                                                                       \
   return update ? launch_bwd<MODE_, true>(sh, w, w_dtype, v, alpha, beta, init_scale, g,     \
                                           g_dtype, eps, st, grad_v_out, grad_alpha_out,      \
@@ -785,6 +801,24 @@ int mr_fq_step_requant_mapped(const void* w, int w_dtype, float* v, float* alpha
                           g_dtype, rows, cols, group_size, bits, mode, eps, 1, lr, coef_lo, coef_hi,
                           v_bound, nullptr, nullptr, nullptr,
                           mr::RowMap{row_block, row_stride, row_offset, 0}, stream, wq_out, wq_dtype);
+}
+
+int mr_fq_step_requant_mapped_sched(const void* w, int w_dtype, float* v, float* alpha, float* beta,
+                                    const float* init_scale, const void* g, int g_dtype,
+                                    int64_t rows, int64_t cols, int group_size, int bits, int mode,
+                                    float eps, const float* lr_table, int lr_len, const int* step,
+                                    float coef_lo, float coef_hi, float v_bound, int64_t row_block,
+                                    int64_t row_stride, int64_t row_offset, void* wq_out,
+                                    int wq_dtype, void* stream) {
+  if (!wq_out || !lr_table || !step) {
+    mr::clear_error();
+    return mr::fail(MR_EINVAL, "mr_fq_step_requant_mapped_sched: null W', schedule or step");
+  }
+  return fq_backward_impl("mr_fq_step_requant_mapped_sched", w, w_dtype, v, alpha, beta, init_scale,
+                          g, g_dtype, rows, cols, group_size, bits, mode, eps, 1, 0.0f, coef_lo,
+                          coef_hi, v_bound, nullptr, nullptr, nullptr,
+                          mr::RowMap{row_block, row_stride, row_offset, 0}, stream, wq_out, wq_dtype,
+                          lr_table, step, lr_len);
 }
 
 }  // extern "C"

@@ -93,6 +93,9 @@ _SIGNATURES = {
                                            _F, _F, _F, _F, _L, _L, _L, _P]),
     "mr_fq_step_requant_mapped": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F, _F, _F,
                                        _F, _F, _L, _L, _L, _P, _I, _P]),
+    "mr_fq_step_requant_mapped_sched": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F,
+                                             _P, _I, _P, _F, _F, _F, _L, _L, _L, _P, _I, _P]),
+    "mr_counter_add": (_I, [_P, _I, _P]),
     "mr_delta_loss_mapped": (_I, [_P, _I, _P, _L, _L, _I, _P, _I, _I, _F, _P, _L, _L, _L, _P, _P,
                                   _P]),
     "mr_cross_entropy": (_I, [_P, _L, _L, _L, _P, _F, _P, _P, _P, _L, _P]),
@@ -502,6 +505,31 @@ def fq_step_requant_mapped(weight, v, alpha, beta, grad, *, bits, group_size, mo
         v_bound, row_block, row_stride, row_offset, _ptr(wq_out), dtype_code(wq_out.dtype),
         _stream(weight))
     _check(rc, "mr_fq_step_requant_mapped")
+
+
+def fq_step_requant_sched(weight, v, alpha, beta, grad, *, bits, group_size, mode, eps, lr_table, step,
+                          coef_lo, coef_hi, v_bound, row_block, row_stride, row_offset, wq_out,
+                          init_scale=None) -> None:
+    """``mr_fq_step_requant_mapped_sched``: the rate is ``lr_table[step[0]]`` on the device."""
+    rows, cols = weight.shape
+    if grad.shape[1] != cols or wq_out.shape[1] != cols:
+        raise KernelError("the placed gradient and W' must have the weight's column count")
+    if step.dtype != torch.int32:
+        raise KernelError("the step counter is int32")
+    rc = lib().mr_fq_step_requant_mapped_sched(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(v, "v")), _ptr(_f32(alpha, "alpha")),
+        _ptr(_f32(beta, "beta")), _ptr(_f32(init_scale, "init_scale")), _ptr(grad),
+        dtype_code(grad.dtype), rows, cols, group_size, bits, MODE[mode], eps,
+        _ptr(_f32(lr_table, "lr_table")), lr_table.numel(), _ptr(step), coef_lo, coef_hi, v_bound,
+        row_block, row_stride, row_offset, _ptr(wq_out), dtype_code(wq_out.dtype), _stream(weight))
+    _check(rc, "mr_fq_step_requant_mapped_sched")
+
+
+def counter_add(counter, delta: int = 1) -> None:
+    """``mr_counter_add``: ``counter[0] += delta`` on the current stream (int32)."""
+    if counter.dtype != torch.int32:
+        raise KernelError("the counter is int32")
+    _check(lib().mr_counter_add(_ptr(counter), delta, _stream(counter)), "mr_counter_add")
 
 
 def copy_bytes(src, dst, nbytes: int) -> None:

@@ -27,6 +27,11 @@ from mround_amd.pipeline.block import LAYERS, BlockEngine, BlockShape, BlockWeig
 from mround_amd.schemes import DEFAULT_EPS_FP32, QuantScheme, ScaleInit, TuningConfig
 
 V_BOUND = 0.5
+# Steps replay recorded graphs when a batch is at most this many
+# (token x hidden) elements and each batch's graph would replay at least
+# GRAPH_MIN_REPLAYS times (see QuantizationRunner._use_graphs).
+GRAPH_MAX_ELEMENTS = 4096 * 1024
+GRAPH_MIN_REPLAYS = 20
 
 
 @dataclasses.dataclass
@@ -128,7 +133,8 @@ class QuantizationRunner:
     def __init__(self, scheme: QuantScheme, tuning: TuningConfig, *,
                  progress: Callable[[BlockResult], None] | None = None,
                  eps: float = DEFAULT_EPS_FP32, quantized_inputs: bool = True,
-                 holdout_batches: int = 0, per_layer_recipe: bool = False) -> None:
+                 holdout_batches: int = 0, per_layer_recipe: bool = False,
+                 graphs: bool | None = None) -> None:
         if holdout_batches < 0:
             msg = f"holdout_batches must be zero or more, got {holdout_batches}"
             raise CalibrationError(msg)
@@ -139,6 +145,7 @@ class QuantizationRunner:
         self.quantized_inputs = quantized_inputs
         self.holdout_batches = holdout_batches
         self.per_layer_recipe = per_layer_recipe
+        self.graphs = graphs  # None: decided per block (see _use_graphs)
         self._engines: dict = {}
 
     def _scheme_for(self, path: str, overrides: Mapping[str, QuantScheme] | None) -> QuantScheme:
@@ -338,6 +345,32 @@ class QuantizationRunner:
                 K.fq_step_mapped(layer.weight, layer.v, layer.alpha, layer.beta, eng.dw[p.operand],
                                  **common)
 
+    def _use_graphs(self, eng: BlockEngine, n_batches: int) -> bool:
+        """Whether the tuning steps replay a recorded HIP graph per batch: when
+        the host's launch latency, not the kernels, bounds a step (a few
+        batches of a small block) and no launch is being timed. Each batch's
+        graph is recorded once per block and replayed on every later step
+        that uses the batch; the rates come from a schedule in device memory
+        indexed by a device step counter the graph advances."""
+        if self.graphs is not None:
+            return bool(self.graphs) and eng.timers is None
+        small = eng.tokens * eng.shape.hidden <= GRAPH_MAX_ELEMENTS
+        return eng.timers is None and small and n_batches * GRAPH_MIN_REPLAYS <= self.tuning.iters
+
+    def _step_all_scheduled(self, eng: BlockEngine, layers: Mapping[str, _Layer],
+                            sched: Mapping[str, torch.Tensor], counter: torch.Tensor) -> None:
+        """``_step_all(requant=True)`` with each layer's rate read on the device
+        from its schedule at the step counter."""
+        for name, layer in layers.items():
+            p = layer.placement
+            lo, hi = layer.scheme.coefficient_bounds
+            K.fq_step_requant_sched(layer.weight, layer.v, layer.alpha, layer.beta, eng.dw[p.operand],
+                                    bits=layer.scheme.bits, group_size=layer.scheme.group_size,
+                                    mode=layer.mode, eps=self.eps, lr_table=sched[name], step=counter,
+                                    coef_lo=lo, coef_hi=hi, v_bound=V_BOUND, row_block=p.row_block,
+                                    row_stride=p.row_stride, row_offset=p.row_offset,
+                                    wq_out=eng.wq[p.operand], init_scale=layer.init_scale)
+
     def _scores(self, eng, layers, inputs, targets, over, suppress, scratch) -> float:
         """Mean loss over batches ``over`` with the current parameters."""
         self._quantize_all(eng, layers)
@@ -370,14 +403,38 @@ class QuantizationRunner:
         iters = self.tuning.iters
         step_losses = torch.zeros(iters, dtype=torch.float32, device=eng.device)
         self._quantize_all(eng, layers)
+        graphs = self._use_graphs(eng, len(tuning_batches))
+        if graphs:
+            sched = {n: torch.tensor([LinearDecay(rates[n], iters)(t) for t in range(iters)],
+                                     dtype=torch.float32, device=eng.device) for n in layers}
+            counter = torch.zeros(1, dtype=torch.int32, device=eng.device)
+            captured: dict[int, torch.cuda.CUDAGraph] = {}
         for step in range(iters):
             b = tuning_batches[step % len(tuning_batches)]
-            eng.forward(inputs[b], scratch, save=True)
-            step_losses[step:step + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress,
-                                                      with_grad=True))
-            eng.backward()
-            # the step also writes the next step's W'
-            self._step_all(eng, layers, rates, step, requant=True)
+            if not graphs or step == 0:
+                # (step 0 runs eagerly: it also allocates any library workspace
+                # the step needs before a graph records it)
+                eng.forward(inputs[b], scratch, save=True)
+                step_losses[step:step + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress,
+                                                          with_grad=True))
+                eng.backward()
+                # the step also writes the next step's W'
+                self._step_all(eng, layers, rates, step, requant=True)
+                if graphs:
+                    counter.fill_(1)
+                continue
+            g = captured.get(b)
+            if g is None:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    eng.forward(inputs[b], scratch, save=True)
+                    eng.loss(scratch, targets[b], suppress=suppress, with_grad=True)
+                    eng.backward()
+                    self._step_all_scheduled(eng, layers, sched, counter)
+                    K.counter_add(counter, 1)
+                captured[b] = g
+            g.replay()
+            step_losses[step:step + 1].copy_(eng.loss_val)
         torch.cuda.synchronize(eng.device)
         stages["tune"] = time.perf_counter() - t0
 

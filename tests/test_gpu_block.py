@@ -203,3 +203,29 @@ def test_commit_codes_match_oracle_bitwise():
         assert np.array_equal(q.zero_point.cpu().numpy(), zp.reshape(q.zero_point.shape))
         assert np.array_equal(block.weights.linears[n].float().cpu().numpy(),
                               OQ.round_to_bf16(wq.astype(np.float32)))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_recorded_steps_equal_eager_steps(bits):
+    """Tuning steps replayed from per-batch HIP graphs (rates read on the
+    device) give bit-identical step losses, final loss and committed codes to
+    the eager launches; each graph is replayed several times with eager work
+    (the loss copy) and a synchronization between replays."""
+    print("case graphs", bits, flush=True, file=sys.stderr)
+    iters = 9
+    out = []
+    for graphs in (False, True):
+        shape, B, S, w, inputs, targets = _tiny_tune(bits, iters)
+        scheme = QuantScheme(bits=bits, group_size=64, symmetry=Symmetry.ASYMMETRIC)
+        tuning = TuningConfig(iters=iters, batch_size=B, n_samples=2 * B, seq_len=S, lr=0.005)
+        runner = QuantizationRunner(scheme, tuning, graphs=graphs)
+        block = DecoderBlock(0, "model.layers.0", shape, _to_dev(w))
+        res, layers = runner.quantize_block(block, [t.to(dev()) for t in inputs],
+                                            [t.to(dev()) for t in targets], path_prefix=block.name)
+        torch.cuda.synchronize()
+        out.append((res, {k: v.codes.cpu() for k, v in layers.items()}))
+    (r0, c0), (r1, c1) = out
+    assert r0.step_losses == r1.step_losses
+    assert r0.initial_loss == r1.initial_loss and r0.final_loss == r1.final_loss
+    for k in c0:
+        assert torch.equal(c0[k], c1[k]), k

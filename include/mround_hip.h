@@ -8,9 +8,14 @@
  * (mround_amd/kernels/__init__.py) under the reference's own function names.
  *
  * Conventions shared by every entry point:
- *   - All array arguments are device pointers owned by the caller; nothing
- *     here allocates device memory. Reductions take a caller-provided
- *     workspace whose size the matching *_workspace_bytes() query returns.
+ *   - All array arguments are device pointers owned by the caller.
+ *     Reductions take a caller-provided workspace whose size the matching
+ *     *_workspace_bytes() query returns. Two entry points keep an internal
+ *     workspace of their own, allocated on their first call on a device and
+ *     held until the process ends: the GEMMs (mr_gemm, mr_gemm_swiglu,
+ *     mr_gemm_swiglu_bwd share the k-split partials) and mr_attn_bwd (dK/dV
+ *     partials), 128 MB each per device. No other call allocates device
+ *     memory.
  *   - Every call enqueues work on `stream` (a hipStream_t, NULL = default
  *     stream) and returns without synchronising.
  *   - The return value is MR_OK, MR_EINVAL (bad shape or argument, checked on

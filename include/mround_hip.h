@@ -263,7 +263,8 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
  * [M, N], from the row-interleaved weight Wgu [2N, K] (rows 64b .. 64b+31 are
  * gate rows 32b .. 32b+31, rows 64b+32 .. 64b+63 the matching up rows; the
  * fake-quant forward writes this layout directly). Optionally also the bf16
- * gate and up values, gu [M, 2N], interleaved the same way by column.
+ * gate and up values, gu [M, 2N], interleaved the same way by column. X, Wgu,
+ * act and gu are 16-byte aligned with leading dimensions multiples of 8.
  * Replaces the mlp's gate/up linears and `nn.silu(g) * u` of the mlx-lm
  * block reached at mround/pipeline/blocks.py:605.
  */

@@ -222,6 +222,12 @@ template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int WM = BM / kWaveRows, WN = BN / (kWaves / kWaveRows);
   constexpr int TM = WM / 32, TN = WN / 32;
+  // The SwiGLU forward feeds the MFMA with W as the first operand and X as the
+  // second, so that each accumulator holds C transposed: lane l then owns row
+  // l % 32 of its 32 x 32 block and, in register group gi, the 4 consecutive
+  // columns 8 gi + 4 (l / 32) .. + 3, which the epilogue packs into 8-byte
+  // pieces. (Every output element is the same k-ordered sum either way.)
+  constexpr bool SWAP = EPI == EPI_SWIGLU;
   // Two LDS stages as four distinct arrays, indexed only with compile-time
   // stage numbers (the k loop below is unrolled by two), so that the waits
   // for the direct-to-LDS loads into one stage are not placed in front of the
@@ -353,7 +359,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
       auto mm = [&](auto ijc) {
         constexpr int i = decltype(ijc)::value / TN, j = decltype(ijc)::value % TN;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
+        if constexpr (SWAP)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cur][i], bfr[cur][j], acc[i][j], 0, 0, 0);
       };
       StaticFor<0, TM * TN>::run(mm);
     };
@@ -397,39 +406,90 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
     float* out = p.ws + (static_cast<int64_t>(bid) * p.ksplit + split) * (BM * BN);
     auto tile = [&](auto ij) {
       constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
+      if constexpr (SWAP) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        out[(wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3)) * BN + wn * WN + j * 32 + lcol] =
-            acc[i][j][r];
+        for (int gi = 0; gi < 4; ++gi)
+          *reinterpret_cast<float4*>(out + (wm * WM + i * 32 + lcol) * BN + wn * WN + j * 32 + gi * 8 + lrow) =
+              make_float4(acc[i][j][4 * gi], acc[i][j][4 * gi + 1], acc[i][j][4 * gi + 2], acc[i][j][4 * gi + 3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          out[(wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3)) * BN + wn * WN + j * 32 + lcol] =
+              acc[i][j][r];
+      }
     };
     StaticFor<0, TM * TN>::run(tile);
     return;
   }
   if constexpr (EPI == EPI_SWIGLU) {
     // B rows interleave 32 gate rows and 32 up rows, and a wave's column
-    // range starts on a multiple of 64: tile j = 2q holds gate columns and
-    // j = 2q + 1 the up columns for the same 32 act columns.
+    // range starts on a multiple of 64: block j = 2q holds gate columns and
+    // j = 2q + 1 the up columns of the same 32 act columns (accumulators are
+    // transposed, see SWAP). Each 32-row slice of the wave's act and gate/up
+    // outputs is staged in a private LDS region (the k loop's stages are free
+    // after its last barrier) and leaves in whole 16-byte row pieces: the
+    // stores then cover full cache lines instead of 64-byte row pieces.
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+    auto pack4 = [](float a, float b, float c, float d) {
+      u32x2 v;
+      v.x = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+      v.y = static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16);
+      return v;
+    };
+    constexpr int REGION = (BM + BN) * ROW_BYTES * 2 / kWaves;  // bytes of LDS per wave
+    // Row pitches of the staged act (WN / 2 columns) and gate/up (WN columns)
+    // slices: 16 bytes of padding put the 8-byte writes of rows r and r + 16
+    // in different banks only two ways apart, and keep rows 16-byte aligned.
+    constexpr int PA = WN + 16, PG = 2 * WN + 16;
+    static_assert(32 * (PA + PG) <= REGION, "SwiGLU staging does not fit the wave's LDS share");
+    static_assert(2 * REGION == BM * ROW_BYTES && 2 * REGION == BN * ROW_BYTES, "two waves per LDS array");
+    uint8_t* arr = wave < 2 ? As0 : wave < 4 ? As1 : wave < 6 ? Bs0 : Bs1;
+    lds_u8* sa = (lds_u8*)(arr + (wave & 1) * REGION);
+    lds_u8* sg = sa + 32 * PA;
     uint16_t* act = static_cast<uint16_t*>(p.C);
+    constexpr int CA = WN / 16, CG = 2 * WN / 16;  // 16-byte pieces per staged row
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int q = 0; q < TN / 2; ++q) {
-        const int gcol = n0 + wn * WN + 2 * q * 32 + lcol;  // interleaved column of gate
-        const int col = (n0 + wn * WN) / 2 + q * 32 + lcol;  // act column
         const f32x16 gt = acc[i][2 * q];
         const f32x16 ut = acc[i][2 * q + 1];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
-          if (row < p.M && col < p.n_out) {
-            const float g = gt[r];
-            const float u = ut[r];
-            act[static_cast<int64_t>(row) * p.ldc + col] = f32_to_bf16(silu(g) * u);
-            if (p.gu) {
-              p.gu[static_cast<int64_t>(row) * p.ldgu + gcol] = f32_to_bf16(g);
-              p.gu[static_cast<int64_t>(row) * p.ldgu + gcol + 32] = f32_to_bf16(u);
-            }
-          }
+        for (int gi = 0; gi < 4; ++gi) {
+          float a[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[e] = silu(gt[gi * 4 + e]) * ut[gi * 4 + e];
+          const int c = gi * 8 + lrow;
+          *(lds_u32x2*)(sa + lcol * PA + (q * 32 + c) * 2) = pack4(a[0], a[1], a[2], a[3]);
+          *(lds_u32x2*)(sg + lcol * PG + (2 * q * 32 + c) * 2) =
+              pack4(gt[gi * 4], gt[gi * 4 + 1], gt[gi * 4 + 2], gt[gi * 4 + 3]);
+          *(lds_u32x2*)(sg + lcol * PG + (2 * q * 32 + 32 + c) * 2) =
+              pack4(ut[gi * 4], ut[gi * 4 + 1], ut[gi * 4 + 2], ut[gi * 4 + 3]);
+        }
+      }
+      // The same wave reads back what it wrote (LDS keeps a wave's accesses
+      // in order), then the next slice overwrites the region.
+      const int row0 = m0 + wm * WM + i * 32;
+#pragma unroll
+      for (int it = 0; it < 32 * CA / 64; ++it) {
+        const int idx = it * 64 + lane, r = idx / CA, ch = idx % CA;
+        const u32x4 v = *(lds_u32x4*)(sa + r * PA + ch * 16);
+        const int col = (n0 + wn * WN) / 2 + ch * 8;
+        if (row0 + r < p.M && col < p.n_out)
+          *reinterpret_cast<u32x4*>(act + static_cast<int64_t>(row0 + r) * p.ldc + col) = v;
+      }
+      if (p.gu) {
+#pragma unroll
+        for (int it = 0; it < 32 * CG / 64; ++it) {
+          const int idx = it * 64 + lane, r = idx / CG, ch = idx % CG;
+          const u32x4 v = *(lds_u32x4*)(sg + r * PG + ch * 16);
+          const int col = n0 + wn * WN + ch * 8;
+          if (row0 + r < p.M && col < 2 * p.n_out)
+            *reinterpret_cast<u32x4*>(p.gu + static_cast<int64_t>(row0 + r) * p.ldgu + col) = v;
         }
       }
     }
@@ -751,8 +811,9 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
   if (!X || !Wgu || !act) return fail(MR_EINVAL, "mr_gemm_swiglu: null operand");
   if (M % 8 || N % 32 || K % BK || K == 0)
     return fail(MR_EINVAL, "mr_gemm_swiglu: M %% 8, N %% 32 and K %% %d must be 0", BK);
-  if (!ok16(X, ldx) || !ok16(Wgu, ldw))
-    return fail(MR_EINVAL, "mr_gemm_swiglu: operands must be 16-byte aligned");
+  if (!ok16(X, ldx) || !ok16(Wgu, ldw) || !ok16(act, ldact) || (gu && !ok16(gu, ldgu)))
+    return fail(MR_EINVAL, "mr_gemm_swiglu: operands and outputs must be 16-byte aligned with leading "
+                "dimensions multiples of 8");
   if (ldx < K || ldw < K || ldact < N || (gu && ldgu < 2 * N) || ldx > kMaxLd || ldw > kMaxLd)
     return fail(MR_EINVAL, "mr_gemm_swiglu: bad leading dimension");
   GemmParams p{};

@@ -166,6 +166,31 @@ def test_gemm_small_grid_long_k(layout, out, mn):
     assert bool(torch.all((c.float() - ref).abs() <= tol))
 
 
+# 17 x 16 = 272 large tiles: one whole wave and a last wave of 16, which runs
+# as quarter tiles; with M = 4160 the lower quarters of the last tile row lie
+# wholly past the edge, and N = 4056 cuts the last tile column.
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_gemm_quarter_tile_tail(layout, out):
+    M, N, Kd = 4160, 4056, 192
+    print("case gemm quarter-tile tail", layout, out, flush=True, file=sys.stderr)
+    if layout == "nt":
+        a, b = _rand(M, Kd, seed=53).to(dev()), _rand(N, Kd, seed=54).to(dev())
+        ref, bound = _gpu_ref(a, b.t().contiguous())
+    elif layout == "nn":
+        a, b = _rand(M, Kd, seed=55).to(dev()), _rand(Kd, N, seed=56).to(dev())
+        ref, bound = _gpu_ref(a, b)
+    else:
+        a, b = _rand(Kd, M, seed=57).to(dev()), _rand(Kd, N, seed=58).to(dev())
+        ref, bound = _gpu_ref(a.t().contiguous(), b)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(59)).to(dev())
+    c = torch.full((M, N), 7.0, dtype=out, device=dev())
+    K.gemm(layout, a, b, c, M=M, N=N, K=Kd, bias=bias)
+    ref = ref + bias
+    tol = bound + ref.abs() * (2.0**-8 if out == torch.bfloat16 else 2.0**-23)
+    assert bool(torch.all((c.float() - ref).abs() <= tol))
+
+
 def test_gemm_small_grid_bias_residual_and_swiglu():
     M, N, Kd = 328, 256, 6144
     print("case gemm small grid epilogues", flush=True, file=sys.stderr)

@@ -244,7 +244,8 @@ int mr_embed_rows(const void* table, int dtype, int64_t V, int64_t H, int64_t ld
  *        MR_NN: A = dY [M, K], B = W [K, N] (input gradient, dx = dy W)
  *        MR_TN: A = dY [K, M], B = X [K, N] (weight gradient, dW = dy^T x)
  * All row-major with leading dimensions lda/ldb/ldc/ldr in elements; M, N
- * multiples of 8, K a multiple of 64, operands 16-byte aligned. C is fp32 or
+ * multiples of 8, K a multiple of 64, operands, C and resid 16-byte aligned
+ * with rows a multiple of 16 bytes apart. C is fp32 or
  * bf16; with resid (fp32) C is fp32. Long-K problems whose 256 x 256 tiles
  * leave a partial last wave sum that remainder from k-split partial tiles in
  * a 128 MB device workspace the library allocates on the first such call on

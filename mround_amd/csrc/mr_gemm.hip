@@ -11,8 +11,11 @@
 //
 // Tiling: a block of 512 threads (8 waves of 64, 4 x 2) owns a BM x BN tile
 // of C; each wave owns (BM/4) x (BN/2) as a grid of 32 x 32 accumulators fed by
-// v_mfma_f32_32x32x16_bf16 (lane l: A row l%32, B column l%32, k half l/32;
-// accumulator register r: row (r/4)*8 + (l/32)*4 + r%4, column l%32). Every
+// v_mfma_f32_32x32x16_bf16 (lane l: first operand row l%32, second operand
+// row l%32, k half l/32; accumulator register r: first-operand index
+// (r/4)*8 + (l/32)*4 + r%4, second-operand index l%32; the epilogues that
+// stage their tile through LDS pass B first, so a lane holds one row of C and
+// runs of 4 consecutive columns). Every
 // operand tile moves HBM -> LDS by direct buffer loads (buffer_load ... lds,
 // no registers) in the layout it has in memory: a K-major tile as rows of 64
 // k, whose MFMA operand is one 16-byte LDS read; an MN-major tile as rows of
@@ -225,12 +228,13 @@ template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int WM = BM / kWaveRows, WN = BN / (kWaves / kWaveRows);
   constexpr int TM = WM / 32, TN = WN / 32;
-  // The SwiGLU forward feeds the MFMA with W as the first operand and X as the
-  // second, so that each accumulator holds C transposed: lane l then owns row
-  // l % 32 of its 32 x 32 block and, in register group gi, the 4 consecutive
-  // columns 8 gi + 4 (l / 32) .. + 3, which the epilogue packs into 8-byte
-  // pieces. (Every output element is the same k-ordered sum either way.)
-  constexpr bool SWAP = EPI == EPI_SWIGLU;
+  // Every epilogue but the SwiGLU backward feeds the MFMA with B as the first
+  // operand and A as the second, so that each accumulator holds C
+  // transposed: lane l then owns row l % 32 of its 32 x 32 block and, in
+  // register group gi, the 4 consecutive columns 8 gi + 4 (l / 32) .. + 3,
+  // which the epilogue writes to LDS as one 8- or 16-byte piece. (Every
+  // output element is the same k-ordered sum either way.)
+  constexpr bool SWAP = EPI != EPI_SWIGLU_BWD;
   // Two LDS stages as four distinct arrays, indexed only with compile-time
   // stage numbers (the k loop below is unrolled by two), so that the waits
   // for the direct-to-LDS loads into one stage are not placed in front of the
@@ -540,34 +544,80 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       }
     };
     StaticFor<0, TM * TN>::run(tile);
-  } else {
-    auto tile = [&](auto ij) {
-      constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
-      const int col = n0 + wn * WN + j * 32 + lcol;
-      const float bias = (p.bias && col < p.N) ? p.bias[col] : 0.0f;
-      float res[16];
-      if constexpr (EPI == EPI_RESID) {
-        // unguarded loads at clamped addresses, all in flight together
-        const int col_c = min(col, p.N - 1);
+  } else {  // EPI_STORE, EPI_RESID
+    // The transposed accumulators (plus bias) are staged per 32-row slice and
+    // JH column blocks in the wave's LDS share, then leave as 16-byte row
+    // pieces (the residual added on the way): whole cache lines instead of
+    // 64-byte (bf16) row pieces, and a quarter of the store instructions.
+    // Measured on the 7B block: q/k/v projection 9 %, attention-output input
+    // gradient 10 %, fp32 outputs 1-4 % faster.
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    constexpr int OBY = OUT_BF16 ? 2 : 4;
+    constexpr int REGION = (BM + BN) * ROW_BYTES * 2 / kWaves;
+    constexpr int JH = (32 * (TN * 32 * OBY + 16) <= REGION) ? TN : (32 * (2 * 32 * OBY + 16) <= REGION ? 2 : 1);
+    constexpr int PITCH = JH * 32 * OBY + 16;
+    constexpr int CH = JH * 32 * OBY / 16;  // 16-byte pieces per staged row
+    static_assert(32 * PITCH <= REGION && TN % JH == 0, "staging does not fit");
+    uint8_t* arr = wave < 2 ? As0 : wave < 4 ? As1 : wave < 6 ? Bs0 : Bs1;
+    lds_u8* st = (lds_u8*)(arr + (wave & 1) * REGION);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = min(m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3), p.M - 1);
-          res[r] = p.resid[static_cast<int64_t>(row) * p.ldr + col_c];
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int jb = 0; jb < TN / JH; ++jb) {
+#pragma unroll
+        for (int jj = 0; jj < JH; ++jj) {
+          const int j = jb * JH + jj;
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const int col = n0 + wn * WN + j * 32 + gi * 8 + lrow;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * gi + e] + ((p.bias && col + e < p.N) ? p.bias[col + e] : 0.0f);
+            lds_u8* at = st + lcol * PITCH + (jj * 32 + gi * 8 + lrow) * OBY;
+            if constexpr (OUT_BF16) {
+              u32x2 w;
+              w.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+              w.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+              *(__attribute__((address_space(3))) u32x2*)at = w;
+            } else {
+              *(__attribute__((address_space(3))) f32x4*)at = f32x4{v[0], v[1], v[2], v[3]};
+            }
+          }
+        }
+        const int row0 = m0 + wm * WM + i * 32;
+        const int col0 = n0 + wn * WN + jb * JH * 32;
+        constexpr int NIT = 32 * CH / 64;
+        f32x4 res[EPI == EPI_RESID ? NIT : 1];
+        if constexpr (EPI == EPI_RESID) {
+          // every residual piece of the slice in flight before any store
+          // (the output may be the residual itself, so stores cannot move ahead)
+#pragma unroll
+          for (int it = 0; it < NIT; ++it) {
+            const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
+            const int row = min(row0 + r, p.M - 1), col = min(col0 + ch * 4, p.N - 4);
+            res[it] = *reinterpret_cast<const f32x4*>(p.resid + static_cast<int64_t>(row) * p.ldr + col);
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
+          const int row = row0 + r, col = col0 + ch * (16 / OBY);
+          if (row < p.M && col < p.N) {
+            if constexpr (OUT_BF16) {
+              typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+              const u32x4 w = *(__attribute__((address_space(3))) u32x4*)(st + r * PITCH + ch * 16);
+              *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = w;
+            } else {
+              f32x4 w = *(__attribute__((address_space(3))) f32x4*)(st + r * PITCH + ch * 16);
+              if constexpr (EPI == EPI_RESID) w = res[it] + w;
+              *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = w;
+            }
+          }
         }
       }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
-        if (row < p.M && col < p.N) {
-          float x = acc[i][j][r] + bias;
-          if constexpr (EPI == EPI_RESID) x = res[r] + x;
-          const int64_t o = static_cast<int64_t>(row) * p.ldc + col;
-          if constexpr (OUT_BF16) static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(x);
-          else static_cast<float*>(p.C)[o] = x;
-        }
-      }
-    };
-    StaticFor<0, TM * TN>::run(tile);
+    }
   }
 }
 
@@ -801,6 +851,8 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
   if (!ok16(A, lda) || !ok16(B, ldb))
     return fail(MR_EINVAL, "mr_gemm: operands must be 16-byte aligned with ld a multiple of 8");
   if (c_dtype != MR_F32 && c_dtype != MR_BF16) return fail(MR_EINVAL, "mr_gemm: C must be fp32 or bf16");
+  if (!aligned16(C) || ldc % (c_dtype == MR_BF16 ? 8 : 4) || (resid && (!aligned16(resid) || ldr % 4)))
+    return fail(MR_EINVAL, "mr_gemm: C and resid must be 16-byte aligned with 16-byte rows");
   if (resid && c_dtype != MR_F32) return fail(MR_EINVAL, "mr_gemm: the residual form writes fp32");
   if (layout < 0 || layout > 2) return fail(MR_EINVAL, "mr_gemm: unknown layout %d", layout);
   {

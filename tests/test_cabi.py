@@ -82,6 +82,17 @@ def test_host_validation_refuses_before_launch(lib):
     arr = (ctypes.c_int * 9)(*range(9))
     rc = lib.mr_delta_loss(P(16), 1, P(16), 4, 64, 64, arr, 9, 0, 1e-8, P(16), P(16), None)
     assert rc == -22
+    # GEMM outputs are written in 16-byte row pieces: C, resid and the SwiGLU
+    # outputs must be 16-byte aligned with 16-byte rows
+    MR_F32, MR_BF16 = 0, 1
+    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(264), MR_F32, 64, None, None, 0, None)
+    assert rc == -22 and b"16-byte" in lib.mr_last_error()
+    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_BF16, 68, None, None, 0, None)
+    assert rc == -22 and b"16-byte" in lib.mr_last_error()
+    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_F32, 64, None, P(256), 66, None)
+    assert rc == -22 and b"16-byte" in lib.mr_last_error()
+    rc = lib.mr_gemm_swiglu(64, 64, 64, P(256), 64, P(256), 64, P(256), 68, None, 0, None)
+    assert rc == -22 and b"16-byte" in lib.mr_last_error()
 
 
 def test_workspace_sizes(lib):

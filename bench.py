@@ -357,6 +357,9 @@ def main(argv=None):
     ap.add_argument("--no-microbench", action="store_true")
     ap.add_argument("--no-like-for-like", action="store_true",
                     help="skip the extra symmetric searched-scale tune")
+    ap.add_argument("--kernel-sweep", action="store_true",
+                    help="only the fake-quant / update / pack microbench at bits 2, 3, 4, 8 x group "
+                         "sizes 32, 64, 128 (one JSON line each)")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch the fake-quant forward and a copy of known size (counter runs)")
     args = ap.parse_args(argv)
@@ -378,6 +381,12 @@ def main(argv=None):
 
     if args.profile_kernels:
         profile_kernels(torch, K, dev, args.steps)
+        return 0
+    if args.kernel_sweep:
+        for bits in (2, 3, 4, 8):
+            for gs in (32, 64, 128):
+                r = fake_quant_microbench(torch, K, dev, bits, gs, 20)
+                print(json.dumps({"bits": bits, "group_size": gs, **r}), flush=True)
         return 0
 
     tune = time_block_tune(torch, dev, args)

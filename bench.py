@@ -17,8 +17,10 @@ Printed as one JSON line:
   roofline   the dominant kernel of the tune (largest share of GPU time), its
              algorithmic flops per launch over its average launch duration,
              from HIP events recorded around every launch of it inside the
-             timed region, against 2.5 PFLOP/s dense bf16;
-  kernels    the same for every GEMM and attention launch of the block;
+             timed region (the only launches bracketed there), against
+             2.5 PFLOP/s dense bf16;
+  kernels    the same for every GEMM and attention launch of the block, from
+             events around every launch of the warm-up tunes;
   fake_quant the kernel microbench: a bf16 18944 x 3584 weight (0.1 % of
              entries x10), 2-bit gs64; forward, backward + update, the update
              that also writes the next W', and packing, against 8 TB/s;
@@ -100,31 +102,49 @@ def time_block_tune(torch, dev, args, *, workload=None, symmetric=False, steps=N
         return time.perf_counter() - t0, summary.blocks[0]
 
     tag = "sym searched" if symmetric else "asym"
+    eng = runner.engine(shape, entrance[0].shape[0], dev)
+    flops = eng.flops()
+
+    def table(per_launch):
+        out = {}
+        for name, ms in per_launch.items():
+            if ms:
+                avg = sum(ms) / len(ms)
+                out[name] = {"launches": len(ms), "avg_ms": round(avg, 4), "total_ms": round(sum(ms), 2),
+                             "tflops": round(flops[name] / (avg * 1e-3) / 1e12, 1)}
+        return out
+
+    # Events around every launch cost host time per launch, so they bracket
+    # every launch only in the warm-up tunes (the per-kernel table) and only
+    # the dominant kernel's launches in the timed tunes.
+    kernels, timed_kernels = {}, {}
+    if instrument and warmup:
+        eng.time_launches(flops)
     for i in range(warmup):
         print(f"bench: warm-up block tune ({tag}) {i + 1}/{warmup}", file=sys.stderr, flush=True)
         one()
-    eng = runner.engine(shape, entrance[0].shape[0], dev)
-    flops = eng.flops()
     if instrument:
-        eng.time_launches(flops)
+        if warmup:
+            kernels = table(eng.launch_ms())
+            dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
+            eng.time_launches([dominant])
+        else:
+            eng.time_launches(flops)
     times, results = [], []
     for i in range(steps):
         print(f"bench: timed block tune ({tag}) {i + 1}/{steps}", file=sys.stderr, flush=True)
         t, res = one()
         times.append(t)
         results.append(res)
-    per_launch = eng.launch_ms() if instrument else {}
+    if instrument:
+        timed_kernels = table(eng.launch_ms())
+        if not kernels:
+            kernels = timed_kernels
     eng.timers = None
-    kernels = {}
-    for name, ms in per_launch.items():
-        if not ms:
-            continue
-        avg = sum(ms) / len(ms)
-        kernels[name] = {"launches": len(ms), "avg_ms": round(avg, 4), "total_ms": round(sum(ms), 2),
-                         "tflops": round(flops[name] / (avg * 1e-3) / 1e12, 1)}
     gemm_ms = sum(k["total_ms"] for k in kernels.values())
     return {
-        "shape": shape, "times": times, "results": results, "kernels": kernels, "flops": flops,
+        "shape": shape, "times": times, "results": results, "kernels": kernels,
+        "timed_kernels": timed_kernels, "flops": flops,
         "kernel_ms_total": gemm_ms, "tokens_per_batch": entrance[0].shape[0],
         "batches": len(entrance), "workload": (shape, weights, entrance),
     }
@@ -393,7 +413,7 @@ def main(argv=None):
     sec = sum(tune["times"]) / len(tune["times"])
     kernels = tune["kernels"]
     dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
-    dk = kernels[dominant]
+    dk = tune["timed_kernels"].get(dominant, kernels[dominant])  # measured inside the timed region
     res = tune["results"][-1]
     traffic = _measured_traffic()
     like = None

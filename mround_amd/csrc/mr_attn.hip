@@ -342,8 +342,10 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dot(const uint16_t* __restr
 // or after its first key. Q and dO tiles arrive by direct loads, double
 // buffered like the forward's K and V; their transposed operands (for
 // dV = P^T dO and dK = dS^T Q) come from the transposing LDS read.
+// D = 64 fits two waves per SIMD (254 registers, no spills): 7 % faster on
+// the 0.5B shape (8 x 2048 tokens, 14 / 2 heads). D = 128 needs 486.
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 2 : 1))) void attn_bwd_dkdv(
     const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
     const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
     float scale, uint16_t* __restrict__ dqkv, int hsplit, float* __restrict__ part) {

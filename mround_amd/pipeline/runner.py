@@ -134,7 +134,7 @@ class QuantizationRunner:
                  progress: Callable[[BlockResult], None] | None = None,
                  eps: float = DEFAULT_EPS_FP32, quantized_inputs: bool = True,
                  holdout_batches: int = 0, per_layer_recipe: bool = False,
-                 graphs: bool | None = None) -> None:
+                 graphs: bool | None = None, fused_advance: bool = True) -> None:
         if holdout_batches < 0:
             msg = f"holdout_batches must be zero or more, got {holdout_batches}"
             raise CalibrationError(msg)
@@ -146,6 +146,9 @@ class QuantizationRunner:
         self.holdout_batches = holdout_batches
         self.per_layer_recipe = per_layer_recipe
         self.graphs = graphs  # None: decided per block (see _use_graphs)
+        # With a quantized stream and no held-out batches, the final score is
+        # taken from the advance pass (see run); False scores separately.
+        self.fused_advance = fused_advance
         self._engines: dict = {}
 
     def _scheme_for(self, path: str, overrides: Mapping[str, QuantScheme] | None) -> QuantScheme:
@@ -179,6 +182,15 @@ class QuantizationRunner:
             raise CalibrationError("no calibration batches")
         reference_stream = [x.float().contiguous() for x in entrance]
         quantized_stream = [x.clone() for x in reference_stream] if self.quantized_inputs else None
+        # The final score and the advance run the same forward (the tuned W'
+        # equals the committed reconstruction bit for bit) over the same
+        # stream, so with no held-out batches one pass does both: the advance
+        # writes into a spare stream and scores each batch against its target;
+        # a revert re-commits round to nearest and advances again from the
+        # untouched inputs. Identical losses, codes and streams, one pass over
+        # the calibration set fewer per block.
+        fused = quantized_stream is not None and self.fused_advance and self.holdout_batches == 0
+        spare = [torch.empty_like(x) for x in quantized_stream] if fused else None
         results, exported, schemes = [], {}, {}
         for block in blocks:
             t0 = time.perf_counter()
@@ -200,16 +212,34 @@ class QuantizationRunner:
             torch.cuda.synchronize(eng.device)
             targets_seconds = time.perf_counter() - t0
             inputs = quantized_stream if quantized_stream is not None else reference_stream
-            result, layers = self.quantize_block(block, inputs, targets, scheme_by_layer=scheme_by_layer,
-                                                 path_prefix=block.name)
-            exported.update(layers)
-            for path in layers:
-                schemes[path] = self._scheme_for(path, scheme_by_layer)
+            pending = None
+            if fused:
+                result, layers, pending = self._quantize_block(
+                    block, inputs, targets, scheme_by_layer=scheme_by_layer, path_prefix=block.name,
+                    defer_final=True)
+            else:
+                result, layers = self.quantize_block(block, inputs, targets, scheme_by_layer=scheme_by_layer,
+                                                     path_prefix=block.name)
             t1 = time.perf_counter()
-            if quantized_stream is not None:
+            if pending is not None:
+                final = self._advance(eng, block, quantized_stream, spare, targets, pending["suppress"])
+                reverted = final >= pending["initial"]
+                if reverted:
+                    for name, layer in pending["layers"].items():
+                        layer.restore(pending["start"][name])
+                        layers[f"{block.name}.{name}"] = self._commit(block, layer)
+                    self._advance(eng, block, quantized_stream, spare, None, pending["suppress"])
+                quantized_stream, spare = spare, quantized_stream
+                result = dataclasses.replace(
+                    result, final_loss=pending["initial"] if reverted else final, reverted=reverted,
+                    seconds=result.seconds + (time.perf_counter() - t1))
+            elif quantized_stream is not None:
                 eng.load_dense(block.weights.linears)
                 for x in quantized_stream:
                     eng.forward(x, x, save=False)
+            exported.update(layers)
+            for path in layers:
+                schemes[path] = self._scheme_for(path, scheme_by_layer)
             torch.cuda.synchronize(eng.device)
             stages = dict(result.stage_seconds)
             stages["targets"] = targets_seconds
@@ -229,6 +259,16 @@ class QuantizationRunner:
                        path_prefix: str = ""):
         """Tune and commit one block (mround/pipeline/runner.py:627-710). The
         block's linears are replaced by their reconstructions in the model dtype."""
+        result, exported, _ = self._quantize_block(block, inputs, targets, scheme_by_layer=scheme_by_layer,
+                                                   path_prefix=path_prefix)
+        return result, exported
+
+    def _quantize_block(self, block: DecoderBlock, inputs, targets, *, scheme_by_layer=None,
+                        path_prefix: str = "", defer_final: bool = False):
+        """``quantize_block``; with ``defer_final`` the final score and the
+        revert decision are left to the caller (returned as the third item:
+        the initial score, the loss form, the layers and their starting
+        parameters), and the result's final loss is provisional."""
         started = time.perf_counter()
         place = placements(block.shape)
         layers: dict[str, _Layer] = {}
@@ -253,7 +293,7 @@ class QuantizationRunner:
         t_search = time.perf_counter()
         searched = self._search_scales(eng, block, layers, inputs)
         search_seconds = time.perf_counter() - t_search if searched else 0.0
-        outcome = self._tune(eng, layers, inputs, targets)
+        outcome = self._tune(eng, layers, inputs, targets, defer_final=defer_final)
         t_commit = time.perf_counter()
         exported = {}
         for name, layer in layers.items():
@@ -268,7 +308,23 @@ class QuantizationRunner:
             seconds=time.perf_counter() - started, tuned=tuple(sorted(layers)),
             reverted=outcome["reverted"], generalization_gap=outcome["gap"],
             search_seconds=search_seconds, stage_seconds=stages, step_losses=tuple(outcome["losses"]))
-        return result, exported
+        pending = None
+        if defer_final and "start" in outcome:
+            pending = {"initial": outcome["initial"], "suppress": outcome["suppress"], "layers": layers,
+                       "start": outcome["start"]}
+        return result, exported, pending
+
+    def _advance(self, eng: BlockEngine, block: DecoderBlock, inputs, outputs, targets, suppress):
+        """The committed block over every batch of ``inputs`` into ``outputs``;
+        with ``targets``, the mean score of the outputs against them (the
+        arithmetic of ``_scores``)."""
+        eng.load_dense(block.weights.linears)
+        acc = torch.zeros(len(inputs), dtype=torch.float32, device=eng.device) if targets else None
+        for b, (x, out) in enumerate(zip(inputs, outputs)):
+            eng.forward(x, out, save=False)
+            if targets:
+                acc[b:b + 1].copy_(eng.loss(out, targets[b], suppress=suppress, with_grad=False))
+        return float(acc.double().sum().item()) / len(inputs) if targets else None
 
     def _commit(self, block: DecoderBlock, layer: _Layer) -> QuantizedLayer:
         """Codes (one byte each), scale and zero point for export, and the
@@ -380,7 +436,8 @@ class QuantizationRunner:
             acc[i:i + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress, with_grad=False))
         return float(acc.double().sum().item()) / len(over)
 
-    def _tune(self, eng: BlockEngine, layers: Mapping[str, _Layer], inputs, targets) -> dict:
+    def _tune(self, eng: BlockEngine, layers: Mapping[str, _Layer], inputs, targets, *,
+              defer_final: bool = False) -> dict:
         """mround/pipeline/runner.py:790-953: the last parameters are kept unless
         the score did not improve."""
         suppress, rates = block_recipe(self.tuning, self.scheme.bits,
@@ -437,6 +494,10 @@ class QuantizationRunner:
             step_losses[step:step + 1].copy_(eng.loss_val)
         torch.cuda.synchronize(eng.device)
         stages["tune"] = time.perf_counter() - t0
+        if defer_final and not held:
+            return {"initial": initial, "final": initial, "gap": None, "reverted": False,
+                    "losses": step_losses.double().cpu().tolist(), "stages": stages,
+                    "suppress": suppress, "start": start}
 
         t0 = time.perf_counter()
         final = self._scores(eng, layers, inputs, targets, scoring_batches, suppress, scratch)

@@ -12,7 +12,9 @@ stage by stage:
   scoring pass (``mround_amd.pipeline.causal_lm``): a fused bf16 copy of every
   block's W', every block's saved activations, the residual stream at each
   block boundary, the logits and the block engine at the scoring batch;
-* ``blocks``: the calibration token ids, the two fp32 calibration streams,
+* ``blocks``: the calibration token ids, the fp32 calibration streams (the
+  reference and quantized streams and the spare the advance writes into; one
+  stream more than a run with held-out batches holds),
   the block engine at the tuning batch, one block's learnables and their
   snapshot, and the committed codes of every block (their peak, at the last
   block);
@@ -185,7 +187,7 @@ def predict_memory(m: ModelShape, run: RunShape) -> MemoryPrediction:
         tokens = run.scoring_samples * run.scoring_seq_len * 8
         stages["scoring"] = base + lm + grids + tokens + run.n_samples * run.seq_len * 8
     T = run.batch_size * run.seq_len
-    streams = (2 if run.quantized_inputs else 1) * run.n_samples * run.seq_len * h * 4
+    streams = (3 if run.quantized_inputs else 1) * run.n_samples * run.seq_len * h * 4
     groups = _groups(m, run.group_size)
     learn = m.block_weights * 4 * 2 + groups * 4 * 4 + (groups * 4 if run.searched else 0)
     committed = L * (m.block_weights + groups * 8)
@@ -221,7 +223,7 @@ class MemoryCheck:
         if self.fits:
             return self.describe()
         return (self.describe() + ". The calibration streams take 4 bytes per token and hidden unit "
-                "(twice with quantized inputs), so fewer calibration samples, shorter sequences or "
+                "(three times with quantized inputs), so fewer calibration samples, shorter sequences or "
                 "quantized_inputs=False reduce the blocks stage; a smaller scoring_batch_size or "
                 "scoring_seq_len reduces the scoring stage")
 

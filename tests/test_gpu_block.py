@@ -229,3 +229,36 @@ def test_recorded_steps_equal_eager_steps(bits):
     assert r0.initial_loss == r1.initial_loss and r0.final_loss == r1.final_loss
     for k in c0:
         assert torch.equal(c0[k], c1[k]), k
+
+
+@pytest.mark.parametrize("lr", [0.005, 0.0])
+def test_fused_advance_equals_separate_score(lr):
+    """The final score taken from the advance pass (into a spare stream) gives
+    the same losses, revert decisions, codes and next-block inputs as scoring
+    separately and advancing in place; lr 0 leaves the score unchanged, so
+    both blocks revert and are re-committed at round to nearest."""
+    print("case fused advance", lr, flush=True, file=sys.stderr)
+    iters = 6
+    out = []
+    for fused in (False, True):
+        shape, B, S, w, inputs, _ = _tiny_tune(2, iters)
+        w1 = _problem("tiny_qwen", seed=11)[3]
+        scheme = QuantScheme(bits=2, group_size=64, symmetry=Symmetry.ASYMMETRIC)
+        tuning = TuningConfig(iters=iters, batch_size=B, n_samples=2 * B, seq_len=S, lr=lr)
+        runner = QuantizationRunner(scheme, tuning, fused_advance=fused)
+        blocks = [DecoderBlock(0, "model.layers.0", shape, _to_dev(w)),
+                  DecoderBlock(1, "model.layers.1", shape, _to_dev(w1))]
+        summary, layers = runner.run(blocks, [t.to(dev()) for t in inputs])
+        torch.cuda.synchronize()
+        out.append((summary.blocks, {k: (v.codes.cpu(), v.scale.cpu()) for k, v in layers.items()},
+                    {n: blocks[1].weights.linears[n].cpu() for n in LAYERS}))
+    (r0, c0, w0), (r1, c1, w1_) = out
+    for a, b in zip(r0, r1):
+        assert a.initial_loss == b.initial_loss and a.final_loss == b.final_loss, (a.index, a, b)
+        assert a.reverted == b.reverted and a.step_losses == b.step_losses
+        assert a.reverted == (lr == 0.0)
+    assert c0.keys() == c1.keys()
+    for k in c0:
+        assert torch.equal(c0[k][0], c1[k][0]) and torch.equal(c0[k][1], c1[k][1]), k
+    for n in LAYERS:
+        assert torch.equal(w0[n], w1_[n]), n

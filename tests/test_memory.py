@@ -77,6 +77,18 @@ def test_scoring_formula_is_the_causal_lm(tmp_path):
     assert abs((owned - shared) - formula) <= 0.005 * formula, (owned - shared, formula)
 
 
+def test_blocks_stage_counts_the_calibration_streams():
+    """With quantized inputs the runner holds the reference stream, the
+    quantized stream and the spare its advance writes into; without, one."""
+    m = M.ModelShape.from_config({**GEOMETRIES["qwen2.5-7b"], "vocab_size": 152064})
+    run = M.RunShape(n_samples=128, seq_len=2048, batch_size=8, group_size=64)
+    one = 128 * 2048 * m.hidden * 4
+    with_q = M.predict_memory(m, run).stages["blocks"]
+    without = M.predict_memory(m, M.RunShape(n_samples=128, seq_len=2048, batch_size=8, group_size=64,
+                                             quantized_inputs=False)).stages["blocks"]
+    assert with_q - without == 2 * one
+
+
 def test_api_refuses_a_run_past_the_budget(tmp_path):
     write_random_checkpoint(tmp_path / "m", TINY)
     check = api.predict_memory(tmp_path / "m", memory_budget=10 ** 12, device="cpu")

@@ -9,8 +9,9 @@ block-0 input stream, float32, resident in HBM (16 batches of 8 x 2048
 tokens). The scheme is 2-bit asymmetric, group size 64; 200 sign-SGD steps at
 lr 1/200 with the outlier rule on. One step of this bench is one block of a
 model run: the targets pass over the original weights, the score over all 16
-batches, 200 tuning steps on cycled batches, the second score, the commit
-(codes, scales, reconstruction) and the advance of the quantized stream.
+batches, 200 tuning steps on cycled batches, the commit (codes, scales,
+reconstruction) and the advance of the quantized stream, which also yields the
+second score.
 
 Printed as one JSON line:
   value      seconds per block tune (wall clock of one step, averaged over K);
@@ -460,7 +461,7 @@ def main(argv=None):
                          f"18944, qkv bias), random-init bf16 N(0,0.02); {args.samples} x "
                          f"{args.seq_len} uniform token ids (vocab {VOCAB}) through a random embedding; "
                          f"{BITS}-bit asym gs{GROUP}, {args.iters} sign-SGD steps at batch {args.batch}, "
-                         f"outlier rule on; targets + score + tune + score + commit + advance"),
+                         f"outlier rule on; targets + score + tune + commit + advance (with the second score)"),
             "global_batch": args.batch,
             "seq_len": args.seq_len,
             "iters": args.iters,

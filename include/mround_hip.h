@@ -9,13 +9,11 @@
  *
  * Conventions shared by every entry point:
  *   - All array arguments are device pointers owned by the caller.
- *     Reductions take a caller-provided workspace whose size the matching
- *     *_workspace_bytes() query returns. Two entry points keep an internal
- *     workspace of their own, allocated on their first call on a device and
- *     held until the process ends: the GEMMs (mr_gemm, mr_gemm_swiglu,
- *     mr_gemm_swiglu_bwd share the k-split partials) and mr_attn_bwd (dK/dV
- *     partials), 128 MB each per device. No other call allocates device
- *     memory.
+ *     Reductions, the GEMMs' k-split partials and the attention backward's
+ *     dK/dV partials live in a caller-provided workspace whose size the
+ *     matching *_workspace_bytes() query returns. The library allocates no
+ *     device memory and keeps no state between calls, so calls on different
+ *     streams with their own workspaces do not interfere.
  *   - Every call enqueues work on `stream` (a hipStream_t, NULL = default
  *     stream) and returns without synchronising.
  *   - The return value is MR_OK, MR_EINVAL (bad shape or argument, checked on
@@ -248,16 +246,20 @@ int mr_embed_rows(const void* table, int dtype, int64_t V, int64_t H, int64_t ld
  * with rows a multiple of 16 bytes apart. C is fp32 or
  * bf16; with resid (fp32) C is fp32. Long-K problems whose 256 x 256 tiles
  * leave a partial last wave sum that remainder from k-split partial tiles in
- * a 128 MB device workspace the library allocates on the first such call on
- * each GPU and keeps (the same for mr_gemm_swiglu and mr_gemm_swiglu_bwd);
- * calls that overlap on one GPU share it, so issue them on one stream. Replaces the matmul of the reference's
- * tunable linear, `x @ weight.T` (mround/pipeline/runner.py:364-368), and the
- * two products MLX autodiff forms for its backward.
+ * the caller's workspace: mr_gemm_workspace_bytes(M, N, K) bytes (0 when the
+ * shape is not split; N is the product's width, 2N for mr_gemm_swiglu), at
+ * most 128 MB, 16-byte aligned. A NULL or smaller workspace narrows or
+ * drops the split: the same product, summed in another order. Replaces the
+ * matmul of the reference's tunable linear, `x @ weight.T`
+ * (mround/pipeline/runner.py:364-368), and the two products MLX autodiff
+ * forms for its backward.
  */
 enum { MR_NT = 0, MR_NN = 1, MR_TN = 2 };
+size_t mr_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
             const void* B, int64_t ldb, void* C, int c_dtype, int64_t ldc, const float* bias,
-            const float* resid, int64_t ldr, void* stream);
+            const float* resid, int64_t ldr, void* workspace, size_t workspace_bytes,
+            void* stream);
 
 /*
  * SwiGLU projection pair in one product: act = silu(x Wg^T) * (x Wu^T), bf16
@@ -270,7 +272,8 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
  * block reached at mround/pipeline/blocks.py:605.
  */
 int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* Wgu,
-                   int64_t ldw, void* act, int64_t ldact, void* gu, int64_t ldgu, void* stream);
+                   int64_t ldw, void* act, int64_t ldact, void* gu, int64_t ldgu, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /*
  * Input gradient of the down projection fused with the SwiGLU backward:
@@ -282,7 +285,7 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
  */
 int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t ldd,
                        const void* Wd, int64_t ldw, const void* gu, int64_t ldgu, void* dgu,
-                       int64_t lddgu, void* stream);
+                       int64_t lddgu, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * RMSNorm over rows of the fp32 residual stream, y = h rsqrt(mean(h^2) + eps) w
@@ -312,18 +315,23 @@ int mr_rope(void* x_bf16, int64_t ld, int64_t T, int S, int n_heads, int head_di
  * writes out [B*S, Hq*head_dim] bf16 (leading dimension ldo) and the natural
  * log-sum-exp per (b, h, s) for the backward. The backward takes dout, writes
  * the gradient of the (post-rope) q/k/v into dqkv (same layout as qkv) and
- * uses dsum_ws (B*Hq*S floats) as workspace. When fewer than 512 blocks of
- * 128 keys would run (Hkv * B * S / 128), the backward splits each kv head's
- * query heads over several blocks and sums their fp32 dK/dV partials in a
- * fixed order; those live in a 128 MB per-device buffer that the first such
- * call allocates and the process keeps. The scaled-dot-product attention of
- * the mlx-lm block (mround/pipeline/blocks.py:605) and its autodiff.
+ * uses dsum_ws (B*Hq*S floats) as workspace. The backward may split each kv
+ * head's G = Hq / Hkv query heads over hsplit blocks, summing their fp32
+ * dK/dV partials in a fixed order from `workspace`
+ * (mr_attn_bwd_workspace_bytes(..., hsplit) bytes, 16-byte aligned).
+ * hsplit = 0 picks the split automatically (more blocks when fewer than 512
+ * blocks of 128 keys would run, Hkv * B * S / 128, within the workspace
+ * given; query the size with hsplit = 0); 1..G forces it and refuses a
+ * workspace too small for it. The scaled-dot-product attention of the
+ * mlx-lm block (mround/pipeline/blocks.py:605) and its autodiff.
  */
 int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int head_dim,
                 float scale, void* out, int64_t ldo, float* lse, void* stream);
+size_t mr_attn_bwd_workspace_bytes(int B, int S, int Hq, int Hkv, int head_dim, int hsplit);
 int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, int64_t ldo,
                 const float* lse, float* dsum_ws, int B, int S, int Hq, int Hkv, int head_dim,
-                float scale, void* dqkv, void* stream);
+                float scale, void* dqkv, int hsplit, void* workspace, size_t workspace_bytes,
+                void* stream);
 
 /*
  * v2 candidate-scale grid search for symmetric schemes: per group, the

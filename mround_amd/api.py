@@ -488,7 +488,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         "skipped": skipped,
         "storage": {"bits_per_weight": storage.bits_per_weight, "compression": storage.compression},
         "seconds": seconds,
-        "memory": {**memory.record(), "library_workspaces": M.LIBRARY_WORKSPACES,
+        "memory": {**memory.record(),
                    "peak_allocated": int(torch.cuda.max_memory_allocated(device)) - held_before
                    if on_gpu else None},
     }

@@ -17,7 +17,6 @@
 // orientations. All sums are in a fixed order: no atomics, deterministic.
 #include <cmath>
 
-#include <mutex>
 
 #include "mr_common.h"
 
@@ -674,43 +673,38 @@ int launch_fwd(const uint16_t* qkv, int64_t ld, int B, int S, int Hq, int Hkv, f
 // Grids of few key blocks (short sequences, few kv heads, small batches)
 // leave CUs idle and put the long causal first blocks on the critical path:
 // then each kv head's query heads are split over several blocks, up to
-// kKvTargetBlocks blocks, whose fp32 dK/dV partials live in a per-device
-// workspace allocated on first use and kept for the life of the process.
-// Measured: 1.3x on 8 x 2048 tokens with 2 kv heads, 3.4x on 2 x 1024; a
-// grid already at 512 blocks (4 kv heads) loses to the partials' traffic.
+// kKvTargetBlocks blocks, whose fp32 dK/dV partials live in the caller's
+// workspace. Measured: 1.3x on 8 x 2048 tokens with 2 kv heads, 3.4x on
+// 2 x 1024; a grid already at 512 blocks (4 kv heads) loses to the partials'
+// traffic.
 constexpr int64_t kKvTargetBlocks = 512;
-constexpr int64_t kKvPartBytes = 128ll << 20;
-float* kv_partials() {
-  static std::mutex mu;
-  static float* ws[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!ws[dev]) {
-    void* q = nullptr;
-    if (hipMalloc(&q, kKvPartBytes) != hipSuccess) return nullptr;
-    ws[dev] = static_cast<float*>(q);
-  }
-  return ws[dev];
+constexpr int64_t kKvPartCapBytes = 128ll << 20;
+
+int64_t kv_part_bytes(int B, int S, int Hkv, int D, int hsplit) {
+  return hsplit > 1 ? static_cast<int64_t>(hsplit) * B * S * 2 * Hkv * D * 4 : 0;
+}
+
+// The automatic split: the smallest that reaches kKvTargetBlocks blocks (or
+// all G query heads), with its partials within cap bytes.
+int auto_hsplit(int B, int S, int Hq, int Hkv, int D, int64_t cap) {
+  const int G = Hq / Hkv;
+  const int64_t blocks = static_cast<int64_t>(Hkv) * B * (S / QB);
+  int hsplit = 1;
+  while (hsplit < G && blocks * hsplit < kKvTargetBlocks && kv_part_bytes(B, S, Hkv, D, hsplit + 1) <= cap)
+    ++hsplit;
+  return hsplit;
 }
 
 template <int D>
 int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint16_t* dout,
                int64_t ldo, const float* lse, float* dsum, int B, int S, int Hq, int Hkv,
-               float scale, uint16_t* dqkv, hipStream_t s) {
+               float scale, uint16_t* dqkv, int hsplit, float* part, hipStream_t s) {
   const int64_t T = static_cast<int64_t>(B) * S;
   const int64_t lanes = T * Hq * (D / 8);
   hipLaunchKernelGGL(attn_bwd_dot<D>, dim3(static_cast<unsigned>((lanes + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, s, dout, out, ldo, T, S, Hq, dsum);
-  const int G = Hq / Hkv;
   const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
-  int hsplit = 1;
-  const int64_t blocks = static_cast<int64_t>(Hkv) * B * (S / QB);
-  while (hsplit < G && blocks * hsplit < kKvTargetBlocks &&
-         (hsplit + 1) * T * W * 4 <= kKvPartBytes)
-    ++hsplit;
-  float* part = hsplit > 1 ? kv_partials() : nullptr;
-  if (!part) hsplit = 1;
+  if (hsplit == 1) part = nullptr;
   hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv * hsplit, B, S / QB), dim3(kThreads), 0, s, qkv, ld,
                      dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
   if (part) {
@@ -757,9 +751,18 @@ int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int 
   return launch_fwd<64>(q, ld, B, S, Hq, Hkv, scale, o, ldo, lse, s);
 }
 
+size_t mr_attn_bwd_workspace_bytes(int B, int S, int Hq, int Hkv, int head_dim, int hsplit) {
+  using namespace mr;
+  if (B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || (head_dim != 64 && head_dim != 128))
+    return 0;
+  const int h = hsplit > 0 ? hsplit : auto_hsplit(B, S, Hq, Hkv, head_dim, kKvPartCapBytes);
+  return static_cast<size_t>(kv_part_bytes(B, S, Hkv, head_dim, h));
+}
+
 int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, int64_t ldo,
                 const float* lse, float* dsum_ws, int B, int S, int Hq, int Hkv, int head_dim,
-                float scale, void* dqkv, void* stream) {
+                float scale, void* dqkv, int hsplit, void* workspace, size_t workspace_bytes,
+                void* stream) {
   using namespace mr;
   clear_error();
   int rc = check("mr_attn_bwd", qkv, ld, B, S, Hq, Hkv, head_dim, ldo);
@@ -767,13 +770,28 @@ int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, 
   if (!out || !dout || !lse || !dsum_ws || !dqkv || !aligned16(out) || !aligned16(dout) ||
       !aligned16(dqkv))
     return fail(MR_EINVAL, "mr_attn_bwd: bad argument");
+  const int G = Hq / Hkv;
+  if (hsplit < 0 || hsplit > G)
+    return fail(MR_EINVAL, "mr_attn_bwd: hsplit %d outside [0, %d] (0 = automatic)", hsplit, G);
+  if (workspace && !aligned16(workspace))
+    return fail(MR_EINVAL, "mr_attn_bwd: workspace must be 16-byte aligned");
+  const int64_t have = workspace ? static_cast<int64_t>(workspace_bytes) : 0;
+  if (hsplit == 0) {
+    hsplit = auto_hsplit(B, S, Hq, Hkv, head_dim, have < kKvPartCapBytes ? have : kKvPartCapBytes);
+  } else if (kv_part_bytes(B, S, Hkv, head_dim, hsplit) > have) {
+    return fail(MR_EINVAL, "mr_attn_bwd: hsplit %d needs a %lld-byte workspace, %lld given", hsplit,
+                static_cast<long long>(kv_part_bytes(B, S, Hkv, head_dim, hsplit)),
+                static_cast<long long>(have));
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* q = static_cast<const uint16_t*>(qkv);
   const uint16_t* o = static_cast<const uint16_t*>(out);
   const uint16_t* dO = static_cast<const uint16_t*>(dout);
   uint16_t* dq = static_cast<uint16_t*>(dqkv);
-  if (head_dim == 128) return launch_bwd<128>(q, ld, o, dO, ldo, lse, dsum_ws, B, S, Hq, Hkv, scale, dq, s);
-  return launch_bwd<64>(q, ld, o, dO, ldo, lse, dsum_ws, B, S, Hq, Hkv, scale, dq, s);
+  float* part = static_cast<float*>(workspace);
+  if (head_dim == 128)
+    return launch_bwd<128>(q, ld, o, dO, ldo, lse, dsum_ws, B, S, Hq, Hkv, scale, dq, hsplit, part, s);
+  return launch_bwd<64>(q, ld, o, dO, ldo, lse, dsum_ws, B, S, Hq, Hkv, scale, dq, hsplit, part, s);
 }
 
 }  // extern "C"

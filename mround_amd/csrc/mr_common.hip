@@ -59,7 +59,7 @@ int mr_counter_add(int* counter, int delta, void* stream) {
   return MR_OK;
 }
 
-int mr_abi_version(void) { return 1; }
+int mr_abi_version(void) { return 2; }
 
 int mr_copy_bytes(const void* src, void* dst, size_t bytes, void* stream) {
   mr::clear_error();

@@ -29,7 +29,6 @@
 // Blocks are renumbered so that each XCD (blocks are dealt to the 8 XCDs
 // round-robin) receives a contiguous run of tiles, grouped along M so that a
 // run shares B panels in that XCD's L2.
-#include <mutex>
 #include <type_traits>
 
 #include "mr_common.h"
@@ -84,7 +83,8 @@ struct GemmParams {
   // sub = 1: this launch's tiles are the four quarters of each of the
   // (2 BM) x (2 BN) tiles tile0 .. of the grid_m x grid_n grid (see launch).
   int sub;
-  float* ws;
+  float* ws;         // k-split partials (caller's workspace), or null: no split
+  int64_t ws_bytes;
 };
 
 // Logical tile -> (tile row, tile column): groups of 8 tile rows, column by
@@ -690,22 +690,42 @@ __global__ __launch_bounds__(256) void gemm_reduce(GemmParams p) {
   }
 }
 
-// Partial-tile workspace for the k-split tails, one per device, allocated
-// on first use and kept for the life of the process.
-constexpr int64_t kSplitWsBytes = 128ll << 20;
+// The k-split tails' partial tiles live in a workspace the caller passes in
+// (mr_gemm_workspace_bytes gives the size the plan below wants; a smaller or
+// absent one narrows or drops the split). kSplitCapBytes bounds the plan.
+constexpr int64_t kSplitCapBytes = 128ll << 20;
 constexpr int kSplitMinKt = 96;
-float* split_workspace() {
-  static std::mutex mu;
-  static float* ws[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!ws[dev]) {
-    void* q = nullptr;
-    if (hipMalloc(&q, kSplitWsBytes) != hipSuccess) return nullptr;
-    ws[dev] = static_cast<float*>(q);
+
+// Blocks per tile for the remainder past the last whole wave of large tiles
+// (1 = no split), with its partials within ws_bytes.
+int split_plan(int64_t tiles, int KT, int64_t ws_bytes) {
+  constexpr int64_t wave = 256, tile_bytes = 256ll * 256 * 4;
+  const int64_t tail = tiles % wave;
+  int split = 1;
+  if (!tail || KT < kSplitMinKt) return 1;
+  const int64_t cap = ws_bytes < kSplitCapBytes ? ws_bytes : kSplitCapBytes;
+  double best = 1.0;
+  for (int sp = 2; sp <= 16 && sp <= KT; ++sp) {
+    if (tail * sp * tile_bytes > cap) break;
+    const double t = static_cast<double>((tail * sp + wave - 1) / wave) / sp;
+    if (t < best - 1e-9) {
+      best = t;
+      split = sp;
+    }
   }
-  return ws[dev];
+  return split;
+}
+
+// Bytes of partials the plan uses for an M x N x K product (0: no split).
+int64_t split_bytes(int64_t M, int64_t N, int64_t K) {
+  const int KT = static_cast<int>(K / BK);
+  if (KT < kSplitMinKt) return 0;  // short K: whole-K tiles of either size
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  const int split = split_plan(tiles, KT, kSplitCapBytes);
+  if (split == 1) return 0;
+  const int kt_per = (KT + split - 1) / split;
+  const int ksplit = (KT + kt_per - 1) / kt_per;
+  return (tiles % 256) * ksplit * 256ll * 256 * 4;
 }
 
 // Large tiles go out in whole waves of 256 (one per CU). When K is long (at
@@ -724,20 +744,7 @@ int launch(GemmParams p, hipStream_t s) {
   const int KT = p.K / BK;
   constexpr int64_t wave = 256;
   const int64_t tail = tiles % wave, full = tiles - tail;
-  int split = 1;
-  if (BM == 256 && tail && KT >= kSplitMinKt) {
-    double best = 1.0;
-    for (int sp = 2; sp <= 16 && sp <= KT; ++sp) {
-      if (tail * sp * BM * BN * 4 > kSplitWsBytes) break;
-      const double t = static_cast<double>((tail * sp + wave - 1) / wave) / sp;
-      if (t < best - 1e-9) {
-        best = t;
-        split = sp;
-      }
-    }
-  }
-  float* ws = split > 1 ? split_workspace() : nullptr;
-  if (split > 1 && !ws) split = 1;
+  const int split = BM == 256 && p.ws ? split_plan(tiles, KT, p.ws_bytes) : 1;
   if constexpr (BM == 256 && EPI == EPI_STORE) {
     // A last wave at most half full runs as quarter tiles (two per CU)
     // instead of leaving half the CUs or more idle: measured 5-6 % faster on
@@ -784,7 +791,6 @@ int launch(GemmParams p, hipStream_t s) {
   p.n_tiles = static_cast<int>(tail);
   p.kt_per = (KT + split - 1) / split;
   p.ksplit = (KT + p.kt_per - 1) / p.kt_per;  // no empty split
-  p.ws = ws;
   hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BKM, EPI, OB>),
                      dim3(static_cast<unsigned>(tail * p.ksplit)), dim3(kThreads), 0, s, p);
   constexpr int CW = EPI == EPI_SWIGLU ? BN / 2 : BN;
@@ -829,14 +835,32 @@ bool ok16(const void* p, int64_t ld) {
   return aligned16(p) && (ld % 8) == 0;
 }
 
+// The caller's k-split workspace: null or zero bytes disable the split.
+bool set_workspace(GemmParams& p, void* ws, size_t bytes) {
+  if (!ws || !bytes) {
+    p.ws = nullptr;
+    p.ws_bytes = 0;
+    return true;
+  }
+  if (!aligned16(ws)) return false;
+  p.ws = static_cast<float*>(ws);
+  p.ws_bytes = static_cast<int64_t>(bytes);
+  return true;
+}
+
 }  // namespace
 }  // namespace mr
 
 extern "C" {
 
+size_t mr_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return static_cast<size_t>(mr::split_bytes(M, N, K));
+}
+
 int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
             const void* B, int64_t ldb, void* C, int c_dtype, int64_t ldc, const float* bias,
-            const float* resid, int64_t ldr, void* stream) {
+            const float* resid, int64_t ldr, void* workspace, size_t workspace_bytes, void* stream) {
   using namespace mr;
   clear_error();
   if (M < 0 || N < 0 || K < 0) return fail(MR_EINVAL, "mr_gemm: negative size");
@@ -873,6 +897,8 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
   p.bias = bias;
   p.resid = resid;
   p.ldr = ldr;
+  if (!set_workspace(p, workspace, workspace_bytes))
+    return fail(MR_EINVAL, "mr_gemm: workspace must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool ob = c_dtype == MR_BF16;
 #define MR_GEMM_CASE(AK, BKM)                                                             \
@@ -889,7 +915,8 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
 }
 
 int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, const void* Wgu,
-                   int64_t ldw, void* act, int64_t ldact, void* gu, int64_t ldgu, void* stream) {
+                   int64_t ldw, void* act, int64_t ldact, void* gu, int64_t ldgu, void* workspace,
+                   size_t workspace_bytes, void* stream) {
   using namespace mr;
   clear_error();
   if (M <= 0 || N <= 0) return MR_OK;
@@ -914,12 +941,14 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
   p.ldc = ldact;
   p.gu = static_cast<uint16_t*>(gu);
   p.ldgu = ldgu;
+  if (!set_workspace(p, workspace, workspace_bytes))
+    return fail(MR_EINVAL, "mr_gemm_swiglu: workspace must be 16-byte aligned");
   return dispatch<true, true, EPI_SWIGLU, true>(p, static_cast<hipStream_t>(stream));
 }
 
 int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t ldd,
                        const void* Wd, int64_t ldw, const void* gu, int64_t ldgu, void* dgu,
-                       int64_t lddgu, void* stream) {
+                       int64_t lddgu, void* workspace, size_t workspace_bytes, void* stream) {
   using namespace mr;
   clear_error();
   if (M <= 0 || N <= 0) return MR_OK;
@@ -943,6 +972,8 @@ int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t 
   p.ldc = lddgu;
   p.gu = const_cast<uint16_t*>(static_cast<const uint16_t*>(gu));
   p.ldgu = ldgu;
+  if (!set_workspace(p, workspace, workspace_bytes))
+    return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: workspace must be 16-byte aligned");
   return dispatch<true, false, EPI_SWIGLU_BWD, true>(p, static_cast<hipStream_t>(stream));
 }
 

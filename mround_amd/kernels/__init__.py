@@ -74,14 +74,17 @@ _SIGNATURES = {
     "mr_delta_loss_workspace_bytes": (ctypes.c_size_t, [_L, _L, _I]),
     "mr_delta_loss": (_I, [_P, _I, _P, _L, _L, _I, _P, _I, _I, _F, _P, _P, _P]),
     "mr_copy_bytes": (_I, [_P, _P, ctypes.c_size_t, _P]),
-    "mr_gemm": (_I, [_I, _L, _L, _L, _P, _L, _P, _L, _P, _I, _L, _P, _P, _L, _P]),
-    "mr_gemm_swiglu": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P]),
-    "mr_gemm_swiglu_bwd": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P]),
+    "mr_gemm_workspace_bytes": (ctypes.c_size_t, [_L, _L, _L]),
+    "mr_gemm": (_I, [_I, _L, _L, _L, _P, _L, _P, _L, _P, _I, _L, _P, _P, _L, _P, ctypes.c_size_t, _P]),
+    "mr_gemm_swiglu": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P, ctypes.c_size_t, _P]),
+    "mr_gemm_swiglu_bwd": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P, ctypes.c_size_t, _P]),
     "mr_rmsnorm_fwd": (_I, [_P, _P, _L, _L, _F, _P, _P, _P]),
     "mr_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _L, _L, _P, _P, _P]),
     "mr_rope": (_I, [_P, _L, _L, _I, _I, _I, _P, _I, _P]),
     "mr_attn_fwd": (_I, [_P, _L, _I, _I, _I, _I, _I, _F, _P, _L, _P, _P]),
-    "mr_attn_bwd": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _F, _P, _P]),
+    "mr_attn_bwd_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I, _I, _I, _I]),
+    "mr_attn_bwd": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _F, _P, _I, _P, ctypes.c_size_t,
+                         _P]),
     "mr_cast_f32_bf16": (_I, [_P, _P, _L, _P]),
     "mr_allocate_bits": (_I, [_I, _P, _P, _P, _L, _L, _P, _P, _P]),
     "mr_search_scales": (_I, [_P, _I, _P, _L, _L, _I, _I, ctypes.c_double, _I, _P, _P]),
@@ -346,31 +349,62 @@ def embed_rows(table, ids, out) -> None:
 GEMM_LAYOUT = {"nt": 0, "nn": 1, "tn": 2}
 
 
-def gemm(layout: str, a, b, c, *, M, N, K, bias=None, resid=None) -> None:
-    """``mr_gemm``: C = op(A) op(B) (+ bias) (+ resid); leading dims from strides."""
+def gemm_workspace_bytes(M: int, N: int, K: int) -> int:
+    """``mr_gemm_workspace_bytes``: k-split partials for an M x N x K product
+    (N is the product's width: 2N for the SwiGLU pair)."""
+    return int(lib().mr_gemm_workspace_bytes(M, N, K))
+
+
+def _gemm_ws(device: torch.device, M: int, N: int, K: int, workspace):
+    """The caller's workspace, or the binding's own per-device one grown to the
+    plan's size (the library allocates nothing)."""
+    if workspace is not None:
+        return workspace
+    nbytes = gemm_workspace_bytes(M, N, K)
+    if nbytes == 0:
+        return None
+    key = (device.index or 0, "gemm")
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def _ws_args(ws):
+    return (None, 0) if ws is None else (_ptr(ws), ws.numel() * ws.element_size())
+
+
+def gemm(layout: str, a, b, c, *, M, N, K, bias=None, resid=None, workspace=None) -> None:
+    """``mr_gemm``: C = op(A) op(B) (+ bias) (+ resid); leading dims from strides.
+    ``workspace``: the k-split partials (a device tensor of at least
+    ``gemm_workspace_bytes(M, N, K)`` bytes); None uses the binding's own."""
+    ws_ptr, ws_bytes = _ws_args(_gemm_ws(a.device, M, N, K, workspace))
     rc = lib().mr_gemm(GEMM_LAYOUT[layout], M, N, K, _ptr(a), a.stride(0), _ptr(b), b.stride(0),
                        _ptr(c), dtype_code(c.dtype), c.stride(0), _ptr(_f32(bias, "bias")),
                        _ptr(_f32(resid, "resid")), resid.stride(0) if resid is not None else 0,
-                       _stream(a))
+                       ws_ptr, ws_bytes, _stream(a))
     _check(rc, "mr_gemm")
 
 
-def gemm_swiglu(x, wgu, act, gu=None) -> None:
+def gemm_swiglu(x, wgu, act, gu=None, *, workspace=None) -> None:
     """``mr_gemm_swiglu`` over the 32-row interleaved gate/up weight ``wgu`` [2N, K]."""
     M, K = x.shape
     N = wgu.shape[0] // 2
+    ws_ptr, ws_bytes = _ws_args(_gemm_ws(x.device, M, 2 * N, K, workspace))
     rc = lib().mr_gemm_swiglu(M, N, K, _ptr(x), x.stride(0), _ptr(wgu), wgu.stride(0), _ptr(act),
                               act.stride(0), _ptr(gu), gu.stride(0) if gu is not None else 0,
-                              _stream(x))
+                              ws_ptr, ws_bytes, _stream(x))
     _check(rc, "mr_gemm_swiglu")
 
 
-def gemm_swiglu_bwd(dd, wd, gu, dgu) -> None:
+def gemm_swiglu_bwd(dd, wd, gu, dgu, *, workspace=None) -> None:
     """``mr_gemm_swiglu_bwd``: dgu from dact = dd Wd and the saved interleaved gate/up."""
     M, K = dd.shape
     N = wd.shape[1]
+    ws_ptr, ws_bytes = _ws_args(_gemm_ws(dd.device, M, N, K, workspace))
     rc = lib().mr_gemm_swiglu_bwd(M, N, K, _ptr(dd), dd.stride(0), _ptr(wd), wd.stride(0), _ptr(gu),
-                                  gu.stride(0), _ptr(dgu), dgu.stride(0), _stream(dd))
+                                  gu.stride(0), _ptr(dgu), dgu.stride(0), ws_ptr, ws_bytes, _stream(dd))
     _check(rc, "mr_gemm_swiglu_bwd")
 
 
@@ -402,13 +436,31 @@ def attn_fwd(qkv, *, batch, seq_len, n_heads, n_kv_heads, head_dim, scale, out, 
     _check(rc, "mr_attn_fwd")
 
 
+def attn_bwd_workspace_bytes(*, batch, seq_len, n_heads, n_kv_heads, head_dim, hsplit=0) -> int:
+    """``mr_attn_bwd_workspace_bytes``: dK/dV partials of the (automatic, 0) head split."""
+    return int(lib().mr_attn_bwd_workspace_bytes(batch, seq_len, n_heads, n_kv_heads, head_dim, hsplit))
+
+
 def attn_bwd(qkv, out, dout, lse, dsum, *, batch, seq_len, n_heads, n_kv_heads, head_dim, scale,
-             dqkv) -> None:
+             dqkv, hsplit=0, workspace=None) -> None:
+    """``mr_attn_bwd``. ``hsplit`` 0 splits the query heads of a kv head over
+    blocks automatically, 1..G forces it; ``workspace`` holds the dK/dV
+    partials (None: the binding's own, sized for the split)."""
     if dout.stride(0) != out.stride(0) or dqkv.stride(0) != qkv.stride(0):
         raise KernelError("attention backward: dout/out and dqkv/qkv must share layouts")
+    if workspace is None:
+        nbytes = attn_bwd_workspace_bytes(batch=batch, seq_len=seq_len, n_heads=n_heads,
+                                          n_kv_heads=n_kv_heads, head_dim=head_dim, hsplit=hsplit)
+        if nbytes:
+            key = (qkv.device.index or 0, "attn")
+            workspace = _workspaces.get(key)
+            if workspace is None or workspace.numel() < nbytes:
+                workspace = torch.empty(nbytes, dtype=torch.uint8, device=qkv.device)
+                _workspaces[key] = workspace
+    ws_ptr, ws_bytes = _ws_args(workspace)
     rc = lib().mr_attn_bwd(_ptr(qkv), qkv.stride(0), _ptr(out), _ptr(dout), out.stride(0),
                            _ptr(_f32(lse, "lse")), _ptr(_f32(dsum, "dsum")), batch, seq_len, n_heads,
-                           n_kv_heads, head_dim, scale, _ptr(dqkv), _stream(qkv))
+                           n_kv_heads, head_dim, scale, _ptr(dqkv), hsplit, ws_ptr, ws_bytes, _stream(qkv))
     _check(rc, "mr_attn_bwd")
 
 

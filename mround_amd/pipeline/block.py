@@ -160,6 +160,28 @@ class BlockWeights:
         return cls(lin, biases, ones, ones.clone())
 
 
+def gemm_problems(shape: BlockShape, tokens: int) -> list[tuple[int, int, int]]:
+    """(M, N, K) of every product of a block's forward and backward at
+    ``tokens`` tokens (N is the product's width: 2 x intermediate for the
+    SwiGLU pair), the shapes whose k-split partials share one workspace."""
+    T, h, mlp, q = tokens, shape.hidden, shape.intermediate, shape.qkv_rows
+    hq_d = shape.n_heads * shape.head_dim
+    return [(T, q, h), (T, h, hq_d), (T, 2 * mlp, h), (T, h, mlp), (T, mlp, h), (h, mlp, T),
+            (T, h, 2 * mlp), (2 * mlp, h, T), (T, hq_d, h), (h, hq_d, T), (q, h, T), (T, h, q)]
+
+
+def workspace_bytes(shape: BlockShape, batch: int, seq_len: int,
+                    extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> tuple[int, int]:
+    """Bytes of the GEMM k-split workspace (the largest any of the block's
+    products, or ``extra_gemms``, plans) and of the attention backward's dK/dV
+    partials (its automatic head split) for a block engine."""
+    probs = gemm_problems(shape, batch * seq_len) + list(extra_gemms)
+    gemm = max(K.gemm_workspace_bytes(M, N, Kd) for M, N, Kd in probs)
+    attn = K.attn_bwd_workspace_bytes(batch=batch, seq_len=seq_len, n_heads=shape.n_heads,
+                                      n_kv_heads=shape.n_kv_heads, head_dim=shape.head_dim)
+    return gemm, attn
+
+
 def rope_table(seq_len: int, head_dim: int, theta: float, device) -> torch.Tensor:
     """cos/sin of ``pos * theta^(-2i/d)``, float32 ``[S, d/2, 2]`` (computed in float64)."""
     inv = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim)
@@ -171,7 +193,8 @@ class BlockEngine:
     """Forward, loss and backward of one block over ``batch`` sequences of
     ``seq_len`` tokens, with every buffer allocated once."""
 
-    def __init__(self, shape: BlockShape, *, batch: int, seq_len: int, device) -> None:
+    def __init__(self, shape: BlockShape, *, batch: int, seq_len: int, device,
+                 extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> None:
         shape.validate(seq_len)
         self.shape, self.batch, self.seq_len = shape, batch, seq_len
         self.device = torch.device(device)
@@ -205,6 +228,12 @@ class BlockEngine:
         self.scale = 1.0 / math.sqrt(shape.head_dim)
         self.place = placements(shape)
         self.loss_ws = K.loss_workspace(self.device, T * h)
+        # the library's scratch for the GEMM k-split partials and the attention
+        # backward's dK/dV partials, owned here (extra_gemms: products a caller
+        # runs with this workspace besides the block's own)
+        gemm_b, attn_b = workspace_bytes(shape, batch, seq_len, extra_gemms)
+        self.gemm_ws = e(gemm_b, dt=torch.uint8) if gemm_b else None
+        self.attn_ws = e(attn_b, dt=torch.uint8) if attn_b else None
         self.x_in: torch.Tensor | None = None  # block input of the last saving forward
         self.dh32: torch.Tensor | None = None  # fp32 residual gradient, for input gradients
         # name -> [(start, end) HIP events] for the launches being timed, or None
@@ -290,25 +319,26 @@ class BlockEngine:
         if x.shape != (T, s.hidden) or out.shape != (T, s.hidden):
             raise ArchitectureError(f"block input must be [{T}, {s.hidden}]")
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
+        ws = self.gemm_ws
         if save:
             if out.data_ptr() == x.data_ptr():
                 raise ArchitectureError("a saving forward needs its input kept: out must not be x")
             self.x_in = x
         K.rmsnorm_fwd(x, self.norm_in, s.norm_eps, self.x1, self.rstd1)
         self._run("gemm_qkv", lambda: K.gemm("nt", self.x1, self.wq["qkv"], self.qkv, M=T, N=s.qkv_rows,
-                                             K=h, bias=self.bias_qkv))
+                                             K=h, bias=self.bias_qkv, workspace=ws))
         K.rope(self.qkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads, head_dim=s.head_dim,
                cos_sin=self.cos_sin)
         self._run("attn_fwd", lambda: K.attn_fwd(
             self.qkv, batch=self.batch, seq_len=self.seq_len, n_heads=s.n_heads,
             n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, scale=self.scale, out=self.attn, lse=self.lse))
         self._run("gemm_o", lambda: K.gemm("nt", self.attn, self.wq["o"], self.h2, M=T, N=h, K=hq_d,
-                                           resid=x))
+                                           resid=x, workspace=ws))
         K.rmsnorm_fwd(self.h2, self.norm_post, s.norm_eps, self.x2, self.rstd2)
         self._run("gemm_gate_up", lambda: K.gemm_swiglu(self.x2, self.wq["gu"], self.act,
-                                                        self.gu if save else None))
+                                                        self.gu if save else None, workspace=ws))
         self._run("gemm_down", lambda: K.gemm("nt", self.act, self.wq["down"], out, M=T, N=h, K=mlp,
-                                              resid=self.h2))
+                                              resid=self.h2, workspace=ws))
 
     def loss(self, out: torch.Tensor, target: torch.Tensor, *, suppress: bool, with_grad: bool) -> torch.Tensor:
         """Reconstruction loss of one batch (device scalar), and dL/dout when asked:
@@ -341,35 +371,36 @@ class BlockEngine:
             if self.dh32 is None:
                 self.dh32 = torch.empty(T, s.hidden, dtype=torch.float32, device=self.device)
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
+        ws = self.gemm_ws
         K.cast_bf16(self.grad_out, self.grad_out16)
         # MLP: dgu from dact = dout Wd'; dWd' = dout^T act; dx2 = dgu Wgu'; dWgu' = dgu^T x2
         self._run("gemm_dact", lambda: K.gemm_swiglu_bwd(self.grad_out16, self.wq["down"], self.gu,
-                                                         self.dgu))
+                                                         self.dgu, workspace=ws))
         self._run("gemm_dw_down", lambda: K.gemm("tn", self.grad_out16, self.act, self.dw["down"], M=h,
-                                                 N=mlp, K=T))
+                                                 N=mlp, K=T, workspace=ws))
         self._run("gemm_dx_gate_up", lambda: K.gemm("nn", self.dgu, self.wq["gu"], self.dx2, M=T, N=h,
-                                                    K=2 * mlp))
+                                                    K=2 * mlp, workspace=ws))
         self._run("gemm_dw_gate_up", lambda: K.gemm("tn", self.dgu, self.x2, self.dw["gu"], M=2 * mlp,
-                                                    N=h, K=T))
+                                                    N=h, K=T, workspace=ws))
         # dh = dout + rmsnorm'(dx2)
         K.rmsnorm_bwd(self.dx2, self.h2, self.norm_post, self.rstd2, self.grad_out, dh_bf16=self.dh2,
                       dh_f32=self.dh32 if dx_out is not None else None)
         # attention output projection
         self._run("gemm_dattn", lambda: K.gemm("nn", self.dh2, self.wq["o"], self.dattn, M=T, N=hq_d,
-                                               K=h))
+                                               K=h, workspace=ws))
         self._run("gemm_dw_o", lambda: K.gemm("tn", self.dh2, self.attn, self.dw["o"], M=h, N=hq_d,
-                                              K=T))
+                                              K=T, workspace=ws))
         self._run("attn_bwd", lambda: K.attn_bwd(
             self.qkv, self.attn, self.dattn, self.lse, self.dsum, batch=self.batch,
             seq_len=self.seq_len, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim,
-            scale=self.scale, dqkv=self.dqkv))
+            scale=self.scale, dqkv=self.dqkv, workspace=self.attn_ws))
         K.rope(self.dqkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads,
                head_dim=s.head_dim, cos_sin=self.cos_sin, backward=True)
         self._run("gemm_dw_qkv", lambda: K.gemm("tn", self.dqkv, self.x1, self.dw["qkv"], M=s.qkv_rows,
-                                                N=h, K=T))
+                                                N=h, K=T, workspace=ws))
         if dx_out is None:
             return
         # dx = dh + rmsnorm'(dqkv Wqkv'); dx2 is free again and holds dx1.
         self._run("gemm_dx_qkv", lambda: K.gemm("nn", self.dqkv, self.wq["qkv"], self.dx2, M=T, N=h,
-                                                K=s.qkv_rows))
+                                                K=s.qkv_rows, workspace=ws))
         K.rmsnorm_bwd(self.dx2, self.x_in, self.norm_in, self.rstd1, self.dh32, dh_f32=dx_out)

@@ -80,7 +80,12 @@ class CausalLM:
         self.batch, self.seq_len = batch, seq_len
         self.n_in = seq_len - 1
         S = padded_length(seq_len)
-        self.eng = BlockEngine(self.shape, batch=batch, seq_len=S, device=self.device)
+        head = model.embed if model.lm_head is None else model.lm_head
+        Vp = -(-int(head.shape[0]) // 64) * 64
+        T0, h0 = batch * S, self.shape.hidden
+        # the head's two products share the block engine's k-split workspace
+        self.eng = BlockEngine(self.shape, batch=batch, seq_len=S, device=self.device,
+                               extra_gemms=((T0, Vp, h0), (T0, h0, Vp)))
         eng, T, h = self.eng, self.eng.tokens, self.shape.hidden
         self.tokens = T
         f32, bf = torch.float32, torch.bfloat16
@@ -101,9 +106,7 @@ class CausalLM:
         self.grads = [torch.empty(T, h, dtype=f32, device=self.device) for _ in range(2)]
         self.scratch = None if keep_activations else torch.empty(T, h, dtype=f32, device=self.device)
         # head
-        head = model.embed if model.lm_head is None else model.lm_head
         self.vocab = V = int(head.shape[0])
-        Vp = -(-V // 64) * 64
         if head.shape[1] != h:
             raise ArchitectureError(f"head is {tuple(head.shape)}, hidden size {h}")
         if Vp == V and head.dtype == bf and head.is_contiguous():
@@ -180,10 +183,12 @@ class CausalLM:
         # head and loss
         V = self.vocab
         K.rmsnorm_fwd(self.stream[L], self.final_norm, s.norm_eps, self.xn, self.rstd)
-        K.gemm("nt", self.xn, self.head, self.logits, M=T, N=self.logits.shape[1], K=h)
+        K.gemm("nt", self.xn, self.head, self.logits, M=T, N=self.logits.shape[1], K=h,
+               workspace=eng.gemm_ws)
         K.cross_entropy(self.logits, self.labels.view(-1), V=V, scale=1.0 / (n * self.n_in),
                         row_loss=self.row_loss, loss_out=self.loss, dlogits=self.logits)
-        K.gemm("nn", self.logits, self.head, self.dxn, M=T, N=h, K=self.logits.shape[1])
+        K.gemm("nn", self.logits, self.head, self.dxn, M=T, N=h, K=self.logits.shape[1],
+               workspace=eng.gemm_ws)
         cur, nxt = self.grads
         K.rmsnorm_bwd(self.dxn, self.stream[L], self.final_norm, self.rstd, None, dh_f32=cur)
         for b in reversed(range(L)):

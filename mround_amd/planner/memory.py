@@ -20,9 +20,11 @@ stage by stage:
   block);
 * ``remainder``: the round-to-nearest codes of the tensors outside the blocks.
 
-Every stage holds the model and the library's two internal workspaces (the
-GEMM k-split partials and the attention dK/dV partials, 128 MiB each).
-Figures are bytes; the torch allocator's rounding adds under 1 %.
+Every block engine holds its own workspaces for the library: the GEMM
+k-split partials and the attention backward's dK/dV partials, at the sizes
+the library's queries give for the engine's products (the library allocates
+nothing itself). Figures are bytes; the torch allocator's rounding adds
+under 1 %.
 """
 
 from __future__ import annotations
@@ -34,7 +36,6 @@ from typing import Any
 from mround_amd.exceptions import ArchitectureError, MemoryBudgetError
 
 GIB = 1 << 30
-LIBRARY_WORKSPACES = 2 * (128 << 20)  # mr_gemm k-split partials + mr_attn_bwd dK/dV partials
 LOSS_WORKSPACE = 401_424  # mr_loss_workspace_bytes
 SEQ_ALIGN = 128
 _DTYPE_BYTES = {"bfloat16": 2, "float16": 2, "float32": 4}
@@ -103,9 +104,21 @@ class ModelShape:
         return self.layers * per_block + embed + head + self.hidden * self.dtype_bytes
 
 
-def engine_bytes(m: ModelShape, tokens: int, seq_len: int, *, input_grads: bool = False) -> int:
+def library_workspace_bytes(m: ModelShape, tokens: int, seq_len: int,
+                            extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> int:
+    """The GEMM k-split and attention dK/dV workspaces a ``BlockEngine`` at
+    ``tokens`` tokens owns (the library's size queries)."""
+    from mround_amd.pipeline.block import BlockShape, workspace_bytes
+
+    shape = BlockShape(hidden=m.hidden, n_heads=m.heads, n_kv_heads=m.kv_heads, head_dim=m.head_dim,
+                       intermediate=m.intermediate)
+    return sum(workspace_bytes(shape, tokens // seq_len, seq_len, extra_gemms))
+
+
+def engine_bytes(m: ModelShape, tokens: int, seq_len: int, *, input_grads: bool = False,
+                 extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> int:
     """``BlockEngine`` at ``tokens`` tokens: fused W' (bf16) and dL/dW' (fp32),
-    the saved activations and the backward's buffers."""
+    the saved activations, the backward's buffers and the library workspaces."""
     T, h, q, mlp = tokens, m.hidden, m.qkv_rows, m.intermediate
     hq_d = m.heads * m.head_dim
     weights = m.block_weights * (2 + 4)
@@ -114,7 +127,8 @@ def engine_bytes(m: ModelShape, tokens: int, seq_len: int, *, input_grads: bool 
     rope = seq_len * (m.head_dim // 2) * 2 * 4
     extra = T * h * 4 if input_grads else 0
     scalars = 2 * 4  # loss value and outlier threshold
-    return weights + acts + bwd + rope + LOSS_WORKSPACE + scalars + extra
+    ws = library_workspace_bytes(m, tokens, seq_len, extra_gemms)
+    return weights + acts + bwd + rope + LOSS_WORKSPACE + scalars + extra + ws
 
 
 def activation_bytes(m: ModelShape, tokens: int) -> int:
@@ -168,7 +182,7 @@ def _groups(m: ModelShape, gs: int) -> int:
 
 def predict_memory(m: ModelShape, run: RunShape) -> MemoryPrediction:
     """Device bytes of each stage of the run (see the module docstring)."""
-    base = m.model_bytes() + LIBRARY_WORKSPACES
+    base = m.model_bytes()
     stages = {"load": base}
     L, h = m.layers, m.hidden
     if run.mixed:
@@ -176,7 +190,8 @@ def predict_memory(m: ModelShape, run: RunShape) -> MemoryPrediction:
         S = -(-n_in // SEQ_ALIGN) * SEQ_ALIGN
         T = run.scoring_batch * S
         Vp = -(-m.vocab // 64) * 64
-        lm = (engine_bytes(m, T, S, input_grads=True) + L * m.block_weights * 2 + L * activation_bytes(m, T)
+        lm = (engine_bytes(m, T, S, input_grads=True, extra_gemms=((T, Vp, h), (T, h, Vp)))
+              + L * m.block_weights * 2 + L * activation_bytes(m, T)
               + (L + 1 + 2) * T * h * 4 + T * Vp * 2 + T * h * (2 + 4) + T * 4 * 2 + 2 * T * 4 + h * 4 + 4)
         if Vp != m.vocab:
             lm += Vp * h * 2

@@ -37,7 +37,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.mr_abi_version() == 1
+    assert lib.mr_abi_version() == 2
 
 
 @pytest.mark.parametrize(("cols", "bits", "words"), [(64, 2, 4), (64, 4, 8), (64, 8, 16), (64, 3, 6),
@@ -85,16 +85,65 @@ def test_host_validation_refuses_before_launch(lib):
     # GEMM outputs are written in 16-byte row pieces: C, resid and the SwiGLU
     # outputs must be 16-byte aligned with 16-byte rows
     MR_F32, MR_BF16 = 0, 1
-    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(264), MR_F32, 64, None, None, 0, None)
+    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(264), MR_F32, 64, None, None, 0, None, 0,
+                     None)
     assert rc == -22 and b"16-byte" in lib.mr_last_error()
-    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_BF16, 68, None, None, 0, None)
+    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_BF16, 68, None, None, 0, None, 0,
+                     None)
     assert rc == -22 and b"16-byte" in lib.mr_last_error()
-    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_F32, 64, None, P(256), 66, None)
+    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_F32, 64, None, P(256), 66, None, 0,
+                     None)
     assert rc == -22 and b"16-byte" in lib.mr_last_error()
-    rc = lib.mr_gemm_swiglu(64, 64, 64, P(256), 64, P(256), 64, P(256), 68, None, 0, None)
+    rc = lib.mr_gemm_swiglu(64, 64, 64, P(256), 64, P(256), 64, P(256), 68, None, 0, None, 0, None)
     assert rc == -22 and b"16-byte" in lib.mr_last_error()
+    # a misaligned k-split workspace
+    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_F32, 64, None, None, 0, P(264), 1024,
+                     None)
+    assert rc == -22 and b"workspace" in lib.mr_last_error()
 
 
 def test_workspace_sizes(lib):
     assert lib.mr_loss_workspace_bytes(1 << 26) > 0
     assert lib.mr_delta_loss_workspace_bytes(3584, 18944, 3) > 0
+
+
+# (M, N, K) of the Qwen2.5-7B block's products at 8 x 2048 tokens whose
+# 256 x 256 tiles leave a partial last wave with a long K: the remainder is
+# cut along K into partial tiles of 256 KiB.
+@pytest.mark.parametrize(("M", "N", "K"), [(16384, 3584, 18944), (16384, 3584, 37888),
+                                           (3584, 18944, 16384), (37888, 3584, 16384)])
+def test_gemm_workspace_split_shapes(lib, M, N, K):
+    tiles = ((M + 255) // 256) * ((N + 255) // 256)
+    nbytes = lib.mr_gemm_workspace_bytes(M, N, K)
+    tile = 256 * 256 * 4
+    assert 0 < nbytes <= 128 << 20 and nbytes % tile == 0
+    assert (nbytes // tile) % (tiles % 256) == 0  # whole splits of every remainder tile
+
+
+@pytest.mark.parametrize(("M", "N", "K"), [(16384, 4608, 3584), (16384, 37888, 3584), (16384, 3584, 3584),
+                                           (16384, 4096, 18944), (64, 64, 64)])
+def test_gemm_workspace_unsplit_shapes(lib, M, N, K):
+    # a short K (under 96 steps of 64) or whole waves of tiles: no partials
+    assert lib.mr_gemm_workspace_bytes(M, N, K) == 0
+
+
+def test_attention_workspace_follows_the_head_split(lib):
+    T = 8 * 2048
+    # 7B: 4 kv heads x 8 x 16 key blocks = 512 blocks, no split
+    assert lib.mr_attn_bwd_workspace_bytes(8, 2048, 28, 4, 128, 0) == 0
+    # 0.5B: 2 kv heads (256 blocks) split the 7 query heads of a group in two
+    assert lib.mr_attn_bwd_workspace_bytes(8, 2048, 14, 2, 64, 0) == 2 * T * 2 * 2 * 64 * 4
+    # a forced split sizes its partials; 1 needs none
+    assert lib.mr_attn_bwd_workspace_bytes(8, 2048, 28, 4, 128, 7) == 7 * T * 2 * 4 * 128 * 4
+    assert lib.mr_attn_bwd_workspace_bytes(8, 2048, 28, 4, 128, 1) == 0
+
+
+def test_attention_backward_refuses_a_bad_split(lib):
+    P = ctypes.c_void_p
+    args = (P(256), 2304, P(256), P(256), 1792, P(256), P(256), 1, 256, 14, 2, 128, 0.1, P(256))
+    # more blocks per kv head than the group has query heads
+    assert lib.mr_attn_bwd(*args, 8, None, 0, None) == -22
+    assert b"hsplit" in lib.mr_last_error()
+    # a forced split without room for its partials
+    assert lib.mr_attn_bwd(*args, 2, P(256), 1024, None) == -22
+    assert b"workspace" in lib.mr_last_error()

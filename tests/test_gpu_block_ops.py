@@ -95,31 +95,13 @@ def test_attention_forward(case):
     assert torch.allclose(lse.double().cpu(), ref["lse"], rtol=0, atol=2e-5)
 
 
-@pytest.mark.parametrize("case", ATTN_CASES)
-def test_attention_backward(case):
-    B, S, Hq, Hkv, D, mag = case
-    print("case attn bwd", case, flush=True, file=sys.stderr)
-    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, mag, seed=22, pad=32)
-    width = (Hq + 2 * Hkv) * D
-    scale = 1.0 / math.sqrt(D)
-    dout = torch.randn(B * S, Hq * D, generator=_gen(23)).to(torch.bfloat16)
+def _check_attention_backward(qkv, dout, got, B, S, Hq, Hkv, D, scale):
+    """dQ, dK, dV of the kernel (``got``: float64 [B*S, (Hq + 2 Hkv) D]) against
+    float64 autograd over the same bf16 inputs, within bounds built from the
+    reference quantities (the kernel's own output, P and dS rounded to bf16)."""
     ref = attention_ref(qkv, B, S, Hq, Hkv, D, scale, dout=dout)
-
-    q_d = qkv.to(dev())
-    out = torch.empty(B * S, Hq * D, dtype=torch.bfloat16, device=dev())
-    lse = torch.empty(B, Hq, S, device=dev())
-    K.attn_fwd(q_d, batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv, head_dim=D, scale=scale,
-               out=out, lse=lse)
-    dsum = torch.empty(B, Hq, S, device=dev())
-    dqkv = torch.full((B * S, ld), 3.0, dtype=torch.bfloat16, device=dev())
-    K.attn_bwd(q_d, out, dout.to(dev()), lse, dsum, batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv,
-               head_dim=D, scale=scale, dqkv=dqkv)
-    got = dqkv.double().cpu()
-    assert torch.all(got[:, width:] == 3.0), "padding columns were written"
-    got = got[:, :width].reshape(B, S, Hq + 2 * Hkv, D)
+    got = got.reshape(B, S, Hq + 2 * Hkv, D)
     want = ref["dqkv"].reshape(B, S, Hq + 2 * Hkv, D)
-
-    # error bounds from the reference quantities
     p, q, k, v = ref["p"], ref["q"], ref["k"], ref["v"]
     do = dout.double().reshape(B, S, Hq, D).permute(0, 2, 1, 3)
     o = ref["out"].reshape(B, S, Hq, D).permute(0, 2, 1, 3)
@@ -144,6 +126,93 @@ def test_attention_backward(case):
         err = (g - w).abs()
         print(f"  {name} max err/tol", float((err / t).max()), file=sys.stderr)
         assert torch.all(err <= t), name
+
+
+def _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, *, hsplit=0):
+    """Forward then backward on the GPU; returns dqkv (device, [B*S, ld], its
+    padding columns pre-filled with 3.0)."""
+    scale = 1.0 / math.sqrt(D)
+    q_d = qkv.to(dev())
+    out = torch.empty(B * S, Hq * D, dtype=torch.bfloat16, device=dev())
+    lse = torch.empty(B, Hq, S, device=dev())
+    K.attn_fwd(q_d, batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv, head_dim=D, scale=scale,
+               out=out, lse=lse)
+    dsum = torch.empty(B, Hq, S, device=dev())
+    dqkv = torch.full((B * S, ld), 3.0, dtype=torch.bfloat16, device=dev())
+    K.attn_bwd(q_d, out, dout.to(dev()), lse, dsum, batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv,
+               head_dim=D, scale=scale, dqkv=dqkv, hsplit=hsplit)
+    return dqkv
+
+
+@pytest.mark.parametrize("case", ATTN_CASES)
+def test_attention_backward(case):
+    B, S, Hq, Hkv, D, mag = case
+    print("case attn bwd", case, flush=True, file=sys.stderr)
+    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, mag, seed=22, pad=32)
+    width = (Hq + 2 * Hkv) * D
+    dout = torch.randn(B * S, Hq * D, generator=_gen(23)).to(torch.bfloat16)
+    got = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld).double().cpu()
+    assert torch.all(got[:, width:] == 3.0), "padding columns were written"
+    _check_attention_backward(qkv, dout, got[:, :width], B, S, Hq, Hkv, D, 1.0 / math.sqrt(D))
+
+
+# Every way the dK/dV kernel can walk a group of G query heads: one block per
+# kv head walking all G (hsplit 1, bf16 written directly: the Qwen2.5-7B
+# launch, G = 7), uneven splits into fp32 partials (G = 7 over 2 blocks: 3 + 4
+# heads, the Qwen2.5-0.5B launch; over 3: 2 + 2 + 3; G = 8 over 2: the
+# Qwen2.5-3B launch) and one head per block (hsplit G).
+SPLIT_CASES = [
+    # B, S, Hq, Hkv, D, hsplit
+    (1, 256, 14, 2, 64, 1), (1, 256, 14, 2, 64, 2), (1, 256, 14, 2, 64, 3), (1, 256, 14, 2, 64, 7),
+    (2, 128, 14, 2, 128, 1), (2, 128, 14, 2, 128, 2), (2, 128, 14, 2, 128, 7),
+    (1, 256, 8, 1, 128, 1), (1, 256, 8, 1, 128, 2), (1, 256, 8, 1, 128, 3), (1, 256, 8, 1, 128, 8),
+    (1, 256, 16, 2, 64, 1), (1, 256, 16, 2, 64, 2), (1, 256, 16, 2, 64, 8),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_attention_backward_head_split(case):
+    B, S, Hq, Hkv, D, hsplit = case
+    print("case attn bwd split", case, flush=True, file=sys.stderr)
+    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, 1.5, seed=24, pad=32)
+    width = (Hq + 2 * Hkv) * D
+    dout = torch.randn(B * S, Hq * D, generator=_gen(25)).to(torch.bfloat16)
+    got = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=hsplit).double().cpu()
+    assert torch.all(got[:, width:] == 3.0), "padding columns were written"
+    _check_attention_backward(qkv, dout, got[:, :width], B, S, Hq, Hkv, D, 1.0 / math.sqrt(D))
+
+
+def test_attention_head_splits_agree():
+    """The split changes only the order dK/dV partials are summed in: every
+    split of one problem agrees within a few bf16 units (dQ is bit-identical)."""
+    B, S, Hq, Hkv, D = 1, 256, 14, 2, 64
+    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, 1.5, seed=26, pad=0)
+    dout = torch.randn(B * S, Hq * D, generator=_gen(27)).to(torch.bfloat16)
+    runs = {h: _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=h).float().cpu() for h in (1, 2, 7)}
+    for h in (2, 7):
+        assert torch.equal(runs[h][:, :Hq * D], runs[1][:, :Hq * D]), "dQ depends on the split"
+        kv = slice(Hq * D, None)
+        assert torch.allclose(runs[h][:, kv], runs[1][:, kv], rtol=4 * U, atol=1e-3)
+
+
+@pytest.mark.parametrize("hsplit", [0, 2])
+def test_attention_backward_7b_launch(hsplit):
+    """The exact launch of the Qwen2.5-7B block tune (8 x 2048 tokens, 28 query
+    and 4 kv heads of 128: 512 dK/dV blocks, each walking its group's 7 query
+    heads; hsplit 0 is the automatic choice, 1 there) and the same over fp32
+    partials, checked on one (sequence, kv head) slice against float64."""
+    B, S, Hq, Hkv, D = 8, 2048, 28, 4, 128
+    print("case attn bwd 7b", hsplit, flush=True, file=sys.stderr)
+    assert K.attn_bwd_workspace_bytes(batch=B, seq_len=S, n_heads=Hq, n_kv_heads=Hkv, head_dim=D) == 0
+    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, 1.0, seed=28, pad=0)
+    dout = torch.randn(B * S, Hq * D, generator=_gen(29)).to(torch.bfloat16)
+    got = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=hsplit).cpu()
+    G, b, g = Hq // Hkv, 5, 2
+    rows = slice(b * S, (b + 1) * S)
+    cols = list(range(g * G * D, (g + 1) * G * D)) + list(range((Hq + g) * D, (Hq + g + 1) * D)) + \
+        list(range((Hq + Hkv + g) * D, (Hq + Hkv + g + 1) * D))
+    _check_attention_backward(qkv[rows][:, cols], dout[rows][:, g * G * D:(g + 1) * G * D],
+                              got[rows][:, cols].double(), 1, S, G, 1, D, 1.0 / math.sqrt(D))
 
 
 def test_attention_rejects_bad_shapes():

@@ -186,6 +186,21 @@ int mr_loss_outlier(const float* pred, const float* target, int64_t n, int64_t k
                     float* grad_out, void* workspace, void* stream);
 
 /*
+ * mr_loss_outlier without a workspace argument and without any allocation:
+ * its workspace (401,424 bytes: block partials, both radix histograms, the
+ * select state) is a static device array of the library, one per GPU, held
+ * until the process ends; zero_hist clears what must start at zero on every
+ * call. No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc). n is at most 2^32 - 1 (MR_EINVAL beyond). Every call on
+ * one GPU shares that array, so calls that overlap on one GPU (different
+ * streams, or threads) race; issue them in order on one stream.
+ */
+int mr_loss_outlier_noalloc(const float* pred, const float* target, int64_t n, int64_t k,
+                            int64_t denom, const float* threshold_in, float* threshold_out,
+                            float* loss_out, float* grad_out, void* stream);
+
+/*
  * DeltaLoss accumulation: scores_out[i] += sum |g * (rtn_i(W) - W)| for each
  * width bits_list[i] (round-to-nearest at that width, fp32 terms, fp64 sum).
  * Replaces the per-batch term of mround/pipeline/scoring.py:238-266;

@@ -16,6 +16,8 @@
 // Sums are deterministic: a fixed grid of kBlocks blocks, fp64 accumulation
 // per thread, a fixed-order block reduction, then one block adding the block
 // partials in order.
+#include <mutex>
+
 #include "mr_common.h"
 
 namespace mr {
@@ -34,6 +36,9 @@ struct Workspace {
   uint32_t hist_lo[kLoBins];
   uint32_t state[4];  // [0] top-15-bit digit, [1] remaining rank k, [2] final key
 };
+constexpr size_t kScratchBytes = sizeof(Workspace);
+constexpr int64_t kMaxElements = 0xffffffffLL;  // histogram counts are 32-bit
+constexpr int kMaxDevices = 64;
 
 __device__ __forceinline__ double block_sum(double x, double* smem) {
   for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
@@ -243,12 +248,76 @@ int grid_for(int64_t n) {
 }
 
 int check_loss(const char* fn, const float* pred, const float* target, int64_t n, int64_t denom,
-               float* loss_out, void* workspace) {
-  if (!pred || !target || !loss_out || !workspace) return fail(MR_EINVAL, "%s: null pointer", fn);
+               float* loss_out) {
+  if (!pred || !target || !loss_out) return fail(MR_EINVAL, "%s: null pointer", fn);
   if (n <= 0) return fail(MR_EINVAL, "%s: empty input", fn);
   if (denom <= 0) return fail(MR_EINVAL, "%s: denominator must be positive", fn);
   if ((n % 4) == 0 && (!aligned16(pred) || !aligned16(target)))
     return fail(MR_EINVAL, "%s: inputs must be 16-byte aligned", fn);
+  return MR_OK;
+}
+
+// The outlier loss on workspace ws (checked by the caller).
+int outlier(const char* fn, const float* pred, const float* target, int64_t n, int64_t k, int64_t denom,
+            const float* threshold_in, float* threshold_out, float* loss_out, float* grad_out,
+            Workspace* ws, hipStream_t s) {
+  if (!threshold_in && (k < 1 || k > n))
+    return fail(MR_EINVAL, "%s: rank k=%lld outside [1, n]", fn, static_cast<long long>(k));
+  if (n > kMaxElements)
+    return fail(MR_EINVAL, "%s: %lld elements, more than the %lld the select counts", fn,
+                static_cast<long long>(n), static_cast<long long>(kMaxElements));
+  if (grad_out && (n % 4) == 0 && !aligned16(grad_out))
+    return fail(MR_EINVAL, "%s: gradient must be 16-byte aligned", fn);
+  const int grid = grid_for(n);
+  if (!threshold_in) {
+    int64_t hg = ((n & 3) == 0 ? n / 4 : n) / kHistThreads + 1;
+    const int hist_grid = static_cast<int>(hg < 256 ? hg : 256);
+    hipLaunchKernelGGL(zero_hist, dim3(kLoBins / kBlock), dim3(kBlock), 0, s, ws, static_cast<uint32_t>(k));
+    hipLaunchKernelGGL(radix_hist_hi, dim3(hist_grid), dim3(kHistThreads), 0, s, pred, target, n, ws);
+    hipLaunchKernelGGL(radix_select, dim3(1), dim3(kSelThreads), 0, s, 1, ws, threshold_out);
+    hipLaunchKernelGGL(radix_hist_lo, dim3(hist_grid), dim3(kHistThreads), 0, s, pred, target, n, ws);
+    hipLaunchKernelGGL(radix_select, dim3(1), dim3(kSelThreads), 0, s, 0, ws, threshold_out);
+  } else if (threshold_out) {
+    return fail(MR_EINVAL, "%s: threshold_out is only written when it is computed", fn);
+  }
+  const float gscale = static_cast<float>(2.0 / static_cast<double>(denom));
+  hipLaunchKernelGGL(loss_pass, dim3(grid), dim3(kBlock), 0, s, pred, target, n, gscale,
+                     threshold_in, ws, 1, grad_out, ws);
+  hipLaunchKernelGGL(finalize, dim3(1), dim3(kBlock), 0, s, ws, grid, static_cast<double>(denom),
+                     loss_out);
+  MR_LAUNCH_CHECK(fn);
+  return MR_OK;
+}
+
+}  // namespace
+}  // namespace mr
+
+// The allocation-free outlier loss keeps its workspace in this array, one
+// copy per GPU, held until the process ends (kScratchBytes = the Workspace,
+// 401,424 bytes). Host code never passes the array's name to a kernel: that
+// name is a host-side stand-in. The device address comes from
+// hipGetSymbolAddress, once per device, on the first call there.
+static __device__ __align__(256) unsigned char scratch[mr::kScratchBytes];
+
+namespace mr {
+namespace {
+
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "mr_loss_outlier_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MR_EINVAL, "mr_loss_outlier_noalloc: device %d past the %d supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "mr_loss_outlier_noalloc: hipGetSymbolAddress(scratch)");
+    addr[dev] = p;
+  }
+  *out = addr[dev];
   return MR_OK;
 }
 
@@ -266,8 +335,9 @@ int mr_loss_mse(const float* pred, const float* target, int64_t n, int64_t denom
                 float* loss_out, float* grad_out, void* workspace, void* stream) {
   using namespace mr;
   clear_error();
-  int rc = check_loss("mr_loss_mse", pred, target, n, denom, loss_out, workspace);
+  int rc = check_loss("mr_loss_mse", pred, target, n, denom, loss_out);
   if (rc) return rc;
+  if (!workspace) return fail(MR_EINVAL, "mr_loss_mse: null workspace");
   if (grad_out && (n % 4) == 0 && !aligned16(grad_out))
     return fail(MR_EINVAL, "mr_loss_mse: gradient must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -287,34 +357,25 @@ int mr_loss_outlier(const float* pred, const float* target, int64_t n, int64_t k
                     float* grad_out, void* workspace, void* stream) {
   using namespace mr;
   clear_error();
-  int rc = check_loss("mr_loss_outlier", pred, target, n, denom, loss_out, workspace);
+  int rc = check_loss("mr_loss_outlier", pred, target, n, denom, loss_out);
   if (rc) return rc;
-  if (!threshold_in && (k < 1 || k > n))
-    return fail(MR_EINVAL, "mr_loss_outlier: rank k=%lld outside [1, n]", static_cast<long long>(k));
-  if (n > 0xffffffffLL) return fail(MR_EINVAL, "mr_loss_outlier: more than 2^32 elements");
-  if (grad_out && (n % 4) == 0 && !aligned16(grad_out))
-    return fail(MR_EINVAL, "mr_loss_outlier: gradient must be 16-byte aligned");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  Workspace* ws = static_cast<Workspace*>(workspace);
-  const int grid = grid_for(n);
-  if (!threshold_in) {
-    int64_t hg = ((n & 3) == 0 ? n / 4 : n) / kHistThreads + 1;
-    const int hist_grid = static_cast<int>(hg < 256 ? hg : 256);
-    hipLaunchKernelGGL(zero_hist, dim3(kLoBins / kBlock), dim3(kBlock), 0, s, ws, static_cast<uint32_t>(k));
-    hipLaunchKernelGGL(radix_hist_hi, dim3(hist_grid), dim3(kHistThreads), 0, s, pred, target, n, ws);
-    hipLaunchKernelGGL(radix_select, dim3(1), dim3(kSelThreads), 0, s, 1, ws, threshold_out);
-    hipLaunchKernelGGL(radix_hist_lo, dim3(hist_grid), dim3(kHistThreads), 0, s, pred, target, n, ws);
-    hipLaunchKernelGGL(radix_select, dim3(1), dim3(kSelThreads), 0, s, 0, ws, threshold_out);
-  } else if (threshold_out) {
-    return fail(MR_EINVAL, "mr_loss_outlier: threshold_out is only written when it is computed");
-  }
-  const float gscale = static_cast<float>(2.0 / static_cast<double>(denom));
-  hipLaunchKernelGGL(loss_pass, dim3(grid), dim3(kBlock), 0, s, pred, target, n, gscale,
-                     threshold_in, ws, 1, grad_out, ws);
-  hipLaunchKernelGGL(finalize, dim3(1), dim3(kBlock), 0, s, ws, grid, static_cast<double>(denom),
-                     loss_out);
-  MR_LAUNCH_CHECK("mr_loss_outlier");
-  return MR_OK;
+  if (!workspace) return fail(MR_EINVAL, "mr_loss_outlier: null workspace");
+  return outlier("mr_loss_outlier", pred, target, n, k, denom, threshold_in, threshold_out, loss_out,
+                 grad_out, static_cast<Workspace*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+int mr_loss_outlier_noalloc(const float* pred, const float* target, int64_t n, int64_t k,
+                            int64_t denom, const float* threshold_in, float* threshold_out,
+                            float* loss_out, float* grad_out, void* stream) {
+  using namespace mr;
+  clear_error();
+  int rc = check_loss("mr_loss_outlier_noalloc", pred, target, n, denom, loss_out);
+  if (rc) return rc;
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  return outlier("mr_loss_outlier_noalloc", pred, target, n, k, denom, threshold_in, threshold_out,
+                 loss_out, grad_out, static_cast<Workspace*>(ws), static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

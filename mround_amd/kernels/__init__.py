@@ -71,6 +71,7 @@ _SIGNATURES = {
     "mr_loss_workspace_bytes": (ctypes.c_size_t, [_L]),
     "mr_loss_mse": (_I, [_P, _P, _L, _L, _P, _P, _P, _P]),
     "mr_loss_outlier": (_I, [_P, _P, _L, _L, _L, _P, _P, _P, _P, _P, _P]),
+    "mr_loss_outlier_noalloc": (_I, [_P, _P, _L, _L, _L, _P, _P, _P, _P, _P]),
     "mr_delta_loss_workspace_bytes": (ctypes.c_size_t, [_L, _L, _I]),
     "mr_delta_loss": (_I, [_P, _I, _P, _L, _L, _I, _P, _I, _I, _F, _P, _P, _P]),
     "mr_copy_bytes": (_I, [_P, _P, ctypes.c_size_t, _P]),
@@ -256,6 +257,17 @@ def loss_outlier(pred, target, *, k, denom, loss_out, threshold_in=None, thresho
                                _ptr(threshold_in), _ptr(threshold_out), _ptr(loss_out),
                                _ptr(grad_out), _ptr(ws), _stream(pred))
     _check(rc, "mr_loss_outlier")
+
+
+def loss_outlier_noalloc(pred, target, *, k, denom, loss_out, threshold_in=None, threshold_out=None,
+                         grad_out=None) -> None:
+    """``mr_loss_outlier_noalloc``: the outlier loss on the library's static
+    per-GPU workspace (no allocation; overlapping calls on one GPU race)."""
+    n = pred.numel()
+    rc = lib().mr_loss_outlier_noalloc(_ptr(_f32(pred, "pred")), _ptr(_f32(target, "target")), n, k, denom,
+                                       _ptr(threshold_in), _ptr(threshold_out), _ptr(loss_out),
+                                       _ptr(grad_out), _stream(pred))
+    _check(rc, "mr_loss_outlier_noalloc")
 
 
 # ------------------------------------------------------------- sensitivity --

@@ -18,7 +18,7 @@ from typing import Any
 import torch
 
 from mround_amd.exceptions import ArchitectureError
-from mround_amd.pipeline.block import LAYERS, QKV, BlockShape, BlockWeights
+from mround_amd.pipeline.block import LAYERS, QKV, ROPE_TYPES, BlockShape, BlockWeights
 from mround_amd.pipeline.runner import DecoderBlock
 
 SUPPORTED_TYPES = ("qwen2", "llama", "mistral")
@@ -41,6 +41,37 @@ class DecoderModel:
         return self.lm_head is None
 
 
+def rope_scaling(config: dict[str, Any]) -> tuple:
+    """The config's RoPE frequency scaling as sorted (key, value) pairs (empty
+    for none). Types the block's rope table does not implement are refused:
+    tuning through the unscaled frequencies would fit a different function
+    from the model's."""
+    raw = config.get("rope_scaling") or config.get("rope_parameters")
+    if not raw:
+        return ()
+    kind = raw.get("rope_type", raw.get("type", "default"))
+    if kind not in ROPE_TYPES:
+        raise ArchitectureError(f"rope_scaling type {kind!r} is not supported (supported: "
+                                f"{', '.join(ROPE_TYPES)})")
+    if kind == "default":
+        return ()
+    need = {"linear": ("factor",),
+            "llama3": ("factor", "low_freq_factor", "high_freq_factor", "original_max_position_embeddings")}[kind]
+    missing = [k for k in need if k not in raw]
+    if missing:
+        raise ArchitectureError(f"rope_scaling of type {kind!r} lacks {', '.join(missing)}")
+    return tuple(sorted([("rope_type", kind)] + [(k, float(raw[k])) for k in need]))
+
+
+def rope_theta(config: dict[str, Any]) -> float:
+    """RoPE base: the top-level ``rope_theta``, or the one inside
+    ``rope_parameters`` (the newer Hugging Face layout), else 10000."""
+    theta = config.get("rope_theta")
+    if theta is None:
+        theta = (config.get("rope_parameters") or {}).get("rope_theta", 10000.0)
+    return float(theta)
+
+
 def block_shape(config: dict[str, Any]) -> BlockShape:
     """The block geometry a config describes."""
     kind = config.get("model_type")
@@ -55,7 +86,7 @@ def block_shape(config: dict[str, Any]) -> BlockShape:
                       n_kv_heads=int(config.get("num_key_value_heads") or heads), head_dim=head_dim,
                       intermediate=int(config["intermediate_size"]),
                       norm_eps=float(config.get("rms_norm_eps", 1e-6)),
-                      rope_theta=float(config.get("rope_theta", 10000.0)), attn_bias=bias)
+                      rope_theta=rope_theta(config), attn_bias=bias, rope_scaling=rope_scaling(config))
 
 
 def _read_tensors(path: Path, device) -> dict[str, torch.Tensor]:

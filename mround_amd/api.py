@@ -30,9 +30,10 @@ from mround_amd.core.quantizer import quantize_codes
 from mround_amd.core.scale_search import search_scales
 from mround_amd.exceptions import (ArchitectureError, CalibrationError, SchemeError,
                                    UnsupportedSchemeError)
-from mround_amd.formats.mlx_export import (QuantizedLayer, export_mlx, narrow_codes,
+from mround_amd.formats.mlx_export import (MLX_GROUP_SIZES, QuantizedLayer, export_mlx, narrow_codes,
                                            require_mlx_representable)
-from mround_amd.pipeline.checkpoint import DecoderModel, dense_tensors, load_model
+from mround_amd.pipeline.block import LAYERS
+from mround_amd.pipeline.checkpoint import DecoderModel, block_shape, dense_tensors, load_model
 from mround_amd.pipeline.runner import QuantizationRunner, RunSummary
 from mround_amd import kernels as K
 from mround_amd.planner import memory as M
@@ -90,6 +91,77 @@ def default_scale_init(narrowest_width: int, symmetry: Symmetry) -> ScaleInit:
     if Symmetry(symmetry) is not Symmetry.SYMMETRIC:
         return ScaleInit.OBSERVED_RANGE
     return ScaleInit.SEARCHED if narrowest_width < LOW_BIT_THRESHOLD else ScaleInit.OBSERVED_RANGE
+
+
+# Below this share of the block stack a run is refused rather than producing a
+# checkpoint mostly at full precision (mround/api.py:156-165).
+MIN_BLOCK_COVERAGE = 0.5
+_DIMENSIONS_SHOWN = 3
+
+
+@dataclasses.dataclass(frozen=True)
+class Coverage:
+    """How much of a block stack a group size reaches (mround/api.py:168-232):
+    a layer is groupable only when its input dimension is a multiple of the
+    group size; the rest are left at full precision."""
+
+    total: int
+    blocked: tuple[tuple[str, int], ...] = ()
+
+    @property
+    def representable(self) -> int:
+        return self.total - len(self.blocked)
+
+    @property
+    def fraction(self) -> float:
+        """Share of the block stack that will be quantized (1 when it has no linears)."""
+        return 1.0 if self.total == 0 else self.representable / self.total
+
+    def alternatives(self, supported) -> tuple[int, ...]:
+        """Which of ``supported`` divide every input dimension that blocked."""
+        dims = {d for _, d in self.blocked}
+        return tuple(sorted(g for g in supported if all(d % g == 0 for d in dims)))
+
+    def explain(self, group_size: int, supported) -> str:
+        dims = sorted({d for _, d in self.blocked})
+        shown = ", ".join(str(d) for d in dims[:_DIMENSIONS_SHOWN]) + (", ..." if len(dims) > _DIMENSIONS_SHOWN
+                                                                        else "")
+        works = self.alternatives(supported)
+        remedy = (f"Group sizes that divide every one of them: {', '.join(str(g) for g in works)}."
+                  if works else "No supported group size divides all of them.")
+        return (f"group size {group_size} can only quantize {self.representable} of {self.total} layers in the "
+                f"block stack ({self.fraction:.0%}); the rest would be left at full precision and the checkpoint "
+                f"would be far larger than the width asked for. Input dimensions that do not divide: {shown}. "
+                f"{remedy}")
+
+
+def block_coverage(model: DecoderModel | str | Path, group_size: int) -> Coverage:
+    """What ``group_size`` can reach in the block stack, from the layers' shapes
+    alone (mround/api.py:257-288): a loaded model, or a checkpoint directory
+    (only its ``config.json`` is read). Per-channel (-1) reaches everything."""
+    if isinstance(model, DecoderModel):
+        blocks = [(b.name, {n: tuple(w.shape) for n, w in b.weights.linears.items()}) for b in model.blocks]
+    else:
+        config = _read_config(model)
+        shape = block_shape(config)
+        blocks = [(f"model.layers.{i}", {n: shape.linear_shape(n) for n in LAYERS})
+                  for i in range(int(config["num_hidden_layers"]))]
+    total, blocked = 0, []
+    for name, shapes in blocks:
+        for layer in LAYERS:
+            total += 1
+            dim = int(shapes[layer][-1])
+            if group_size > 0 and dim % group_size:
+                blocked.append((f"{name}.{layer}", dim))
+    return Coverage(total=total, blocked=tuple(blocked))
+
+
+def _require_coverage(model: DecoderModel, scheme: QuantScheme, minimum: float) -> None:
+    """Refuse a group size that would leave most of the block stack dense
+    (mround/api.py:235-254), before anything is tuned."""
+    coverage = block_coverage(model, scheme.group_size)
+    if coverage.fraction < minimum:
+        raise UnsupportedSchemeError(coverage.explain(scheme.group_size, MLX_GROUP_SIZES))
 
 
 def _resolve_scheme(*, bits, group_size, symmetry, average_bits, candidate_bits, remainder_bits,
@@ -312,7 +384,7 @@ def _read_config(model: str | Path) -> dict[str, Any]:
 
 def _run_shape(config, resolved: QuantScheme, tuning: TuningConfig, *, average_bits, plan, widths,
                gradient_source, scoring_samples, scoring_seq_len, scoring_batch, dense_remainder,
-               quantized_inputs) -> tuple[M.ModelShape, M.RunShape]:
+               quantized_inputs, holdout_batches=0) -> tuple[M.ModelShape, M.RunShape]:
     shape = M.ModelShape.from_config(config)
     mixed = average_bits is not None and plan is None
     samples = SENSITIVITY_SAMPLES if scoring_samples is None else int(scoring_samples)
@@ -324,7 +396,8 @@ def _run_shape(config, resolved: QuantScheme, tuning: TuningConfig, *, average_b
                      group_size=resolved.group_size, searched=resolved.scale_init is ScaleInit.SEARCHED,
                      quantized_inputs=quantized_inputs, mixed=mixed, widths=len(widths),
                      gradient_source=source, scoring_samples=samples, scoring_seq_len=sequence,
-                     scoring_batch=batch, dense_remainder=dense_remainder)
+                     scoring_batch=batch, dense_remainder=dense_remainder, holdout_batches=holdout_batches,
+                     micro_batches=tuning.micro_batches, half=str(config.get("torch_dtype")) == "float16")
     return shape, run
 
 
@@ -335,8 +408,8 @@ def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
                    scoring_samples: int | None = None, scoring_seq_len: int | None = None,
                    scoring_batch_size: int | None = None, scheme: QuantScheme | None = None,
                    tuning: TuningConfig | None = None, scale_init: ScaleInit | str | None = None,
-                   quantized_inputs: bool = True, memory_budget: int | None = None,
-                   device: str = "cuda") -> M.MemoryCheck:
+                   quantized_inputs: bool = True, holdout_batches: int = 0,
+                   memory_budget: int | None = None, device: str = "cuda") -> M.MemoryCheck:
     """Predict the device memory of the run :func:`quantize` would make, and
     stop (mround/api.py:1088-1192). Reads ``config.json`` and nothing else.
     ``memory_budget`` defaults to 90 % of the device's memory."""
@@ -348,7 +421,8 @@ def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
                             widths=candidate_bits if average_bits is not None else (resolved.bits,),
                             gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
                             scoring_seq_len=scoring_seq_len, scoring_batch=scoring_batch_size,
-                            dense_remainder=dense_remainder, quantized_inputs=quantized_inputs)
+                            dense_remainder=dense_remainder, quantized_inputs=quantized_inputs,
+                            holdout_batches=holdout_batches)
     budget = M.default_budget(device) if memory_budget is None else memory_budget
     return M.check_memory(shape, run, budget=budget)
 
@@ -380,6 +454,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
              per_layer_recipe: bool = False, plan: Mapping[str, int] | None = None,
              scale_init: ScaleInit | str | None = None, seed: int | None = None,
              memory_budget: int | None = None, memory_check: bool = True,
+             min_block_coverage: float = MIN_BLOCK_COVERAGE,
              device: str = "cuda", progress=None, scoring_progress=None) -> QuantizeResult:
     """Quantize the local checkpoint ``model`` into ``output_dir``.
 
@@ -393,7 +468,10 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     The run's device memory is predicted from ``config.json`` before anything
     is loaded (``predict_memory``) and a run past ``memory_budget`` (default
     90 % of the device's memory) is refused with ``MemoryBudgetError`` unless
-    ``memory_check`` is off. Raises the reference's exceptions for
+    ``memory_check`` is off. A group size that reaches less than
+    ``min_block_coverage`` of the block stack's linears is refused with
+    ``UnsupportedSchemeError`` (``block_coverage``); the layers it cannot
+    reach are left dense and reported in ``skipped``. Raises the reference's exceptions for
     unrepresentable schemes, bad calibration, unusable plans and unsupported
     architectures.
     """
@@ -414,7 +492,8 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
                                 widths=candidate_bits if average_bits is not None else (resolved.bits,),
                                 gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
                                 scoring_seq_len=scoring_seq_len, scoring_batch=scoring_batch_size,
-                                dense_remainder=dense_remainder, quantized_inputs=quantized_inputs)
+                                dense_remainder=dense_remainder, quantized_inputs=quantized_inputs,
+                                holdout_batches=holdout_batches)
     budget = M.default_budget(device) if memory_budget is None else memory_budget
     memory = M.check_memory(mshape, rshape, budget=budget)
     if memory_check:
@@ -427,6 +506,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     t0 = time.perf_counter()
     m = load_model(model, device=device)
     load_s = time.perf_counter() - t0
+    _require_coverage(m, resolved, min_block_coverage)
     tokens = _load_tokens(m, calibration, tuning, seed, device)
     if tokens.shape[1] != tuning.seq_len:
         raise CalibrationError(f"calibration sequences have {tokens.shape[1]} tokens, tuning.seq_len "
@@ -459,6 +539,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     del entrance
     t1 = time.perf_counter()
     remainder, skipped = _round_to_nearest(m, remainder_scheme, dense=dense_remainder)
+    skipped = [(f"{b.name}.{n}", why) for b in summary.blocks for n, why in b.skipped] + skipped
     quantized.update(remainder)
     if not quantized:
         raise ArchitectureError(f"nothing in {model!r} could be quantized at group_size={group_size}")

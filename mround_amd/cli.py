@@ -50,7 +50,10 @@ def _parser() -> argparse.ArgumentParser:
     q.add_argument("--lr", type=float, default=None)
     q.add_argument("--calibration", default="random")
     q.add_argument("--seed", type=int, default=None)
-    q.add_argument("--allow-dense", action="store_true", help="leave embedding/head dense")
+    q.add_argument("--micro-batches", type=int, default=None,
+                   help="run each step's batch in this many pieces, summing their gradients (default: 1)")
+    q.add_argument("--allow-dense", action="store_true",
+                   help="proceed even when the group size reaches under half of the block stack's layers")
     q.add_argument("--memory-budget", type=float, default=None,
                    help="GB the run may use on the device (default: 90 %% of its memory)")
     q.add_argument("--skip-memory-check", action="store_true",
@@ -94,7 +97,8 @@ def _tuning(args):
 
     kw = {}
     for field, val in (("iters", args.iters), ("n_samples", args.samples), ("seq_len", args.seq_len),
-                       ("batch_size", args.batch_size), ("lr", args.lr)):
+                       ("batch_size", args.batch_size), ("lr", args.lr),
+                       ("micro_batches", getattr(args, "micro_batches", None))):
         if val is not None:
             kw[field] = val
     return TuningConfig(**kw)
@@ -138,8 +142,7 @@ def main(argv=None) -> int:
                 args.model, bits=args.bits, group_size=args.group_size,
                 symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
                 average_bits=args.average_bits, candidate_bits=_widths(args.options),
-                remainder_bits=args.remainder_bits, dense_remainder=args.allow_dense,
-                tuning=_tuning(args), memory_budget=budget)
+                remainder_bits=args.remainder_bits, tuning=_tuning(args), memory_budget=budget)
             print(f"  {check.explain()}")
             return 0 if check.fits else 1
         plan = None
@@ -152,7 +155,8 @@ def main(argv=None) -> int:
                               average_bits=args.average_bits, candidate_bits=_widths(args.options),
                               remainder_bits=args.remainder_bits, plan=plan, tuning=_tuning(args),
                               calibration=args.calibration, export_format=args.format,
-                              dense_remainder=args.allow_dense, seed=args.seed, memory_budget=budget,
+                              min_block_coverage=0.0 if args.allow_dense else api.MIN_BLOCK_COVERAGE,
+                              seed=args.seed, memory_budget=budget,
                               memory_check=not args.skip_memory_check,
                               progress=lambda b: print(f"  block {b.index}: loss {b.initial_loss:.4g} -> "
                                                        f"{b.final_loss:.4g} in {b.seconds:.2f} s", flush=True),

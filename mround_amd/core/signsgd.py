@@ -5,6 +5,9 @@
 form: the straight-through backward of ``fake_quantize``, the sign step and
 the projection of ``mround/core/quantizer.py:430-446`` in one HIP kernel that
 reads W, v and dL/dW' once and writes v, alpha and beta in place.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

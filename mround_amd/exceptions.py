@@ -7,6 +7,9 @@ caller checking argument values catches it the ordinary way.
 :class:`KernelError` is this package's addition: the HIP library reported a
 failure (a bad argument caught by the C ABI, or a HIP runtime error). It is
 raised instead of falling back to any other implementation.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

@@ -8,6 +8,9 @@ files are written with ``safetensors`` (``metadata={"format": "mlx"}``).
 MLX reconstructs ``W = scales * q_u + biases`` with ``q_u`` the stored
 unsigned code; the bias is formed from the *stored* (rounded) scale, so
 symmetric zero stays exactly representable.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

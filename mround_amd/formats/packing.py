@@ -5,6 +5,9 @@ itself is ``mr_pack_codes`` / ``mr_unpack_codes``. Codes are expected in one
 byte each (uint8, or int8 with ``offset``) -- the form the tuning path keeps
 them in (``mround/formats/mlx_export.py:109-125``); wider integer tensors are
 narrowed after their range has been checked.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

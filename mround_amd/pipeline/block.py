@@ -56,6 +56,9 @@ class BlockShape:
     norm_eps: float = 1e-6
     rope_theta: float = 10000.0
     attn_bias: bool = False
+    # RoPE frequency scaling as sorted (key, value) pairs of the config's
+    # rope_scaling ("rope_type" plus its parameters); empty: none.
+    rope_scaling: tuple = ()
 
     @property
     def qkv_rows(self) -> int:
@@ -182,9 +185,40 @@ def workspace_bytes(shape: BlockShape, batch: int, seq_len: int,
     return gemm, attn
 
 
-def rope_table(seq_len: int, head_dim: int, theta: float, device) -> torch.Tensor:
-    """cos/sin of ``pos * theta^(-2i/d)``, float32 ``[S, d/2, 2]`` (computed in float64)."""
+ROPE_TYPES = ("default", "linear", "llama3")
+
+
+def rope_frequencies(head_dim: int, theta: float, scaling: tuple = ()) -> torch.Tensor:
+    """The rotary frequencies ``theta^(-2i/d)`` (float64), rescaled as the
+    config's ``rope_scaling`` asks: "linear" divides every frequency by
+    ``factor``; "llama3" (Meta's Llama 3.1 rule) keeps the frequencies whose
+    wavelength is under ``original_max_position_embeddings / high_freq_factor``,
+    divides those over ``original_max_position_embeddings / low_freq_factor``
+    by ``factor``, and blends the two linearly in between, by where
+    ``original_max_position_embeddings / wavelength`` falls between the two
+    factors."""
     inv = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim)
+    params = dict(scaling)
+    kind = params.get("rope_type", "default")
+    if kind == "default":
+        return inv
+    factor = float(params["factor"])
+    if kind == "linear":
+        return inv / factor
+    if kind == "llama3":
+        low, high = float(params["low_freq_factor"]), float(params["high_freq_factor"])
+        context = float(params["original_max_position_embeddings"])
+        wavelength = 2 * math.pi / inv
+        blend = ((context / wavelength - low) / (high - low)).clamp(0.0, 1.0)
+        scaled = (1 - blend) * inv / factor + blend * inv
+        return torch.where(wavelength < context / high, inv,
+                           torch.where(wavelength > context / low, inv / factor, scaled))
+    raise ArchitectureError(f"rope_scaling type {kind!r} is not supported (supported: {', '.join(ROPE_TYPES)})")
+
+
+def rope_table(seq_len: int, head_dim: int, theta: float, device, scaling: tuple = ()) -> torch.Tensor:
+    """cos/sin of ``pos * frequency_i``, float32 ``[S, d/2, 2]`` (computed in float64)."""
+    inv = rope_frequencies(head_dim, theta, scaling)
     ang = torch.arange(seq_len, dtype=torch.float64)[:, None] * inv[None, :]
     return torch.stack([torch.cos(ang), torch.sin(ang)], -1).float().to(device)
 
@@ -224,7 +258,7 @@ class BlockEngine:
         self.dqkv = e(T, shape.qkv_rows)
         self.loss_val = e(1, dt=f32)
         self.threshold = e(1, dt=f32)
-        self.cos_sin = rope_table(seq_len, shape.head_dim, shape.rope_theta, self.device)
+        self.cos_sin = rope_table(seq_len, shape.head_dim, shape.rope_theta, self.device, shape.rope_scaling)
         self.scale = 1.0 / math.sqrt(shape.head_dim)
         self.place = placements(shape)
         self.loss_ws = K.loss_workspace(self.device, T * h)
@@ -236,11 +270,33 @@ class BlockEngine:
         self.attn_ws = e(attn_b, dt=torch.uint8) if attn_b else None
         self.x_in: torch.Tensor | None = None  # block input of the last saving forward
         self.dh32: torch.Tensor | None = None  # fp32 residual gradient, for input gradients
+        self.capacity = batch  # sequences the buffers hold (see set_sequences)
+        self._full = {n: getattr(self, n) for n in self.PER_TOKEN + self.PER_SEQUENCE}
         # name -> [(start, end) HIP events] for the launches being timed, or None
         self.timers: dict[str, list] | None = None
 
     # What a forward(save=True) leaves for the backward, besides its input.
     ACTIVATIONS = ("x1", "rstd1", "qkv", "attn", "lse", "h2", "x2", "rstd2", "act", "gu")
+    # Buffers with a row per token, and with a leading sequence dimension.
+    PER_TOKEN = ("x1", "rstd1", "qkv", "attn", "h2", "x2", "rstd2", "act", "gu", "grad_out",
+                 "grad_out16", "dgu", "dx2", "dh2", "dattn", "dqkv")
+    PER_SEQUENCE = ("lse", "dsum")
+
+    def set_sequences(self, n: int) -> None:
+        """Run the next passes over ``n`` sequences (at most the capacity the
+        engine was built for): every per-token buffer becomes a view of its
+        first ``n * seq_len`` rows. A step's batch runs in pieces this way
+        (``TuningConfig.micro_batches``) on one set of buffers."""
+        if not 1 <= n <= self.capacity:
+            raise ArchitectureError(f"{n} sequences do not fit an engine built for {self.capacity}")
+        if n == self.batch:
+            return
+        T = n * self.seq_len
+        for name in self.PER_TOKEN:
+            setattr(self, name, self._full[name][:T])
+        for name in self.PER_SEQUENCE:
+            setattr(self, name, self._full[name][:n])
+        self.batch, self.tokens = n, T
 
     def new_activations(self) -> dict[str, torch.Tensor]:
         """A fresh set of the saved-activation buffers, for keeping several
@@ -340,26 +396,35 @@ class BlockEngine:
         self._run("gemm_down", lambda: K.gemm("nt", self.act, self.wq["down"], out, M=T, N=h, K=mlp,
                                               resid=self.h2, workspace=ws))
 
-    def loss(self, out: torch.Tensor, target: torch.Tensor, *, suppress: bool, with_grad: bool) -> torch.Tensor:
+    def loss(self, out: torch.Tensor, target: torch.Tensor, *, suppress: bool, with_grad: bool,
+             denom: int | None = None, threshold: torch.Tensor | None = None) -> torch.Tensor:
         """Reconstruction loss of one batch (device scalar), and dL/dout when asked:
         mean squared error, or with the top 0.1 % of |residuals| excluded
-        (mround/core/losses.py:42-107)."""
+        (mround/core/losses.py:42-107). A piece of a batch passes the whole
+        batch's element count as ``denom`` and, with the outlier rule, the
+        whole batch's ``threshold`` (``piece_loss``, mround/core/losses.py:110-130)."""
         n = out.numel()
+        denom = n if denom is None else denom
         grad = self.grad_out if with_grad else None
-        if suppress:
-            K.loss_outlier(out, target, k=max(1, int(n * 0.001)), denom=n, loss_out=self.loss_val,
+        if suppress and threshold is not None:
+            K.loss_outlier(out, target, k=1, denom=denom, loss_out=self.loss_val, threshold_in=threshold,
+                           grad_out=grad, workspace=self.loss_ws)
+        elif suppress:
+            K.loss_outlier(out, target, k=max(1, int(n * 0.001)), denom=denom, loss_out=self.loss_val,
                            threshold_out=self.threshold, grad_out=grad, workspace=self.loss_ws)
         else:
-            K.loss_mse(out, target, denom=n, loss_out=self.loss_val, grad_out=grad,
+            K.loss_mse(out, target, denom=denom, loss_out=self.loss_val, grad_out=grad,
                        workspace=self.loss_ws)
         return self.loss_val
 
     # --------------------------------------------------------------- backward --
-    def backward(self, dx_out: torch.Tensor | None = None) -> None:
+    def backward(self, dx_out: torch.Tensor | None = None, *, accumulate: bool = False) -> None:
         """dL/dW' of all seven layers into ``self.dw`` from ``self.grad_out``
         (after ``forward(save=True)`` and ``loss(with_grad=True)``, or with
-        ``grad_out`` filled by the caller). With ``dx_out`` (float32 ``[T, h]``,
-        not ``grad_out``) also the gradient with respect to the block input."""
+        ``grad_out`` filled by the caller); ``accumulate`` adds them to what
+        ``self.dw`` holds (the weight-gradient products' residual epilogue), as
+        the pieces of a batch do. With ``dx_out`` (float32 ``[T, h]``, not
+        ``grad_out``) also the gradient with respect to the block input."""
         s, T = self.shape, self.tokens
         if dx_out is not None:
             if self.x_in is None:
@@ -368,20 +433,21 @@ class BlockEngine:
                 raise ArchitectureError(f"dx_out must be float32 [{T}, {s.hidden}]")
             if dx_out.data_ptr() == self.grad_out.data_ptr():
                 raise ArchitectureError("dx_out must not be the output gradient buffer")
-            if self.dh32 is None:
+            if self.dh32 is None or self.dh32.shape[0] != T:
                 self.dh32 = torch.empty(T, s.hidden, dtype=torch.float32, device=self.device)
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
         ws = self.gemm_ws
+        acc = (lambda k: self.dw[k]) if accumulate else (lambda k: None)
         K.cast_bf16(self.grad_out, self.grad_out16)
         # MLP: dgu from dact = dout Wd'; dWd' = dout^T act; dx2 = dgu Wgu'; dWgu' = dgu^T x2
         self._run("gemm_dact", lambda: K.gemm_swiglu_bwd(self.grad_out16, self.wq["down"], self.gu,
                                                          self.dgu, workspace=ws))
         self._run("gemm_dw_down", lambda: K.gemm("tn", self.grad_out16, self.act, self.dw["down"], M=h,
-                                                 N=mlp, K=T, workspace=ws))
+                                                 N=mlp, K=T, resid=acc("down"), workspace=ws))
         self._run("gemm_dx_gate_up", lambda: K.gemm("nn", self.dgu, self.wq["gu"], self.dx2, M=T, N=h,
                                                     K=2 * mlp, workspace=ws))
         self._run("gemm_dw_gate_up", lambda: K.gemm("tn", self.dgu, self.x2, self.dw["gu"], M=2 * mlp,
-                                                    N=h, K=T, workspace=ws))
+                                                    N=h, K=T, resid=acc("gu"), workspace=ws))
         # dh = dout + rmsnorm'(dx2)
         K.rmsnorm_bwd(self.dx2, self.h2, self.norm_post, self.rstd2, self.grad_out, dh_bf16=self.dh2,
                       dh_f32=self.dh32 if dx_out is not None else None)
@@ -389,7 +455,7 @@ class BlockEngine:
         self._run("gemm_dattn", lambda: K.gemm("nn", self.dh2, self.wq["o"], self.dattn, M=T, N=hq_d,
                                                K=h, workspace=ws))
         self._run("gemm_dw_o", lambda: K.gemm("tn", self.dh2, self.attn, self.dw["o"], M=h, N=hq_d,
-                                              K=T, workspace=ws))
+                                              K=T, resid=acc("o"), workspace=ws))
         self._run("attn_bwd", lambda: K.attn_bwd(
             self.qkv, self.attn, self.dattn, self.lse, self.dsum, batch=self.batch,
             seq_len=self.seq_len, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim,
@@ -397,7 +463,7 @@ class BlockEngine:
         K.rope(self.dqkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads,
                head_dim=s.head_dim, cos_sin=self.cos_sin, backward=True)
         self._run("gemm_dw_qkv", lambda: K.gemm("tn", self.dqkv, self.x1, self.dw["qkv"], M=s.qkv_rows,
-                                                N=h, K=T, workspace=ws))
+                                                N=h, K=T, resid=acc("qkv"), workspace=ws))
         if dx_out is None:
             return
         # dx = dh + rmsnorm'(dqkv Wqkv'); dx2 is free again and holds dx1.

@@ -24,6 +24,7 @@ from mround_amd.core.signsgd import LinearDecay
 from mround_amd.exceptions import ArchitectureError, CalibrationError
 from mround_amd.formats.mlx_export import QuantizedLayer
 from mround_amd.pipeline.block import LAYERS, BlockEngine, BlockShape, BlockWeights, placements, unplace
+from mround_amd.pipeline.block import place as place_rows
 from mround_amd.schemes import DEFAULT_EPS_FP32, QuantScheme, ScaleInit, TuningConfig
 
 V_BOUND = 0.5
@@ -32,6 +33,20 @@ V_BOUND = 0.5
 # GRAPH_MIN_REPLAYS times (see QuantizationRunner._use_graphs).
 GRAPH_MAX_ELEMENTS = 4096 * 1024
 GRAPH_MIN_REPLAYS = 20
+
+
+def piece_bounds(size: int, pieces: int) -> list[tuple[int, int]]:
+    """``size`` sequences in at most ``pieces`` contiguous runs, none empty,
+    the first ones a sequence longer where they cannot be equal
+    (mround/pipeline/blocks.py:609-624)."""
+    count = max(1, min(pieces, size))
+    base, extra = divmod(size, count)
+    bounds, start = [], 0
+    for i in range(count):
+        stop = start + base + (1 if i < extra else 0)
+        bounds.append((start, stop))
+        start = stop
+    return bounds
 
 
 @dataclasses.dataclass
@@ -106,7 +121,7 @@ class _Layer:
         self.mode = mode_of(scheme)
         self.placement = placement
         rows, cols = weight.shape
-        ng = cols // scheme.group_size
+        ng = 1 if scheme.group_size == -1 else cols // scheme.group_size
         dev = weight.device
         self.v = torch.zeros(rows, cols, dtype=torch.float32, device=dev)
         self.alpha = torch.ones(rows, ng, dtype=torch.float32, device=dev)
@@ -115,7 +130,7 @@ class _Layer:
 
     def params(self) -> dict[str, torch.Tensor]:
         rows, cols = self.weight.shape
-        gs = self.scheme.group_size
+        gs = cols if self.scheme.group_size == -1 else self.scheme.group_size
         return {"v": self.v.view(rows, -1, gs), "alpha": self.alpha.unsqueeze(-1),
                 "beta": self.beta.unsqueeze(-1)}
 
@@ -157,16 +172,33 @@ class QuantizationRunner:
         return overrides.get(path, self.scheme)
 
     def engine(self, shape: BlockShape, tokens: int, device) -> BlockEngine:
-        """The block engine for this geometry, built once per run."""
+        """The block engine for this geometry, built once per run: for a batch
+        of ``tokens`` tokens, or for its largest piece when steps run in
+        pieces (``TuningConfig.micro_batches``)."""
         seq = self.tuning.seq_len
         if tokens % seq:
             raise CalibrationError(f"a batch of {tokens} tokens is not whole sequences of {seq}")
-        key = (shape, tokens, str(device))
+        n_seq = tokens // seq
+        capacity = max(hi - lo for lo, hi in piece_bounds(n_seq, self.tuning.micro_batches))
+        key = (shape, capacity, str(device))
         eng = self._engines.get(key)
         if eng is None:
-            eng = BlockEngine(shape, batch=tokens // seq, seq_len=seq, device=device)
+            eng = BlockEngine(shape, batch=capacity, seq_len=seq, device=device)
             self._engines = {key: eng}
         return eng
+
+    def _pieces(self, x: torch.Tensor) -> list[tuple[int, int]]:
+        """Token row ranges of a batch's pieces."""
+        seq = self.tuning.seq_len
+        return [(lo * seq, hi * seq) for lo, hi in piece_bounds(x.shape[0] // seq, self.tuning.micro_batches)]
+
+    def _forward(self, eng: BlockEngine, x: torch.Tensor, out: torch.Tensor) -> None:
+        """``out = block(x)`` for a whole batch (no activations kept), a piece at
+        a time when the engine holds pieces; ``out`` may be ``x``."""
+        seq = self.tuning.seq_len
+        for lo, hi in self._pieces(x):
+            eng.set_sequences((hi - lo) // seq)
+            eng.forward(x[lo:hi], out[lo:hi], save=False)
 
     # ------------------------------------------------------------------ run --
     def run(self, blocks: Sequence[DecoderBlock], entrance: Sequence[torch.Tensor], *,
@@ -188,9 +220,16 @@ class QuantizationRunner:
         # writes into a spare stream and scores each batch against its target;
         # a revert re-commits round to nearest and advances again from the
         # untouched inputs. Identical losses, codes and streams, one pass over
-        # the calibration set fewer per block.
-        fused = quantized_stream is not None and self.fused_advance and self.holdout_batches == 0
+        # the calibration set fewer per block. (A float16 model's committed
+        # reconstruction is rounded through float16, so its W' is not the
+        # tuned one: there the final score is taken separately.)
+        half = any(w.dtype == torch.float16 for b in blocks for w in b.weights.linears.values())
+        fused = (quantized_stream is not None and self.fused_advance and self.holdout_batches == 0
+                 and not half)
         spare = [torch.empty_like(x) for x in quantized_stream] if fused else None
+        # Without a quantized stream the targets are a second stream; the two
+        # trade places after each block, so two streams are held in all.
+        free_targets = None
         results, exported, schemes = [], {}, {}
         for block in blocks:
             t0 = time.perf_counter()
@@ -202,13 +241,11 @@ class QuantizationRunner:
             if quantized_stream is not None:
                 targets = reference_stream
                 for x in targets:
-                    eng.forward(x, x, save=False)
+                    self._forward(eng, x, x)
             else:
-                targets = []
-                for x in reference_stream:
-                    out = torch.empty_like(x)
-                    eng.forward(x, out, save=False)
-                    targets.append(out)
+                targets = free_targets or [torch.empty_like(x) for x in reference_stream]
+                for x, out in zip(reference_stream, targets):
+                    self._forward(eng, x, out)
             torch.cuda.synchronize(eng.device)
             targets_seconds = time.perf_counter() - t0
             inputs = quantized_stream if quantized_stream is not None else reference_stream
@@ -236,7 +273,7 @@ class QuantizationRunner:
             elif quantized_stream is not None:
                 eng.load_dense(block.weights.linears)
                 for x in quantized_stream:
-                    eng.forward(x, x, save=False)
+                    self._forward(eng, x, x)
             exported.update(layers)
             for path in layers:
                 schemes[path] = self._scheme_for(path, scheme_by_layer)
@@ -245,6 +282,8 @@ class QuantizationRunner:
             stages["targets"] = targets_seconds
             stages["advance"] = time.perf_counter() - t1
             result = dataclasses.replace(result, stage_seconds=stages)
+            if quantized_stream is None:
+                free_targets = reference_stream  # this block's inputs, free once its outputs exist
             reference_stream = targets
             results.append(result)
             if self.progress is not None:
@@ -277,22 +316,26 @@ class QuantizationRunner:
             path = f"{path_prefix}.{name}" if path_prefix else name
             scheme = self._scheme_for(path, scheme_by_layer)
             w = block.weights.linears[name]
-            if scheme.group_size == -1 or w.shape[-1] % scheme.group_size:
+            if scheme.group_size > 0 and w.shape[-1] % scheme.group_size:
                 skipped.append((name, f"last dimension {w.shape[-1]} is not a multiple of "
                                       f"{scheme.group_size}"))
                 continue
             layers[name] = _Layer(name, w, scheme, place[name])
-        if skipped:
-            # The fused operands need every layer's W'; a partly quantized block
-            # would need a dense path per skipped layer.
+        if not layers:
             reasons = "; ".join(f"{n}: {why}" for n, why in skipped)
-            raise ArchitectureError(f"block {block.name!r} cannot be tuned whole: {reasons}")
+            raise ArchitectureError(f"nothing in {block.name!r} can be quantized at this group size, so the "
+                                    f"block would be left at full precision without saying so. {reasons}")
 
         eng = self.engine(block.shape, inputs[0].shape[0], inputs[0].device)
         eng.set_block(block.weights)
         t_search = time.perf_counter()
         searched = self._search_scales(eng, block, layers, inputs)
         search_seconds = time.perf_counter() - t_search if searched else 0.0
+        # Layers left dense keep their weight (rounded to bf16) in the fused
+        # operands; the tuned layers' rows are rewritten every step.
+        for name, _ in skipped:
+            p = place[name]
+            place_rows(eng.wq[p.operand], block.weights.linears[name].to(torch.bfloat16), p)
         outcome = self._tune(eng, layers, inputs, targets, defer_final=defer_final)
         t_commit = time.perf_counter()
         exported = {}
@@ -306,7 +349,7 @@ class QuantizationRunner:
             index=block.index, name=block.name, initial_loss=outcome["initial"],
             final_loss=outcome["final"], iterations=self.tuning.iters,
             seconds=time.perf_counter() - started, tuned=tuple(sorted(layers)),
-            reverted=outcome["reverted"], generalization_gap=outcome["gap"],
+            skipped=tuple(skipped), reverted=outcome["reverted"], generalization_gap=outcome["gap"],
             search_seconds=search_seconds, stage_seconds=stages, step_losses=tuple(outcome["losses"]))
         pending = None
         if defer_final and "start" in outcome:
@@ -321,7 +364,7 @@ class QuantizationRunner:
         eng.load_dense(block.weights.linears)
         acc = torch.zeros(len(inputs), dtype=torch.float32, device=eng.device) if targets else None
         for b, (x, out) in enumerate(zip(inputs, outputs)):
-            eng.forward(x, out, save=False)
+            self._forward(eng, x, out)
             if targets:
                 acc[b:b + 1].copy_(eng.loss(out, targets[b], suppress=suppress, with_grad=False))
         return float(acc.double().sum().item()) / len(inputs) if targets else None
@@ -354,12 +397,15 @@ class QuantizationRunner:
                "x2": torch.zeros(s.hidden, device=dev), "act": torch.zeros(s.intermediate, device=dev)}
         eng.load_dense(block.weights.linears)
         scratch = torch.empty_like(inputs[0])
+        seq = self.tuning.seq_len
         for x in inputs:
-            eng.forward(x, scratch, save=False)
-            K.colsumsq(eng.x1, imp["x1"])
-            K.colsumsq(eng.attn, imp["attn"])
-            K.colsumsq(eng.x2, imp["x2"])
-            K.colsumsq(eng.act, imp["act"])
+            for lo, hi in self._pieces(x):
+                eng.set_sequences((hi - lo) // seq)
+                eng.forward(x[lo:hi], scratch[lo:hi], save=False)
+                K.colsumsq(eng.x1, imp["x1"])
+                K.colsumsq(eng.attn, imp["attn"])
+                K.colsumsq(eng.x2, imp["x2"])
+                K.colsumsq(eng.act, imp["act"])
         source = {"self_attn.q_proj": "x1", "self_attn.k_proj": "x1", "self_attn.v_proj": "x1",
                   "self_attn.o_proj": "attn", "mlp.gate_proj": "x2", "mlp.up_proj": "x2",
                   "mlp.down_proj": "act"}
@@ -408,6 +454,8 @@ class QuantizationRunner:
         graph is recorded once per block and replayed on every later step
         that uses the batch; the rates come from a schedule in device memory
         indexed by a device step counter the graph advances."""
+        if eng.capacity * eng.seq_len != self._batch_tokens:
+            return False  # steps in pieces run from the host
         if self.graphs is not None:
             return bool(self.graphs) and eng.timers is None
         small = eng.tokens * eng.shape.hidden <= GRAPH_MAX_ELEMENTS
@@ -427,12 +475,41 @@ class QuantizationRunner:
                                     row_stride=p.row_stride, row_offset=p.row_offset,
                                     wq_out=eng.wq[p.operand], init_scale=layer.init_scale)
 
+    def _gradients(self, eng: BlockEngine, x, target, scratch, suppress: bool, loss_out) -> None:
+        """One step's loss (into ``loss_out``) and dL/dW' of every layer (into
+        ``eng.dw``) for the batch ``x``. A batch in pieces is still one step
+        (mround/pipeline/runner.py:955-1044): each piece's loss is its squared
+        errors over the whole batch's element count and the pieces' weight
+        gradients are summed; the outlier rule's threshold is first taken over
+        the whole batch's output, from a forward pass without activations."""
+        pieces = self._pieces(x)
+        if len(pieces) == 1:
+            eng.set_sequences(eng.capacity)
+            eng.forward(x, scratch, save=True)
+            loss_out.copy_(eng.loss(scratch, target, suppress=suppress, with_grad=True))
+            eng.backward()
+            return
+        n = x.numel()
+        threshold = None
+        if suppress:
+            self._forward(eng, x, scratch)
+            eng.loss(scratch, target, suppress=True, with_grad=False)
+            threshold = eng.threshold
+        loss_out.zero_()
+        seq = self.tuning.seq_len
+        for i, (lo, hi) in enumerate(pieces):
+            eng.set_sequences((hi - lo) // seq)
+            eng.forward(x[lo:hi], scratch[lo:hi], save=True)
+            loss_out.add_(eng.loss(scratch[lo:hi], target[lo:hi], suppress=suppress, with_grad=True, denom=n,
+                                   threshold=threshold))
+            eng.backward(accumulate=i > 0)
+
     def _scores(self, eng, layers, inputs, targets, over, suppress, scratch) -> float:
         """Mean loss over batches ``over`` with the current parameters."""
         self._quantize_all(eng, layers)
         acc = torch.zeros(len(over), dtype=torch.float32, device=eng.device)
         for i, b in enumerate(over):
-            eng.forward(inputs[b], scratch, save=False)
+            self._forward(eng, inputs[b], scratch)
             acc[i:i + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress, with_grad=False))
         return float(acc.double().sum().item()) / len(over)
 
@@ -444,6 +521,7 @@ class QuantizationRunner:
                                        {n: l.scheme.bits for n, l in layers.items()},
                                        per_layer=self.per_layer_recipe)
         n_batches = len(inputs)
+        self._batch_tokens = inputs[0].shape[0]
         held = min(self.holdout_batches, n_batches - 1)
         tuning_batches = list(range(n_batches - held))
         scoring_batches = list(range(n_batches - held, n_batches)) if held else tuning_batches
@@ -471,10 +549,7 @@ class QuantizationRunner:
             if not graphs or step == 0:
                 # (step 0 runs eagerly: it also allocates any library workspace
                 # the step needs before a graph records it)
-                eng.forward(inputs[b], scratch, save=True)
-                step_losses[step:step + 1].copy_(eng.loss(scratch, targets[b], suppress=suppress,
-                                                          with_grad=True))
-                eng.backward()
+                self._gradients(eng, inputs[b], targets[b], scratch, suppress, step_losses[step:step + 1])
                 # the step also writes the next step's W'
                 self._step_all(eng, layers, rates, step, requant=True)
                 if graphs:

@@ -12,12 +12,13 @@ stage by stage:
   scoring pass (``mround_amd.pipeline.causal_lm``): a fused bf16 copy of every
   block's W', every block's saved activations, the residual stream at each
   block boundary, the logits and the block engine at the scoring batch;
-* ``blocks``: the calibration token ids, the fp32 calibration streams (the
-  reference and quantized streams and the spare the advance writes into; one
-  stream more than a run with held-out batches holds),
-  the block engine at the tuning batch, one block's learnables and their
-  snapshot, and the committed codes of every block (their peak, at the last
-  block);
+* ``blocks``: the calibration token ids, the fp32 calibration streams (with
+  quantized inputs the reference and quantized streams, plus the spare the
+  advance writes into when no batches are held out and the model is not
+  float16; without, the inputs and the targets),
+  the block engine at the tuning batch (at its largest piece when steps run
+  in pieces), one block's learnables and their snapshot, and the committed
+  codes of every block (their peak, at the last block);
 * ``remainder``: the round-to-nearest codes of the tensors outside the blocks.
 
 Every block engine holds its own workspaces for the library: the GEMM
@@ -156,6 +157,20 @@ class RunShape:
     scoring_seq_len: int = 1024
     scoring_batch: int = 2
     dense_remainder: bool = False
+    holdout_batches: int = 0
+    micro_batches: int = 1
+    half: bool = False  # float16 model: the final score is taken apart from the advance
+
+    @property
+    def streams(self) -> int:
+        """Calibration streams the block loop holds at once."""
+        fused = self.quantized_inputs and self.holdout_batches == 0 and not self.half
+        return 3 if fused else 2
+
+    @property
+    def piece_sequences(self) -> int:
+        """Sequences the block engine holds: the batch's largest piece."""
+        return -(-self.batch_size // max(1, min(self.micro_batches, self.batch_size)))
 
 
 @dataclasses.dataclass(frozen=True)
@@ -202,12 +217,13 @@ def predict_memory(m: ModelShape, run: RunShape) -> MemoryPrediction:
         tokens = run.scoring_samples * run.scoring_seq_len * 8
         stages["scoring"] = base + lm + grids + tokens + run.n_samples * run.seq_len * 8
     T = run.batch_size * run.seq_len
-    streams = (3 if run.quantized_inputs else 1) * run.n_samples * run.seq_len * h * 4
+    streams = run.streams * run.n_samples * run.seq_len * h * 4
     groups = _groups(m, run.group_size)
     learn = m.block_weights * 4 * 2 + groups * 4 * 4 + (groups * 4 if run.searched else 0)
     committed = L * (m.block_weights + groups * 8)
     transient = m.largest_layer * (1 + 4) + T * h * 4
-    stages["blocks"] = (base + run.n_samples * run.seq_len * 8 + streams + engine_bytes(m, T, run.seq_len)
+    piece = run.piece_sequences * run.seq_len
+    stages["blocks"] = (base + run.n_samples * run.seq_len * 8 + streams + engine_bytes(m, piece, run.seq_len)
                         + learn + committed + transient)
     rem = 0
     if not run.dense_remainder:
@@ -237,9 +253,10 @@ class MemoryCheck:
     def explain(self) -> str:
         if self.fits:
             return self.describe()
-        return (self.describe() + ". The calibration streams take 4 bytes per token and hidden unit "
-                "(three times with quantized inputs), so fewer calibration samples, shorter sequences or "
-                "quantized_inputs=False reduce the blocks stage; a smaller scoring_batch_size or "
+        return (self.describe() + ". The calibration streams take 4 bytes per token and hidden unit, "
+                "three times with quantized inputs and twice without (or with held-out batches), so fewer "
+                "calibration samples, shorter sequences or quantized_inputs=False reduce the blocks stage, "
+                "and micro_batches shrinks the step's activations; a smaller scoring_batch_size or "
                 "scoring_seq_len reduces the scoring stage")
 
     def record(self) -> dict[str, Any]:

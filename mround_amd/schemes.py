@@ -6,6 +6,9 @@ learning-rate rule and the outlier switch. The names, defaults, validation and
 error messages follow the reference so that code written against it reads the
 same here. The enums derive from ``str`` because this package runs on Python
 3.10, which has no ``enum.StrEnum``.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

@@ -279,3 +279,31 @@ def test_gemm_rejects_bad_shapes():
     c = torch.zeros(10, 16, device=dev())
     with pytest.raises(Exception, match="multiples of 8"):
         K.gemm("nt", a, b, c, M=10, N=16, K=64)
+
+
+# The residual epilogue on every layout, with the output written over the
+# residual itself (the accumulation of weight gradients over the pieces of a
+# batch): short K on large tiles, and a long K whose remainder wave is cut
+# along K (the reduce kernel adds the residual).
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("mnk", [(304, 264, 128), (4352, 4096, 6144)])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_gemm_residual_every_layout(layout, mnk, inplace):
+    M, N, Kd = mnk
+    print("case gemm residual", layout, mnk, inplace, flush=True, file=sys.stderr)
+    if layout == "nt":
+        a, b = _rand(M, Kd, seed=61).to(dev()), _rand(N, Kd, seed=62).to(dev())
+        prod, bound = _gpu_ref(a, b.t().contiguous())
+    elif layout == "nn":
+        a, b = _rand(M, Kd, seed=63).to(dev()), _rand(Kd, N, seed=64).to(dev())
+        prod, bound = _gpu_ref(a, b)
+    else:
+        a, b = _rand(Kd, M, seed=65).to(dev()), _rand(Kd, N, seed=66).to(dev())
+        prod, bound = _gpu_ref(a.t().contiguous(), b)
+    resid = torch.randn(M, N, generator=torch.Generator().manual_seed(67)).to(dev())
+    ref = resid + prod
+    c = resid if inplace else torch.full((M, N), 7.0, device=dev())
+    if Kd >= 6144:
+        assert K.gemm_workspace_bytes(M, N, Kd) > 0  # the k-split path
+    K.gemm(layout, a, b, c, M=M, N=N, K=Kd, resid=resid)
+    assert bool(torch.all((c - ref).abs() <= bound + ref.abs() * 2.0**-22))

@@ -27,6 +27,8 @@ from mround_amd.pipeline.causal_lm import CausalLM
 from mround_amd.pipeline.checkpoint import DecoderModel, write_random_checkpoint
 from mround_amd.pipeline.runner import DecoderBlock
 from mround_amd.pipeline.scoring import score_widths
+from mround_amd.planner.allocator import allocate_bits
+from mround_amd.planner.sensitivity import mixed_budget_bits, score_layer_options
 from mround_amd.schemes import QuantScheme, ScaleInit, Symmetry, TuningConfig
 from oracle import block as OB
 from oracle import causal_lm as OC
@@ -324,6 +326,44 @@ def test_score_widths_match_oracle(searched, source):
             assert rel < 3e-2, (p, b, res.scores[p][b], ref[p][b])
     print(f"  worst rel {worst:.2e}", file=sys.stderr)
     assert res.shapes["model.layers.0.mlp.down_proj"] == (128, 256)
+    _check_plans(res.scores, ref, res.shapes, base, worst)
+
+
+def _check_plans(gpu, ref, shapes, base, worst):
+    """The allocation made from the GPU's scores against the one made from
+    the float64 oracle's (mround/planner/allocator.py:98-194) at several
+    budgets: the same assignment, or, where scores within ``worst`` of each
+    other leave a near-tie, a plan whose DeltaLoss under the oracle's scores
+    is within that error of the oracle's optimum."""
+    widths = sorted(next(iter(ref.values())))
+    for avg in np.linspace(widths[0], widths[-1], 7)[1:-1]:
+        budget = mixed_budget_bits(shapes, float(avg), base.group_size)
+        a_gpu = allocate_bits(score_layer_options(gpu, shapes, base), budget_bits=budget)
+        a_ref = allocate_bits(score_layer_options(ref, shapes, base), budget_bits=budget)
+        if a_gpu.by_layer == a_ref.by_layer:
+            continue
+        under_ref = sum(ref[p][b] for p, b in a_gpu.by_layer.items())
+        print(f"  average {avg:.3f}: plans differ; oracle loss of the GPU plan {under_ref:.6g}, "
+              f"optimum {a_ref.predicted_loss:.6g}", file=sys.stderr)
+        assert under_ref <= a_ref.predicted_loss * (1 + worst) / (1 - worst) + 1e-12
+
+
+def test_three_width_plan_matches_oracle():
+    """Scores at 2, 3 and 4 bits (each width's own gradients) and the plans made
+    from them at budgets across the range, against the float64 oracle."""
+    _case("plan 2/3/4")
+    m = _model("qwen2", vocab=256, tied=True, layers=2, seed=6)
+    om = _oracle_model(m)
+    tokens = torch.randint(0, 256, (4, 129), generator=torch.Generator().manual_seed(13))
+    batches = [tokens[:2].to(dev()), tokens[2:].to(dev())]
+    base = QuantScheme(bits=2, group_size=64, symmetry=Symmetry.ASYMMETRIC)
+    res = score_widths(m, batches, [2, 3, 4], base, gradient_source="own_width")
+    ref = OC.score_widths(om, [t.cpu() for t in batches], [2, 3, 4], group_size=64, mode="asym",
+                          gradient_source="own_width")
+    worst = max(abs(res.scores[p][b] - ref[p][b]) / ref[p][b] for p in ref for b in (2, 3, 4))
+    print(f"  worst rel {worst:.2e}", file=sys.stderr)
+    assert worst < 3e-2
+    _check_plans(res.scores, ref, res.shapes, base, worst)
 
 
 def test_schedules_agree_at_the_widest_width():

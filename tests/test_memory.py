@@ -79,14 +79,32 @@ def test_scoring_formula_is_the_causal_lm(tmp_path):
 
 def test_blocks_stage_counts_the_calibration_streams():
     """With quantized inputs the runner holds the reference stream, the
-    quantized stream and the spare its advance writes into; without, one."""
+    quantized stream and the spare its advance writes into (not with held-out
+    batches, whose final score is taken apart); without, the inputs and the
+    targets."""
     m = M.ModelShape.from_config({**GEOMETRIES["qwen2.5-7b"], "vocab_size": 152064})
-    run = M.RunShape(n_samples=128, seq_len=2048, batch_size=8, group_size=64)
     one = 128 * 2048 * m.hidden * 4
-    with_q = M.predict_memory(m, run).stages["blocks"]
-    without = M.predict_memory(m, M.RunShape(n_samples=128, seq_len=2048, batch_size=8, group_size=64,
-                                             quantized_inputs=False)).stages["blocks"]
-    assert with_q - without == 2 * one
+
+    def blocks(**kw):
+        return M.predict_memory(m, M.RunShape(n_samples=128, seq_len=2048, batch_size=8, group_size=64,
+                                              **kw)).stages["blocks"]
+
+    with_q = blocks()
+    assert with_q - blocks(quantized_inputs=False) == one
+    assert with_q - blocks(holdout_batches=1) == one
+    assert with_q - blocks(half=True) == one
+    assert blocks(quantized_inputs=False) == blocks(quantized_inputs=False, holdout_batches=2)
+
+
+def test_micro_batches_shrink_the_engine():
+    """Steps in pieces hold the engine at the largest piece (8 sequences in 3
+    pieces: 3), the rest of the blocks stage unchanged."""
+    m = M.ModelShape.from_config(GEOMETRIES["qwen2.5-0.5b"])
+    whole = M.RunShape(n_samples=16, seq_len=2048, batch_size=8, group_size=64)
+    pieces = M.RunShape(n_samples=16, seq_len=2048, batch_size=8, group_size=64, micro_batches=3)
+    assert pieces.piece_sequences == 3
+    drop = M.predict_memory(m, whole).stages["blocks"] - M.predict_memory(m, pieces).stages["blocks"]
+    assert drop == M.engine_bytes(m, 8 * 2048, 2048) - M.engine_bytes(m, 3 * 2048, 2048) > 0
 
 
 def test_api_refuses_a_run_past_the_budget(tmp_path):

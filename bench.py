@@ -25,8 +25,12 @@ Printed as one JSON line:
   fake_quant the kernel microbench: a bf16 18944 x 3584 weight (0.1 % of
              entries x10), 2-bit gs64; forward, backward + update, the update
              that also writes the next W', and packing, against 8 TB/s;
-  cpu_baseline  the oracle (float32 PyTorch block + NumPy fake quantization)
-             timed on the host on a bounded sample, extrapolated to the tune.
+  cpu_baseline  the CPU path measured on the host's cores: the whole 200-step
+             tune of one SmolLM2-135M-shaped block (8 x 512 tokens, 4-bit) in
+             float32 (the oracle's PyTorch block under its NumPy fake
+             quantization and straight-through gradient), beside the same tune
+             on the GPU; the microbench kernels in NumPy; and, labelled as
+             such, the 7B block tune extrapolated from a timed sample.
 
 ``--gpus N`` with N > 1 exits: the benchmark runs on one GPU only.
 """
@@ -295,19 +299,195 @@ def cpu_baseline(args, tokens_per_batch, batches):
     step = t_fq_fwd + t_fq_bwd + (t_fwd + t_bwd) * scale
     passes = 4 * batches  # targets, two scores, advance
     tune = args.iters * step + passes * (t_fq_fwd / 7 + t_fwd * scale)
-    return {
+    extrapolated = {
         "value": round(tune, 1),
-        "unit": "s per block tune (extrapolated)",
-        "cores": threads,
-        "kind": "port",
+        "unit": "s per 7B block tune (extrapolated)",
         "sample": (f"one tuning step of the 7B block: oracle fake-quant forward + gradient of all 7 "
                    f"layers (NumPy float32, 1 thread, timed on 1/{div} of the rows and scaled) "
                    f"{t_fq_fwd + t_fq_bwd:.2f} s; oracle block "
                    f"forward + backward (PyTorch float32, {threads} threads) on {sample_tokens} tokens "
-                   f"{t_fwd + t_bwd:.2f} s, scaled linearly to {tokens_per_batch} tokens per batch; "
-                   f"x {args.iters} steps + {passes} forward passes"),
-        "cpu": _cpu_model(),
+                   f"{t_fwd + t_bwd:.2f} s, scaled linearly to {tokens_per_batch} tokens per batch "
+                   f"(attention's quadratic term undercounted); x {args.iters} steps + {passes} forward "
+                   f"passes"),
     }
+    print("bench: cpu baseline, SmolLM2-shaped block tune", file=sys.stderr, flush=True)
+    secs, initial, final = smollm2_cpu_tune(torch, threads)
+    print("bench: cpu baseline, microbench kernels", file=sys.stderr, flush=True)
+    kern = cpu_kernels(torch)
+    return {
+        "value": round(secs, 2),
+        "unit": "s per SmolLM2-135M-shaped block tune (measured)",
+        "cores": threads,
+        "kind": "port",
+        "sample": ("the whole 200-step tune of one SmolLM2-135M-shaped block (hidden 576, 9/3 heads x 64, "
+                   "SwiGLU 1536; 8 x 512 tokens, 4-bit asym gs64, lr 5e-3): targets, score, 200 steps, "
+                   f"score, in float32 on {threads} host threads (PyTorch block, NumPy fake quantization "
+                   "and straight-through gradient)"),
+        "loss": {"initial": initial, "final": final},
+        "cpu": _cpu_model(),
+        "kernels_18944x3584_2bit_gs64": kern,
+        "kernels_note": ("NumPy float32 on one thread, median of 3 over a quarter of the rows, scaled; GB/s "
+                         "over the algorithmic bytes of the GPU figures"),
+        "extrapolated_7b_block": extrapolated,
+    }
+
+
+# The SmolLM2-135M-shaped block workload, the one the CPU path runs in full:
+# hidden 576, 9 / 3 heads x 64, SwiGLU 1536, RMSNorm eps 1e-5, RoPE theta 1e4,
+# no biases, fp32 weights N(0, 0.02) (seed 0); 8 x 512 hidden states N(0, 1)
+# (seed 1) with channels 7, 111, 333, 500 x20; 4-bit asymmetric gs64, 200
+# steps at lr 5e-3, batch 8 (one batch, no outlier rule at 4 bits).
+SHAPE_135M = dict(hidden=576, n_heads=9, n_kv_heads=3, head_dim=64, intermediate=1536, norm_eps=1e-5,
+                  rope_theta=1e4)
+SMOL_B, SMOL_S, SMOL_LR, SMOL_BITS = 8, 512, 5e-3, 4
+
+
+def smollm2_workload(torch):
+    from mround_amd.pipeline.block import BlockShape, BlockWeights
+
+    shape = BlockShape(**SHAPE_135M)
+    w = BlockWeights.random(shape, dtype=torch.float32, device="cpu", seed=0, std=0.02)
+    x = torch.randn(SMOL_B, SMOL_S, shape.hidden, generator=torch.Generator().manual_seed(1))
+    x[..., [7, 111, 333, 500]] *= 20.0
+    return shape, w, x
+
+
+def smollm2_gpu_tune(torch, dev, reps=3):
+    """The SmolLM2-shaped block tune on the GPU (targets from the original
+    block, then score, 200 steps, score, commit), seconds (median of reps)."""
+    from mround_amd.pipeline.block import BlockEngine, BlockWeights
+    from mround_amd.pipeline.runner import DecoderBlock, QuantizationRunner
+    from mround_amd.schemes import QuantScheme, Symmetry, TuningConfig
+
+    shape, w, x = smollm2_workload(torch)
+    wd = BlockWeights({n: t.to(dev) for n, t in w.linears.items()}, {}, w.input_norm.to(dev),
+                      w.post_norm.to(dev))
+    xd = x.reshape(SMOL_B * SMOL_S, -1).to(dev)
+    eng = BlockEngine(shape, batch=SMOL_B, seq_len=SMOL_S, device=dev)
+    eng.set_block(wd)
+    eng.load_dense(wd.linears)
+    target = torch.empty_like(xd)
+    eng.forward(xd, target, save=False)
+    scheme = QuantScheme(bits=SMOL_BITS, group_size=GROUP, symmetry=Symmetry.ASYMMETRIC)
+    tuning = TuningConfig(iters=200, batch_size=SMOL_B, n_samples=SMOL_B, seq_len=SMOL_S, lr=SMOL_LR)
+    runner = QuantizationRunner(scheme, tuning)
+    times = []
+    for _ in range(reps + 1):
+        block = DecoderBlock(0, "model.layers.0", shape, BlockWeights(dict(wd.linears), {}, wd.input_norm,
+                                                                      wd.post_norm))
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        runner.quantize_block(block, [xd], [target], path_prefix=block.name)
+        torch.cuda.synchronize(dev)
+        times.append(time.perf_counter() - t0)
+    return sorted(times[1:])[len(times[1:]) // 2]
+
+
+def smollm2_cpu_tune(torch, threads):
+    """The same tune on the host in float32: the oracle's block (PyTorch, all
+    threads) under the oracle's NumPy fake quantization and straight-through
+    gradient, the sign step and projection; targets, score, 200 steps, score.
+    Returns (seconds, initial loss, final loss)."""
+    import numpy as np
+
+    from oracle import block as OB
+    from oracle import quantize as OQ
+
+    torch.set_num_threads(threads)
+    shape, w, x = smollm2_workload(torch)
+    oshape = OB.Shape(**SHAPE_135M)
+    lin = {n: w.linears[n].float() for n in OB.LAYERS}
+    norms = (w.input_norm.float(), w.post_norm.float())
+
+    class FQ(torch.autograd.Function):  # float32 W' with the reference's STE gradient
+        @staticmethod
+        def forward(ctx, v, a, b, w_np):
+            q = OQ.fake_quantize(w_np, v.numpy(), a.numpy(), b.numpy(), bits=SMOL_BITS, group_size=GROUP,
+                                 mode="asym")[0]
+            ctx.save_for_backward(v, a, b)
+            ctx.w_np = w_np
+            return torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32))
+
+        @staticmethod
+        def backward(ctx, g):
+            v, a, b = ctx.saved_tensors
+            gv, ga, gb = OQ.quantize_grad(ctx.w_np, v.numpy(), a.numpy(), b.numpy(), g.numpy(),
+                                          bits=SMOL_BITS, group_size=GROUP, mode="asym")
+            t = lambda arr, like: torch.from_numpy(np.ascontiguousarray(arr, dtype=np.float32)).reshape(like.shape)
+            return t(gv, v), t(ga, a), t(gb, b), None
+
+    t0 = time.perf_counter()
+    w_np = {n: t.numpy() for n, t in lin.items()}
+    with torch.no_grad():
+        target = OB.block_forward(x, lin, {}, norms, oshape)
+    params = OB.init_params(lin, OB.Scheme(SMOL_BITS, GROUP))
+
+    def loss_at(prm, grad):
+        leaf = {n: tuple(t.clone().requires_grad_(grad) for t in p) for n, p in prm.items()}
+        wq = {n: FQ.apply(*leaf[n], w_np[n]) for n in OB.LAYERS}
+        loss = ((OB.block_forward(x, wq, {}, norms, oshape) - target) ** 2).mean()
+        return loss, leaf
+
+    with torch.no_grad():
+        initial = float(loss_at(params, False)[0])
+    for step in range(200):
+        loss, leaf = loss_at(params, True)
+        loss.backward()
+        rate = SMOL_LR * (1.0 - step / 200)
+        new = {}
+        for n, p in leaf.items():
+            stepped = [OQ.sign_step(t.detach().numpy(), t.grad.numpy(), rate) for t in p]
+            new[n] = tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in OQ.project_params(*stepped, "asym"))
+        params = new
+    with torch.no_grad():
+        final = float(loss_at(params, False)[0])
+    return time.perf_counter() - t0, initial, final
+
+
+def cpu_kernels(torch, sample_div=4, reps=3):
+    """The microbench kernels on the host (NumPy float32, one thread) at 2-bit
+    gs64: fake-quant forward, straight-through gradient + sign step, packing;
+    median of reps over the matrix's first rows / sample_div, scaled to the
+    matrix, with the same algorithmic bytes the GPU figures use."""
+    import numpy as np
+
+    from oracle import packing as OP
+    from oracle import quantize as OQ
+
+    rows = ROWS // sample_div
+    gen = np.random.default_rng(0)
+    w = (gen.standard_normal((rows, COLS), dtype=np.float32) * 0.02)
+    v = gen.random((rows, COLS), dtype=np.float32) - 0.5
+    g = gen.standard_normal((rows, COLS), dtype=np.float32)
+    ones = np.ones((rows, COLS // GROUP), np.float32)
+
+    def med(fn):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[reps // 2] * sample_div
+
+    out = {}
+    codes = None
+
+    def fwd():
+        nonlocal codes
+        codes = OQ.fake_quantize(w, v, ones, ones, bits=BITS, group_size=GROUP, mode="asym")[1]
+
+    def bwd():
+        gv, ga, gb = OQ.quantize_grad(w, v, ones, ones, g, bits=BITS, group_size=GROUP, mode="asym")
+        OQ.project_params(OQ.sign_step(v.reshape(gv.shape), gv, 0.005), OQ.sign_step(ones, ga.reshape(ones.shape), 0.005),
+                          OQ.sign_step(ones, gb.reshape(ones.shape), 0.005), "asym")
+
+    out["fwd"] = med(fwd)
+    out["bwd_update"] = med(bwd)
+    flat = codes.reshape(rows, COLS).astype(np.int64)
+    out["pack"] = med(lambda: OP.pack_codes(flat, BITS))
+    n, ng = ROWS * COLS, ROWS * COLS // GROUP
+    nbytes = {"fwd": n * 8 + 8 * ng, "bwd_update": n * 14 + 16 * ng, "pack": n * (1 + BITS / 8)}
+    return {k: {"s": round(t, 3), "gbps": round(nbytes[k] / t / 1e9, 2)} for k, t in out.items()}
 
 
 def _measured_traffic():
@@ -333,12 +513,15 @@ def _cpu_model():
 
 
 def profile_kernels(torch, K, dev, steps):
-    """Launch, ``steps`` times each, the kernels whose HBM traffic the counter
-    runs measure: the 7B block's gate/up GEMM with the SwiGLU epilogue, its
-    weight-gradient and input-gradient GEMMs, the down projection, the
-    fake-quant forward of the microbench, and a 1 GiB copy that calibrates the
-    counters (read and written bytes are known exactly)."""
+    """Launch, ``steps`` times each, the kernels the counter runs measure: the
+    7B block's gate/up GEMM with the SwiGLU epilogue, its weight-gradient and
+    input-gradient GEMMs, the down projection, the attention-output
+    projection, the SwiGLU-backward GEMM, the attention-output weight
+    gradient, the fake-quant forward of the microbench, and a 1 GiB copy that
+    calibrates the traffic counters (read and written bytes are known
+    exactly)."""
     T, h, mlp = 16384, SHAPE_7B["hidden"], SHAPE_7B["intermediate"]
+    hq_d = SHAPE_7B["n_heads"] * SHAPE_7B["head_dim"]
     g = torch.Generator(device=dev).manual_seed(0)
     rnd = lambda *s: (torch.randn(*s, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     x, wgu, wd = rnd(T, h), rnd(2 * mlp, h), rnd(h, mlp)
@@ -347,15 +530,23 @@ def profile_kernels(torch, K, dev, steps):
     dgu, dw = rnd(T, 2 * mlp), torch.empty(2 * mlp, h, device=dev)
     dx = torch.empty(T, h, device=dev)
     out = torch.empty(T, h, device=dev)
+    attn, wo, dh = rnd(T, hq_d), rnd(h, hq_d), rnd(T, h)
+    dwo = torch.empty(h, hq_d, device=dev)
+    ws = torch.empty(max(K.gemm_workspace_bytes(*mnk) for mnk in ((2 * mlp, h, T), (T, h, 2 * mlp),
+                                                                   (T, h, mlp), (h, hq_d, T))),
+                     dtype=torch.uint8, device=dev)
     w, v, a, b, _ = fq_inputs(torch, dev, GROUP)
     wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(steps):
-        K.gemm_swiglu(x, wgu, act, gu)                                   # gemm_gate_up
-        K.gemm("tn", dgu, x, dw, M=2 * mlp, N=h, K=T)                    # gemm_dw_gate_up
-        K.gemm("nn", dgu, wgu, dx, M=T, N=h, K=2 * mlp)                  # gemm_dx_gate_up
-        K.gemm("nt", act, wd, out, M=T, N=h, K=mlp, resid=dx)            # gemm_down
+        K.gemm_swiglu(x, wgu, act, gu, workspace=ws)                               # gemm_gate_up
+        K.gemm("tn", dgu, x, dw, M=2 * mlp, N=h, K=T, workspace=ws)                # gemm_dw_gate_up
+        K.gemm("nn", dgu, wgu, dx, M=T, N=h, K=2 * mlp, workspace=ws)              # gemm_dx_gate_up
+        K.gemm("nt", act, wd, out, M=T, N=h, K=mlp, resid=dx, workspace=ws)        # gemm_down
+        K.gemm("nt", attn, wo, out, M=T, N=h, K=hq_d, resid=dx, workspace=ws)      # gemm_o
+        K.gemm_swiglu_bwd(x, wd, gu, dgu, workspace=ws)                            # gemm_dact
+        K.gemm("tn", dh, attn, dwo, M=h, N=hq_d, K=T, workspace=ws)                # gemm_dw_o
         K.fq_forward(w, v, a, b, bits=BITS, group_size=GROUP, mode="asym", eps=1e-8, wq_out=wq)
         K.copy_bytes(src, dst, src.numel())
     torch.cuda.synchronize(dev)
@@ -440,6 +631,9 @@ def main(argv=None):
     if not args.no_cpu_baseline:
         print("bench: cpu baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(args, tune["tokens_per_batch"], tune["batches"])
+        print("bench: the same SmolLM2-shaped block tune on the GPU", file=sys.stderr, flush=True)
+        cpu["gpu_same_workload_s"] = round(smollm2_gpu_tune(torch, dev), 4)
+        cpu["gpu_speedup"] = round(cpu["value"] / cpu["gpu_same_workload_s"], 1)
     line = {
         "metric": "sec per decoder-block tune (7B shape, 2-bit); fake-quant HBM GB/s",
         "value": round(sec, 3),

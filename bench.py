@@ -24,7 +24,8 @@ Printed as one JSON line:
              events around every launch of the warm-up tunes;
   fake_quant the kernel microbench: a bf16 18944 x 3584 weight (0.1 % of
              entries x10), 2-bit gs64; forward, backward + update, the update
-             that also writes the next W', and packing, against 8 TB/s;
+             that also writes the next W', packing, and the fused quantize +
+             pack of the export, against 8 TB/s;
   cpu_baseline  the CPU path measured on the host's cores: the whole 200-step
              tune of one SmolLM2-135M-shaped block (8 x 512 tokens, 4-bit) in
              float32 (the oracle's PyTorch block under its NumPy fake
@@ -188,6 +189,12 @@ def pack_bytes(n, bits):
     return n * (1 + bits / 8)
 
 
+def quantize_pack_bytes(n, gs, bits):
+    """The fused quantize + pack: bf16 weight and fp32 v in, packed words out per
+    weight; alpha, beta in and bf16 scales, biases out per group."""
+    return n * (6 + bits / 8) + (n // gs) * 12
+
+
 def fake_quant_microbench(torch, K, dev, bits, gs, steps):
     """Average launch duration of each kernel: ``steps`` back-to-back launches
     between two HIP events on the launch stream."""
@@ -198,6 +205,8 @@ def fake_quant_microbench(torch, K, dev, bits, gs, steps):
     scale = torch.empty(ROWS, COLS // gs, dtype=torch.float32, device=dev)
     zp = torch.empty_like(scale)
     packed = torch.empty(ROWS, K.packed_width(COLS, bits), dtype=torch.uint32, device=dev)
+    qp_scales = torch.empty(ROWS, COLS // gs, dtype=torch.bfloat16, device=dev)
+    qp_biases = torch.empty_like(qp_scales)
     fns = {
         "fwd": lambda: K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8,
                                     wq_out=wq),
@@ -211,6 +220,8 @@ def fake_quant_microbench(torch, K, dev, bits, gs, steps):
         "codes": lambda: K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8,
                                       codes_out=codes, scale_out=scale, zp_out=zp),
         "pack": lambda: K.pack_codes(codes, bits, signed=False, offset=0, packed_out=packed),
+        "quantize_pack": lambda: K.quantize_pack(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8,
+                                                 packed_out=packed, scales_out=qp_scales, biases_out=qp_biases),
     }
     for fn in fns.values():
         fn()
@@ -226,7 +237,8 @@ def fake_quant_microbench(torch, K, dev, bits, gs, steps):
         e.synchronize()
         out[name] = s.elapsed_time(e) / steps
     nbytes = {"fwd": fwd_bytes(n, gs), "bwd_update": bwd_bytes(n, gs),
-              "step_requant": step_requant_bytes(n, gs), "pack": pack_bytes(n, bits)}
+              "step_requant": step_requant_bytes(n, gs), "pack": pack_bytes(n, bits),
+              "quantize_pack": quantize_pack_bytes(n, gs, bits)}
     return {
         "workload": f"{ROWS}x{COLS} bf16 weight, {bits}-bit asym gs{gs}",
         **{k: {"ms": round(out[k], 5), "bytes": nbytes[k],

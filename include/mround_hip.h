@@ -152,6 +152,24 @@ int mr_pack_codes(const void* codes, int codes_signed, int code_offset, int64_t 
                   int64_t cols, int bits, uint32_t* packed_out, int32_t* range_out,
                   void* stream);
 
+/*
+ * Quantize and pack in one pass, for export: the codes of mr_fq_forward (same
+ * arguments, same arithmetic) packed into MLX uint32 words as mr_pack_codes
+ * packs them (symmetric codes offset by 2^(bits-1)), and the MLX metadata of
+ * mr_to_affine, without the one-byte codes in between. Replaces
+ * _tensors_for_layer's quantize -> pack_codes -> to_affine chain
+ * (mround/formats/mlx_export.py:198-235) and the round-to-nearest export of
+ * the remainder (mround/api.py:1877-1937).
+ *   w            (rows, cols) bf16 or fp32, 16-byte aligned
+ *   packed_out   (rows, cols * bits / 32) uint32
+ *   scales_out, biases_out  (rows, cols / group_size) in out_dtype
+ * group_size a power of two >= 32 dividing cols; cols a multiple of 32.
+ */
+int mr_quantize_pack(const void* w, int w_dtype, const float* v, const float* alpha, const float* beta,
+                     const float* init_scale, int64_t rows, int64_t cols, int group_size, int bits,
+                     int mode, float eps, uint32_t* packed_out, void* scales_out, void* biases_out,
+                     int out_dtype, void* stream);
+
 /* Words per row, or MR_EINVAL (mround/formats/packing.py:84-116). */
 int64_t mr_packed_width(int64_t cols, int bits);
 

@@ -26,7 +26,7 @@ from typing import Any
 
 import torch
 
-from mround_amd.core.quantizer import quantize_codes
+from mround_amd.core.quantizer import quantize_codes, quantize_pack
 from mround_amd.core.scale_search import search_scales
 from mround_amd.exceptions import (ArchitectureError, CalibrationError, SchemeError,
                                    UnsupportedSchemeError)
@@ -353,9 +353,21 @@ def _round_to_nearest(model: DecoderModel, scheme: QuantScheme, *, dense: bool):
             skipped.append((path, "dense by request, to match a reference's coverage"))
             continue
         init = search_scales(w, scheme) if scheme.scale_init is ScaleInit.SEARCHED else None
-        codes, scale, zp = quantize_codes(w, None, scheme, init_scale=init, narrow=True)
-        out[path] = QuantizedLayer(narrow_codes(codes, scheme), scale, zp, scheme)
+        out[path] = _rtn_layer(w, scheme, init, model.dtype)
     return out, skipped
+
+
+def _rtn_layer(w: torch.Tensor, scheme: QuantScheme, init_scale, dtype: torch.dtype) -> QuantizedLayer:
+    """A layer at round to nearest, straight into MLX's words, scales and biases
+    in the checkpoint dtype (``mr_quantize_pack``) where the group size allows;
+    otherwise as codes, packed at export."""
+    rows, cols = w.shape
+    gs = scheme.group_size
+    if gs >= 32 and gs & (gs - 1) == 0 and cols % gs == 0 and w.dtype in (torch.bfloat16, torch.float32):
+        return QuantizedLayer(None, None, None, scheme, packed=quantize_pack(w, None, scheme, init_scale=init_scale,
+                                                                             dtype=dtype))
+    codes, scale, zp = quantize_codes(w, None, scheme, init_scale=init_scale, narrow=True)
+    return QuantizedLayer(narrow_codes(codes, scheme), scale, zp, scheme)
 
 
 def _storage(model: DecoderModel, quantized: Mapping[str, QuantizedLayer]) -> Storage:
@@ -367,7 +379,7 @@ def _storage(model: DecoderModel, quantized: Mapping[str, QuantizedLayer]) -> St
         params += n
         if name.endswith(".weight") and path in quantized:
             layer = quantized[path]
-            groups = layer.scale.numel()
+            groups = layer.groups
             total += n * layer.scheme.bits + 2 * groups * dtype_bits
         else:
             total += n * dtype_bits
@@ -618,8 +630,7 @@ def quantize_round_to_nearest(model: str | Path, *, output_dir: str | Path, bits
             if group_size != -1 and w.shape[-1] % group_size:
                 skipped.append((path, f"last dimension {w.shape[-1]} is not a multiple of {group_size}"))
                 continue
-            codes, scale, zp = quantize_codes(w, None, scheme, narrow=True)
-            quantized[path] = QuantizedLayer(narrow_codes(codes, scheme), scale, zp, scheme)
+            quantized[path] = _rtn_layer(w, scheme, None, m.dtype)
     remainder, rem_skipped = _round_to_nearest(m, scheme, dense=dense_remainder)
     quantized.update(remainder)
     skipped.extend(rem_skipped)

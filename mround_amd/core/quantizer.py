@@ -174,6 +174,34 @@ def quantize_codes(
     return codes, scale, zp
 
 
+def quantize_pack(
+    weight: torch.Tensor,
+    params: Mapping[str, torch.Tensor] | None,
+    scheme: QuantScheme,
+    *,
+    eps: float = DEFAULT_EPS_FP32,
+    init_scale: torch.Tensor | None = None,
+    dtype: torch.dtype = torch.bfloat16,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(packed, scales, biases)`` in MLX's layout, in one pass over the weight:
+    the packed codes of :func:`quantize_codes` (``mround/formats/packing.py:119-163``)
+    and the affine metadata of ``to_affine`` (``mround/formats/mlx_export.py:159-195``)
+    in ``dtype``, with no one-byte codes in between. The group size must be a
+    power of two of at least 32 that divides the row."""
+    _check_weight(weight)
+    _check_init_scale(scheme, init_scale)
+    rows, cols, gs, ng = _geometry(weight, scheme)
+    v, alpha, beta = _unpack(params, rows, ng, gs)
+    dev = weight.device
+    packed = torch.empty((rows, cols * scheme.bits // 32), dtype=torch.uint32, device=dev)
+    scales = torch.empty((rows, ng), dtype=dtype, device=dev)
+    biases = torch.empty((rows, ng), dtype=dtype, device=dev)
+    K.quantize_pack(weight.contiguous(), v, alpha, beta, bits=scheme.bits, group_size=scheme.group_size,
+                    mode=mode_of(scheme), eps=eps, init_scale=_init_scale_arg(init_scale, rows, ng),
+                    packed_out=packed, scales_out=scales, biases_out=biases)
+    return packed, scales, biases
+
+
 def dequantize(codes, scale, zero_point, shape: tuple[int, int], scheme: QuantScheme) -> torch.Tensor:
     """``mround/core/quantizer.py:401-411``."""
     c = codes.to(torch.float32)

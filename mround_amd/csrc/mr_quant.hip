@@ -233,6 +233,94 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
   }
 }
 
+// Quantize and pack in one pass: the forward's codes go straight into MLX
+// uint32 words (element 0 in the low bits; 3/5/6/7-bit codes straddle words),
+// with the group's MLX scale and bias (scales = out(s), biases =
+// out(-scales * out(zp)), zp = 2^(bits-1) for the symmetric modes) from the
+// group leader. Four consecutive lanes hold 32 codes, which fill exactly
+// `bits` words: each lane shifts its 8 codes (8 * bits stream bits, at most 64)
+// into place in every word they touch, the four lanes OR their words together
+// by two xor-shuffles, and lane r of the four stores words r and r + 4.
+// Needs cols % 32 == 0 (every 32-code run lies in one row and one group).
+template <int WT, int OT, int MODE, bool HAS_V, int TPG>
+__global__ __launch_bounds__(kBlock) void fq_pack_fast(
+    const void* __restrict__ w, const float* __restrict__ v, const float* __restrict__ alpha,
+    const float* __restrict__ beta, const float* __restrict__ init_scale, uint32_t* __restrict__ packed,
+    void* __restrict__ scales, void* __restrict__ biases, int64_t n_chunks, int tpg, int tpg_shift,
+    int bits, float maxq, float qmin, float qmax, float eps) {
+  int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const bool active = chunk < n_chunks;
+  if (!active) chunk = n_chunks - 1;  // whole groups of inactive lanes stay for the shuffles
+  const int64_t grp = chunk >> tpg_shift;
+  const int64_t e = chunk * 8;
+
+  float x[8];
+  load8<WT>(w, e, x);
+  float mx = x[0], mn = x[0];
+#pragma unroll
+  for (int k = 1; k < 8; ++k) {
+    mx = fmaxf(mx, x[k]);
+    mn = fminf(mn, x[k]);
+  }
+  if constexpr (MODE != MR_SYM_SEARCHED) {
+    mx = gmax<TPG>(mx, tpg);
+    mn = gmin<TPG>(mn, tpg);
+  }
+  float a = 1.0f, b = 1.0f, base = 0.0f;
+  if constexpr (HAS_V) {
+    a = alpha[grp];
+    b = beta[grp];
+  }
+  if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+  float vv[8];
+  if constexpr (HAS_V) {
+    load8_f32(v, e, vv);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) vv[k] = 0.0f;
+  }
+  // stored (unsigned) codes: the symmetric ones offset by 2^(bits-1)
+  const uint32_t off = MODE == MR_ASYM ? 0u : static_cast<uint32_t>(maxq);
+  uint64_t stream = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float c, in;
+    quant_one<MODE, HAS_V>(x[k], vv[k], p, qmin, qmax, c, in);
+    const uint32_t u = static_cast<uint32_t>(static_cast<int>(c) + static_cast<int>(off));
+    stream |= static_cast<uint64_t>(u) << (k * bits);
+  }
+  const int r = static_cast<int>(chunk & 3);
+  const int start = 8 * r * bits;  // this lane's first bit in the 32-code run
+  uint32_t word[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int sh = start - 32 * q;  // where the lane's bits start relative to word q
+    uint32_t part = 0;
+    if (q < bits) {
+      if (sh >= 0) part = sh < 32 ? static_cast<uint32_t>(stream << sh) : 0u;
+      else part = -sh < 64 ? static_cast<uint32_t>(stream >> (-sh)) : 0u;
+    }
+    part |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(part), 1, 64));
+    part |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(part), 2, 64));
+    word[q] = part;
+  }
+  if (!active) return;
+  uint32_t* dst = packed + (e >> 5) * bits;
+  if (r < bits) dst[r] = word[r];
+  if (r + 4 < bits) dst[r + 4] = word[r + 4];
+  if ((chunk & (tpg - 1)) == 0) {
+    store_elem<OT>(scales, grp, p.s);
+    const float sq = load_elem<OT>(scales, grp);
+    float z = maxq;  // symmetric: the stored code offset
+    if constexpr (MODE == MR_ASYM) {
+      store_elem<OT>(biases, grp, p.zp);
+      z = load_elem<OT>(biases, grp);
+    }
+    store_elem<OT>(biases, grp, -sq * z);
+  }
+}
+
 __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
   if (dt == MR_F32) return load_elem<MR_F32>(p, i);
   if (dt == MR_BF16) return load_elem<MR_BF16>(p, i);
@@ -657,10 +745,84 @@ int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, f
   return MR_OK;
 }
 
+template <int MODE, bool HAS_V>
+int launch_pack(const Shape& sh, const void* w, int wt, const float* v, const float* alpha,
+                const float* beta, const float* init_scale, uint32_t* packed, void* scales, void* biases,
+                int ot, int bits, float eps, hipStream_t stream) {
+  const int64_t n_chunks = sh.rows * sh.cols / 8;
+  const int64_t blocks = (n_chunks + kBlock - 1) / kBlock;
+  if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_quantize_pack: tensor too large");
+#define MR_PACK_T(WT_, OT_, T_)                                                                    \
+  hipLaunchKernelGGL((fq_pack_fast<WT_, OT_, MODE, HAS_V, T_>), dim3(static_cast<unsigned>(blocks)), \
+                     dim3(kBlock), 0, stream, w, v, alpha, beta, init_scale, packed, scales, biases,   \
+                     n_chunks, sh.tpg, sh.tpg_shift, bits, sh.maxq, sh.qmin, sh.qmax, eps)
+#define MR_PACK_W(WT_, OT_)                             \
+  do {                                                  \
+    if (sh.tpg == 8) MR_PACK_T(WT_, OT_, 8);            \
+    else if (sh.tpg == 4) MR_PACK_T(WT_, OT_, 4);       \
+    else if (sh.tpg == 16) MR_PACK_T(WT_, OT_, 16);     \
+    else MR_PACK_T(WT_, OT_, 0);                        \
+  } while (0)
+#define MR_PACK_O(WT_)                                   \
+  do {                                                   \
+    if (ot == MR_BF16) MR_PACK_W(WT_, MR_BF16);          \
+    else if (ot == MR_F16) MR_PACK_W(WT_, MR_F16);       \
+    else MR_PACK_W(WT_, MR_F32);                         \
+  } while (0)
+  if (wt == MR_BF16) MR_PACK_O(MR_BF16);
+  else MR_PACK_O(MR_F32);
+#undef MR_PACK_O
+#undef MR_PACK_W
+#undef MR_PACK_T
+  MR_LAUNCH_CHECK("mr_quantize_pack");
+  return MR_OK;
+}
+
 }  // namespace
 }  // namespace mr
 
 extern "C" {
+
+int mr_quantize_pack(const void* w, int w_dtype, const float* v, const float* alpha, const float* beta,
+                     const float* init_scale, int64_t rows, int64_t cols, int group_size, int bits,
+                     int mode, float eps, uint32_t* packed_out, void* scales_out, void* biases_out,
+                     int out_dtype, void* stream) {
+  using namespace mr;
+  const char* fn = "mr_quantize_pack";
+  clear_error();
+  Shape sh;
+  int rc = check_common(fn, w, w_dtype, rows, cols, group_size, bits, mode, init_scale, sh);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return MR_OK;
+  const bool any_v = v || alpha || beta;
+  if (any_v && !(v && alpha && beta))
+    return fail(MR_EINVAL, "%s: v, alpha and beta are given together or not at all", fn);
+  if (!packed_out || !scales_out || !biases_out) return fail(MR_EINVAL, "%s: null output", fn);
+  if (!valid_dtype(out_dtype)) return fail(MR_EINVAL, "%s: unknown output dtype %d", fn, out_dtype);
+  if (w_dtype != MR_BF16 && w_dtype != MR_F32) return fail(MR_EINVAL, "%s: the weight must be bf16 or fp32", fn);
+  if (group_size < 32 || !sh.fast || cols % 32)
+    return fail(MR_EINVAL, "%s: needs a power-of-two group size of at least 32 dividing the row, and rows "
+                "of whole 32-code runs (got group_size %d, cols %lld)", fn, group_size,
+                static_cast<long long>(cols));
+  if (!aligned16(w) || (v && !aligned16(v)) || (reinterpret_cast<uintptr_t>(packed_out) & 3u))
+    return fail(MR_EINVAL, "%s: the weight and v must be 16-byte aligned and the words 4-byte aligned", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* pk = packed_out;
+  if (mode == MR_ASYM)
+    return any_v ? launch_pack<MR_ASYM, true>(sh, w, w_dtype, v, alpha, beta, init_scale, pk, scales_out,
+                                              biases_out, out_dtype, bits, eps, s)
+                 : launch_pack<MR_ASYM, false>(sh, w, w_dtype, v, alpha, beta, init_scale, pk, scales_out,
+                                               biases_out, out_dtype, bits, eps, s);
+  if (mode == MR_SYM)
+    return any_v ? launch_pack<MR_SYM, true>(sh, w, w_dtype, v, alpha, beta, init_scale, pk, scales_out,
+                                             biases_out, out_dtype, bits, eps, s)
+                 : launch_pack<MR_SYM, false>(sh, w, w_dtype, v, alpha, beta, init_scale, pk, scales_out,
+                                              biases_out, out_dtype, bits, eps, s);
+  return any_v ? launch_pack<MR_SYM_SEARCHED, true>(sh, w, w_dtype, v, alpha, beta, init_scale, pk,
+                                                    scales_out, biases_out, out_dtype, bits, eps, s)
+               : launch_pack<MR_SYM_SEARCHED, false>(sh, w, w_dtype, v, alpha, beta, init_scale, pk,
+                                                     scales_out, biases_out, out_dtype, bits, eps, s);
+}
 
 static int fq_forward_impl(const char* fn, const void* w, int w_dtype, const float* v,
                            const float* alpha, const float* beta, const float* init_scale,

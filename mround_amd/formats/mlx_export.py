@@ -52,12 +52,22 @@ _DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torc
 
 @dataclasses.dataclass(frozen=True)
 class QuantizedLayer:
-    """One layer's codes, scale, zero point and scheme (``mlx_export.py:89-106``)."""
+    """One layer's codes, scale, zero point and scheme (``mlx_export.py:89-106``).
 
-    codes: torch.Tensor
-    scale: torch.Tensor
+    ``packed`` optionally holds the layer already in MLX's layout (uint32 words,
+    scales, biases; ``mround_amd.core.quantizer.quantize_pack``), written as is
+    when its dtype is the checkpoint's; ``codes``, ``scale`` and
+    ``zero_point`` may then be ``None``."""
+
+    codes: torch.Tensor | None
+    scale: torch.Tensor | None
     zero_point: torch.Tensor | None
     scheme: QuantScheme
+    packed: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
+
+    @property
+    def groups(self) -> int:
+        return self.scale.numel() if self.scale is not None else self.packed[1].numel()
 
 
 def narrow_codes(codes: torch.Tensor, scheme: QuantScheme) -> torch.Tensor:
@@ -106,6 +116,12 @@ def _tensors_for_layer(path: str, layer: QuantizedLayer, dtype: torch.dtype) -> 
     """Packed weight, scales and biases under MLX's names (``mlx_export.py:198-235``)."""
     scheme = layer.scheme
     _require_mlx_representable(path, scheme)
+    if layer.packed is not None and (layer.packed[1].dtype == dtype or layer.codes is None):
+        packed, scales, biases = layer.packed
+        if scales.dtype != dtype:
+            msg = f"{path}: packed with {scales.dtype} metadata, the checkpoint is {dtype}"
+            raise ExportError(msg)
+        return {f"{path}.weight": packed, f"{path}.scales": scales, f"{path}.biases": biases}
     if layer.codes.ndim != GROUPED_NDIM:
         msg = (f"{path}: expected grouped codes shaped (out_features, n_groups, group_size), "
                f"got {tuple(layer.codes.shape)}")

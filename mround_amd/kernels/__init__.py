@@ -39,6 +39,7 @@ __all__ = [
     "loss_workspace",
     "pack_codes",
     "packed_width",
+    "quantize_pack",
     "to_affine",
     "unpack_codes",
 ]
@@ -65,6 +66,7 @@ _SIGNATURES = {
     "mr_fq_backward_signsgd": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _I, _F, _I, _F,
                                     _F, _F, _F, _P, _P, _P, _P]),
     "mr_pack_codes": (_I, [_P, _I, _I, _L, _L, _I, _P, _P, _P]),
+    "mr_quantize_pack": (_I, [_P, _I, _P, _P, _P, _P, _L, _L, _I, _I, _I, _F, _P, _P, _P, _I, _P]),
     "mr_packed_width": (_L, [_L, _I]),
     "mr_unpack_codes": (_I, [_P, _L, _L, _I, _P, _P]),
     "mr_to_affine": (_I, [_P, _P, _L, _I, _I, _P, _P, _P]),
@@ -211,6 +213,20 @@ def pack_codes(codes, bits: int, *, signed: bool, offset: int, packed_out, range
     rc = lib().mr_pack_codes(_ptr(codes), int(signed), offset, rows, cols, bits, _ptr(packed_out),
                              _ptr(range_out), _stream(codes))
     _check(rc, "mr_pack_codes")
+
+
+def quantize_pack(weight, v, alpha, beta, *, bits, group_size, mode, eps, packed_out, scales_out,
+                  biases_out, init_scale=None) -> None:
+    """``mr_quantize_pack``: MLX words, scales and biases straight from the weight."""
+    rows, cols = weight.shape
+    if scales_out.dtype != biases_out.dtype:
+        raise KernelError("scales and biases share one dtype")
+    rc = lib().mr_quantize_pack(
+        _ptr(weight), dtype_code(weight.dtype), _ptr(_f32(v, "v")), _ptr(_f32(alpha, "alpha")),
+        _ptr(_f32(beta, "beta")), _ptr(_f32(init_scale, "init_scale")), rows, cols, group_size, bits,
+        MODE[mode], eps, _ptr(packed_out), _ptr(scales_out), _ptr(biases_out), dtype_code(scales_out.dtype),
+        _stream(weight))
+    _check(rc, "mr_quantize_pack")
 
 
 def unpack_codes(packed, rows: int, cols: int, bits: int, codes_out) -> None:

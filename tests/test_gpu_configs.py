@@ -5,7 +5,7 @@
   dL/dW' N(0, 1) fp32 (seed 3), asymmetric, at every bits x group size point
   of the sweep (2/3/4/8 x 32/64/128). On sampled rows, against the float32
   oracle: the forward (W', codes, scale, zero point) and the packed words bit
-  for bit; the fused sign-SGD step (v bit for bit, alpha and beta wherever the
+  for bit, and the fused quantize + pack of the export identical to them; the fused sign-SGD step (v bit for bit, alpha and beta wherever the
   gradient's sign is clear of its summation-order error) and the next W' it
   writes, bit-identical to the oracle forward of the parameters it wrote. The
   step without the W' write leaves the same parameters over the whole matrix.
@@ -35,6 +35,7 @@ import torch
 
 from mround_amd import kernels as K
 from mround_amd.core import quantizer as QZ
+from mround_amd.formats import mlx_export as MX
 from mround_amd.formats import packing as PK
 from mround_amd.pipeline.block import LAYERS, BlockEngine, BlockShape, BlockWeights, placements, unplace
 from mround_amd.pipeline.runner import DecoderBlock, QuantizationRunner
@@ -96,6 +97,13 @@ def test_microbench_matrix(micro, bits, gs):
     packed = PK.pack_codes(codes.view(ROWS, COLS), bits)
     want = OP.pack_codes(ref_c.reshape(len(SEL), COLS).astype(np.int64), bits)
     assert np.array_equal(packed.view(torch.int32).cpu().numpy().view(np.uint32)[SEL], want), "packed words"
+    # the fused quantize + pack of the export: the same words, and the affine metadata, over the whole matrix
+    scheme = QuantScheme(bits=bits, group_size=gs, symmetry=Symmetry.ASYMMETRIC)
+    params = {"v": v.view(ROWS, ng, gs), "alpha": a.view(ROWS, ng, 1), "beta": b.view(ROWS, ng, 1)}
+    words, scl, bia = QZ.quantize_pack(wd, params, scheme, dtype=torch.bfloat16)
+    assert torch.equal(words.view(torch.int32), packed.view(torch.int32)), "fused words"
+    ws_, wb_ = MX.to_affine(scale, zp, scheme, dtype=torch.bfloat16)
+    assert torch.equal(scl, ws_.reshape(ROWS, ng)) and torch.equal(bia, wb_.reshape(ROWS, ng)), "fused metadata"
 
     # the fused step that also writes the next W' (identity placement)
     lr = 0.005

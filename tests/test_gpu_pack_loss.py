@@ -23,6 +23,7 @@ from mround_amd.formats import packing as PK
 from mround_amd.schemes import QuantScheme
 from oracle import losses as OL
 from oracle import packing as OP
+from oracle import quantize as Q
 from oracle import sensitivity as OS
 from tests.helpers import dev, to_np, weight
 
@@ -95,6 +96,65 @@ def test_export_tensors_bit_exact(bits, symmetry, dtype):
     if symmetry == "sym":
         s = tensors["m.q.scales"].float()
         assert torch.all(s * 2 ** (bits - 1) + tensors["m.q.biases"].float() == 0)
+
+
+# ------------------------------------------------------- fused quantize+pack --
+
+QP_SCHEMES = {"asym": dict(symmetry="asym"), "sym": dict(symmetry="sym"),
+              "searched": dict(symmetry="sym", scale_init="searched")}
+
+
+@pytest.mark.parametrize("mode", ["asym", "sym", "searched"])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("learned", [False, True])
+def test_quantize_pack_equals_the_separate_chain(mode, bits, gs, learned):
+    """mr_quantize_pack against quantize_codes -> pack_codes -> to_affine on the
+    same weight and parameters: words, scales and biases identical, in every
+    output dtype."""
+    rows, cols = 40, 512
+    print("case quantize_pack", mode, bits, gs, learned, flush=True, file=sys.stderr)
+    scheme = QuantScheme(bits=bits, group_size=gs, **QP_SCHEMES[mode])
+    w = weight(rows, cols, seed=bits * gs, std=0.05).to(dev())
+    params = None
+    if learned:
+        g = torch.Generator().manual_seed(bits + gs)
+        params = {"v": ((torch.rand(rows, cols // gs, gs, generator=g) - 0.5) * 0.9).to(dev()),
+                  "alpha": (1 - 0.4 * torch.rand(rows, cols // gs, 1, generator=g)).to(dev()),
+                  "beta": (1 - 0.4 * torch.rand(rows, cols // gs, 1, generator=g)).to(dev())}
+    init = None
+    if mode == "searched":
+        init = -(torch.rand(rows, cols // gs, 1, generator=torch.Generator().manual_seed(9)) * 0.01 + 0.002).to(dev())
+    codes, scale, zp = QZ.quantize_codes(w, params, scheme, init_scale=init, narrow=True)
+    off = 0 if mode == "asym" else 2 ** (bits - 1)
+    want_words = PK.pack_codes(codes.reshape(rows, cols), bits, offset=off)
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        words, scales, biases = QZ.quantize_pack(w, params, scheme, init_scale=init, dtype=dtype)
+        assert torch.equal(words.view(torch.int32), want_words.view(torch.int32)), dtype
+        ws, wb = MX.to_affine(scale, zp, scheme, dtype=dtype)
+        assert torch.equal(scales, ws.reshape(rows, -1)) and torch.equal(biases, wb.reshape(rows, -1)), dtype
+
+
+def test_quantize_pack_against_the_oracle():
+    """Round to nearest at 3 bits (words straddle): the oracle's codes packed by
+    the oracle, and the oracle's affine metadata."""
+    rows, cols, gs, bits = 64, 1024, 64, 3
+    w = weight(rows, cols, seed=77)
+    scheme = QuantScheme(bits=bits, group_size=gs, symmetry="asym")
+    words, scales, biases = QZ.quantize_pack(w.to(dev()), None, scheme, dtype=torch.bfloat16)
+    _, c, s, z = Q.fake_quantize(to_np(w), None, None, None, bits=bits, group_size=gs, mode="asym")
+    assert np.array_equal(words.view(torch.int32).cpu().numpy().view(np.uint32),
+                          OP.pack_codes(c.reshape(rows, cols).astype(np.int64), bits))
+    ws, wb = OP.to_affine(s.reshape(rows, -1), z.reshape(rows, -1), bits, "bfloat16")
+    assert np.array_equal(scales.float().cpu().numpy(), ws) and np.array_equal(biases.float().cpu().numpy(), wb)
+
+
+def test_quantize_pack_refuses_what_it_cannot_pack():
+    w = weight(8, 96, seed=1).to(dev())
+    with pytest.raises(Exception, match="power-of-two group size"):
+        QZ.quantize_pack(w, None, QuantScheme(bits=4, group_size=48, symmetry="asym"))
+    with pytest.raises(Exception, match="power-of-two group size"):
+        QZ.quantize_pack(weight(8, 80, seed=1).to(dev()), None, QuantScheme(bits=4, group_size=16, symmetry="asym"))
 
 
 @pytest.mark.parametrize("n", [1000, 4096, 2_359_296, 3 * 1024 + 1])

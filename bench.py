@@ -57,6 +57,8 @@ HBM_PEAK_GBPS = 8000.0
 
 # fake-quant microbench matrix (a 7B gate/up projection)
 ROWS, COLS = 18944, 3584
+# gate/up interleave period of the fused operand (mround_amd.pipeline.block)
+SWIGLU_ROWS = 32
 
 
 def block_workload(torch, dev, *, n_samples, seq_len, batch):
@@ -172,6 +174,16 @@ def fq_inputs(torch, dev, gs):
             torch.ones(ROWS, ng, 1, device=dev), g.to(dev))
 
 
+def place_gate_rows(torch, g, dev):
+    """The float32 gradient of a gate_proj-shaped layer inside the fused gate/up
+    operand (blocks of SWIGLU_ROWS rows, every other block), and a bf16 W'
+    buffer of the fused shape: what the tune's fused step reads and writes."""
+    rows, cols = g.shape
+    g_fused = torch.zeros(2 * rows, cols, dtype=g.dtype, device=dev)
+    g_fused.view(-1, 2 * SWIGLU_ROWS, cols)[:, :SWIGLU_ROWS] = g.view(-1, SWIGLU_ROWS, cols)
+    return g_fused, torch.empty(2 * rows, cols, dtype=torch.bfloat16, device=dev)
+
+
 def fwd_bytes(n, gs):
     return n * (2 + 4 + 2) + (n // gs) * 8
 
@@ -201,6 +213,8 @@ def fake_quant_microbench(torch, K, dev, bits, gs, steps):
     w, v, a, b, g = fq_inputs(torch, dev, gs)
     n = ROWS * COLS
     wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
+    # the tune's placement of gate_proj in the fused gate/up operand
+    g_fused, wq_fused = place_gate_rows(torch, g, dev)
     codes = torch.empty(ROWS, COLS, dtype=torch.uint8, device=dev)
     scale = torch.empty(ROWS, COLS // gs, dtype=torch.float32, device=dev)
     zp = torch.empty_like(scale)
@@ -213,10 +227,11 @@ def fake_quant_microbench(torch, K, dev, bits, gs, steps):
         "bwd_update": lambda: K.fq_backward_signsgd(w, v, a, b, g, bits=bits, group_size=gs,
                                                     mode="asym", eps=1e-8, update=True, lr=0.005,
                                                     coef_lo=0.1, coef_hi=1.0, v_bound=0.5),
-        "step_requant": lambda: K.fq_step_requant_mapped(w, v, a, b, g, bits=bits, group_size=gs,
+        "step_requant": lambda: K.fq_step_requant_mapped(w, v, a, b, g_fused, bits=bits, group_size=gs,
                                                          mode="asym", eps=1e-8, lr=0.005, coef_lo=0.1,
-                                                         coef_hi=1.0, v_bound=0.5, row_block=0,
-                                                         row_stride=0, row_offset=0, wq_out=wq),
+                                                         coef_hi=1.0, v_bound=0.5, row_block=SWIGLU_ROWS,
+                                                         row_stride=2 * SWIGLU_ROWS, row_offset=0,
+                                                         wq_out=wq_fused),
         "codes": lambda: K.fq_forward(w, v, a, b, bits=bits, group_size=gs, mode="asym", eps=1e-8,
                                       codes_out=codes, scale_out=scale, zp_out=zp),
         "pack": lambda: K.pack_codes(codes, bits, signed=False, offset=0, packed_out=packed),
@@ -529,9 +544,10 @@ def profile_kernels(torch, K, dev, steps):
     7B block's gate/up GEMM with the SwiGLU epilogue, its weight-gradient and
     input-gradient GEMMs, the down projection, the attention-output
     projection, the SwiGLU-backward GEMM, the attention-output weight
-    gradient, the fake-quant forward of the microbench, and a 1 GiB copy that
-    calibrates the traffic counters (read and written bytes are known
-    exactly)."""
+    gradient, the fake-quant forward, the fused sign-SGD step with the next
+    W' (gate_proj's placement) and the fused quantize + pack of the microbench,
+    and a 1 GiB copy that calibrates the traffic counters (read and written
+    bytes are known exactly)."""
     T, h, mlp = 16384, SHAPE_7B["hidden"], SHAPE_7B["intermediate"]
     hq_d = SHAPE_7B["n_heads"] * SHAPE_7B["head_dim"]
     g = torch.Generator(device=dev).manual_seed(0)
@@ -547,8 +563,12 @@ def profile_kernels(torch, K, dev, steps):
     ws = torch.empty(max(K.gemm_workspace_bytes(*mnk) for mnk in ((2 * mlp, h, T), (T, h, 2 * mlp),
                                                                    (T, h, mlp), (h, hq_d, T))),
                      dtype=torch.uint8, device=dev)
-    w, v, a, b, _ = fq_inputs(torch, dev, GROUP)
+    w, v, a, b, gq = fq_inputs(torch, dev, GROUP)
     wq = torch.empty(ROWS, COLS, dtype=torch.bfloat16, device=dev)
+    g_fused, wq_fused = place_gate_rows(torch, gq, dev)
+    packed = torch.empty(ROWS, K.packed_width(COLS, BITS), dtype=torch.uint32, device=dev)
+    qp_scales = torch.empty(ROWS, COLS // GROUP, dtype=torch.bfloat16, device=dev)
+    qp_biases = torch.empty_like(qp_scales)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(steps):
@@ -560,6 +580,12 @@ def profile_kernels(torch, K, dev, steps):
         K.gemm_swiglu_bwd(x, wd, gu, dgu, workspace=ws)                            # gemm_dact
         K.gemm("tn", dh, attn, dwo, M=h, N=hq_d, K=T, workspace=ws)                # gemm_dw_o
         K.fq_forward(w, v, a, b, bits=BITS, group_size=GROUP, mode="asym", eps=1e-8, wq_out=wq)
+        K.fq_step_requant_mapped(w, v, a, b, g_fused, bits=BITS, group_size=GROUP, mode="asym",
+                                 eps=1e-8, lr=0.005, coef_lo=0.1, coef_hi=1.0, v_bound=0.5,
+                                 row_block=SWIGLU_ROWS, row_stride=2 * SWIGLU_ROWS, row_offset=0,
+                                 wq_out=wq_fused)                                  # step_requant
+        K.quantize_pack(w, v, a, b, bits=BITS, group_size=GROUP, mode="asym", eps=1e-8,
+                        packed_out=packed, scales_out=qp_scales, biases_out=qp_biases)
         K.copy_bytes(src, dst, src.numel())
     torch.cuda.synchronize(dev)
     print(json.dumps({"profile_kernels": True, "steps": steps}))

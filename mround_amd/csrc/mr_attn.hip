@@ -35,7 +35,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+  return pack_bf16x2(a, b);
 }
 
 // ---- LDS tiles --------------------------------------------------------------
@@ -560,8 +560,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_kv_reduce(const float* __re
     acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
   }
   const int64_t row = e / W, c = e % W;
-  const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(acc.x)) | (static_cast<uint32_t>(f32_to_bf16(acc.y)) << 16);
-  const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(acc.z)) | (static_cast<uint32_t>(f32_to_bf16(acc.w)) << 16);
+  const uint32_t lo = pack_bf16x2(acc.x, acc.y);
+  const uint32_t hi = pack_bf16x2(acc.z, acc.w);
   *reinterpret_cast<uint2*>(dqkv + row * ld + col0 + c) = make_uint2(lo, hi);
 }
 

@@ -121,8 +121,8 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ 
 // so each row is read from HBM once.
 
 __device__ __forceinline__ uint2 pack4_bf16(float a, float b, float c, float d) {
-  return make_uint2(static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16),
-                    static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16));
+  return make_uint2(pack_bf16x2(a, b),
+                    pack_bf16x2(c, d));
 }
 
 template <int NV>
@@ -236,8 +236,8 @@ __global__ __launch_bounds__(kBlock) void rope_v(uint16_t* __restrict__ x, int64
       ya0 = a0 * t4.x - b0 * t4.y; yb0 = b0 * t4.x + a0 * t4.y;
       ya1 = a1 * t4.z - b1 * t4.w; yb1 = b1 * t4.z + a1 * t4.w;
     }
-    ow_a[k] = static_cast<uint32_t>(f32_to_bf16(ya0)) | (static_cast<uint32_t>(f32_to_bf16(ya1)) << 16);
-    ow_b[k] = static_cast<uint32_t>(f32_to_bf16(yb0)) | (static_cast<uint32_t>(f32_to_bf16(yb1)) << 16);
+    ow_a[k] = pack_bf16x2(ya0, ya1);
+    ow_b[k] = pack_bf16x2(yb0, yb1);
   }
   *reinterpret_cast<uint4*>(p) = make_uint4(ow_a[0], ow_a[1], ow_a[2], ow_a[3]);
   *reinterpret_cast<uint4*>(p + half) = make_uint4(ow_b[0], ow_b[1], ow_b[2], ow_b[3]);

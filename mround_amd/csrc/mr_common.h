@@ -1,8 +1,7 @@
 // Shared helpers for the libmround_hip kernels (gfx950).
 //
-// Element conversions are written out on bit patterns so that their rounding
-// is explicit: bf16 and fp16 widen exactly, and narrowing rounds to nearest,
-// ties to even, which is what torch and MLX do.
+// Element conversions: bf16 and fp16 widen exactly, and narrowing rounds to
+// nearest, ties to even, which is what torch and MLX do.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,14 +32,21 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round to nearest even; a NaN keeps its sign and high payload bits and is
-// made quiet. Both results are formed and one selected (a branch per element
-// costs a handful of exec-mask instructions in the unrolled epilogues).
+// Narrowing to bfloat16 rounds to nearest even; a NaN keeps its sign and high
+// payload bits and is made quiet. gfx950 does this in one instruction for two
+// values (v_cvt_pk_bf16_f32, low half from the first operand); the device
+// test of mr_cast_f32_bf16 compares it with that bit-pattern rule on all 2^32
+// inputs.
+typedef float mr_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 mr_bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const mr_f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, mr_bf16x2));
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t quiet_nan = (u >> 16) | 0x40u;
-  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? quiet_nan : rounded);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
@@ -129,15 +135,12 @@ __device__ __forceinline__ void store8(void* p, int64_t i, const float (&x)[8]) 
     uint32_t words[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      uint16_t lo, hi;
       if constexpr (DT == MR_BF16) {
-        lo = f32_to_bf16(x[2 * k]);
-        hi = f32_to_bf16(x[2 * k + 1]);
+        words[k] = pack_bf16x2(x[2 * k], x[2 * k + 1]);
       } else {
-        lo = f32_to_f16(x[2 * k]);
-        hi = f32_to_f16(x[2 * k + 1]);
+        words[k] = static_cast<uint32_t>(f32_to_f16(x[2 * k])) |
+                   (static_cast<uint32_t>(f32_to_f16(x[2 * k + 1])) << 16);
       }
-      words[k] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
     }
     st16_stream(static_cast<uint16_t*>(p) + i, make_uint4(words[0], words[1], words[2], words[3]));
   }

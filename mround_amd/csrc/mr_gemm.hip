@@ -450,8 +450,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
     auto pack4 = [](float a, float b, float c, float d) {
       u32x2 v;
-      v.x = static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
-      v.y = static_cast<uint32_t>(f32_to_bf16(c)) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16);
+      v.x = pack_bf16x2(a, b);
+      v.y = pack_bf16x2(c, d);
       return v;
     };
     constexpr int REGION = (BM + BN) * ROW_BYTES * 2 / kWaves;  // bytes of LDS per wave
@@ -578,8 +578,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
             lds_u8* at = st + lcol * PITCH + (jj * 32 + gi * 8 + lrow) * OBY;
             if constexpr (OUT_BF16) {
               u32x2 w;
-              w.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-              w.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+              w.x = pack_bf16x2(v[0], v[1]);
+              w.y = pack_bf16x2(v[2], v[3]);
               *(__attribute__((address_space(3))) u32x2*)at = w;
             } else {
               *(__attribute__((address_space(3))) f32x4*)at = f32x4{v[0], v[1], v[2], v[3]};

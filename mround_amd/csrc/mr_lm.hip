@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kCeBlock) void ce_rows(const uint16_t* logits, int6
         const int64_t j = i * 8 + 2 * k;
         if (!ignored && j == label) p0 -= scale;
         if (!ignored && j + 1 == label) p1 -= scale;
-        w[k] = static_cast<uint32_t>(f32_to_bf16(p0)) | (static_cast<uint32_t>(f32_to_bf16(p1)) << 16);
+        w[k] = pack_bf16x2(p0, p1);
       }
       d8[i] = make_uint4(w[0], w[1], w[2], w[3]);
     }

@@ -3,12 +3,13 @@
 //
 // Arithmetic follows the reference's float32 operation order exactly
 // (mround/reference/quantize.py:156-319 forward, 370-522 backward; the
-// round-to-nearest shortcut of mround/core/quantizer.py:269-284): IEEE
-// division (never a reciprocal multiply), round half to even (rintf), no
-// contraction into fused multiply-adds (this file is built with
-// -ffp-contract=off). Codes and reconstructions are therefore bit-identical to
-// a float32 evaluation of the reference's formulas; only the per-group sums of
-// the backward differ, by summation order.
+// round-to-nearest shortcut of mround/core/quantizer.py:269-284): correctly
+// rounded quotients (IEEE division, or the exact reciprocal-and-correction
+// forms of div_maxq() and quotients() where those are proven exact), round
+// half to even (rintf), no contraction into fused multiply-adds (this file is
+// built with -ffp-contract=off). Codes and reconstructions are therefore
+// bit-identical to a float32 evaluation of the reference's formulas; only the
+// per-group sums of the backward differ, by summation order.
 //
 // Two launch shapes:
 //   fast    each lane owns 8 consecutive weights; a group of gs weights spans
@@ -31,18 +32,52 @@ constexpr int kBlock = 256;
 // Row placement of the reconstruction (forward) or of the gradient (backward)
 // inside a larger row-major buffer with the same column count: row r lives at
 // (r / blk) * stride + off + r % blk; blk == 0 is the identity.
+// n / d for 0 <= n < 2^31 and a divisor d >= 1 fixed per launch: with
+// l = ceil(log2 d), p = 31 + l and m = ceil(2^p / d) < 2^32, floor(n * m / 2^p)
+// equals floor(n / d), because n * m / 2^p exceeds n / d by less than
+// 2^31 / 2^p = 2^-l <= 1 / d. One 32 x 32 -> 64-bit multiply and a shift
+// instead of an integer division.
+struct FastDiv {
+  uint32_t m = 0;
+  int p = 0;
+  static FastDiv make(uint32_t d) {
+    FastDiv f;
+    int l = 0;
+    while ((uint64_t{1} << l) < d) ++l;
+    f.p = 31 + l;
+    f.m = static_cast<uint32_t>(((uint64_t{1} << f.p) + d - 1) / d);
+    return f;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return static_cast<uint32_t>((static_cast<uint64_t>(n) * m) >> p);
+  }
+};
+
 struct RowMap {
   int64_t blk, stride, off;
-  int cpr;  // 8-element chunks per row (fast kernels)
+  int cpr;              // 8-element chunks per row (fast kernels)
+  FastDiv by_cpr, by_blk;  // set on the host by prepare() (fast kernels)
   __device__ __forceinline__ int64_t row(int64_t r) const {
     return blk ? (r / blk) * stride + off + r % blk : r;
+  }
+  // The fast kernels' constants for `cols` columns; mapped launches have
+  // fewer than 2^31 chunks, so chunk and row indices fit 31 bits.
+  void prepare(int64_t cols) {
+    cpr = static_cast<int>(cols / 8);
+    if (blk) {
+      by_cpr = FastDiv::make(static_cast<uint32_t>(cpr));
+      by_blk = FastDiv::make(static_cast<uint32_t>(blk));
+    }
   }
   // Element index of chunk `chunk` (8 elements) under the placement.
   __device__ __forceinline__ int64_t chunk_elem(int64_t chunk) const {
     if (!blk) return chunk * 8;
-    const int c32 = static_cast<int>(chunk);
-    const int r = c32 / cpr;
-    return (row(r) * cpr + (c32 - r * cpr)) * 8;
+    const uint32_t c = static_cast<uint32_t>(chunk);
+    const uint32_t r = by_cpr.div(c);
+    const uint32_t col = c - r * static_cast<uint32_t>(cpr);
+    const uint32_t rb = by_blk.div(r);
+    const uint32_t rr = r - rb * static_cast<uint32_t>(blk);
+    return ((static_cast<int64_t>(rb) * stride + off + rr) * cpr + col) * 8;
   }
 };
 
@@ -52,6 +87,7 @@ struct Group {
   float wmax_raw;  // max(max(W_g), 0)
   float wmin_raw;  // min(min(W_g), 0)
   float wmin;      // wmin_raw * beta
+  float wmin_s;    // wmin / s (asymmetric)
   float base;      // searched scale
   bool pos_dom;    // symmetric: the positive extreme dominates
 };
@@ -62,13 +98,29 @@ __device__ __forceinline__ float clamp_magnitude(float s, float eps) {
   return sg * fmaxf(fabsf(s), eps);
 }
 
+// x / maxq, correctly rounded, from inv_maxq = RN(1/maxq): the fused
+// correction of quotients() below. maxq is 2^b - 1 or 2^(b - 1), b in [2, 8],
+// a divisor of at most 8 significant bits, and the identity holds for every
+// float32 significand of x (checked exhaustively for each maxq by the test
+// suite); x is zero or of magnitude in [2^-60, 2^60], otherwise it divides.
+__device__ __forceinline__ float div_maxq(float x, float maxq, float inv_maxq) {
+  const float ax = fabsf(x);
+  if (ax == 0.0f || (ax >= 0x1p-60f && ax <= 0x1p60f)) {
+    const float q0 = x * inv_maxq;
+    const float r = fmaf(q0, maxq, -x);
+    return fmaf(-r, inv_maxq, q0);
+  }
+  return x / maxq;
+}
+
 // Per-group scale and zero point: mround/reference/quantize.py:156-246.
 template <int MODE>
 __device__ __forceinline__ Group group_params(float mx, float mn, float a, float b, float base,
-                                              float maxq, float eps) {
+                                              float maxq, float inv_maxq, float eps) {
   Group p;
   p.base = base;
   p.zp = 0.0f;
+  p.wmin_s = 0.0f;
   p.pos_dom = false;
   p.wmax_raw = fmaxf(mx, 0.0f);
   p.wmin_raw = fminf(mn, 0.0f);
@@ -79,25 +131,28 @@ __device__ __forceinline__ Group group_params(float mx, float mn, float a, float
     float wmax = p.wmax_raw * a;
     p.wmin = p.wmin_raw * b;
     if constexpr (MODE == MR_ASYM) {
-      p.s = fmaxf((wmax - p.wmin) / maxq, eps);
-      p.zp = rintf(-p.wmin / p.s);
+      p.s = fmaxf(div_maxq(wmax - p.wmin, maxq, inv_maxq), eps);
+      // -wmin / s rounds to -(wmin / s): one division serves both.
+      p.wmin_s = p.wmin / p.s;
+      p.zp = rintf(-p.wmin_s);
     } else {
       float pos_mag = wmax;
       float neg_mag = -p.wmin;
       p.pos_dom = pos_mag >= neg_mag;
       float dominant = p.pos_dom ? pos_mag : neg_mag;
       float signed_ = p.pos_dom ? -dominant : dominant;
-      p.s = clamp_magnitude(signed_ / maxq, eps);
+      p.s = clamp_magnitude(div_maxq(signed_, maxq, inv_maxq), eps);
     }
   }
   return p;
 }
 
-// One weight: code (before narrowing), clamp mask, reconstruction.
+// One weight from its quotient t = w / s: code (before narrowing), clamp mask,
+// reconstruction.
 template <int MODE, bool HAS_V>
-__device__ __forceinline__ float quant_one(float w, float v, const Group& p, float qmin, float qmax,
-                                           float& code, float& inside) {
-  float x = w / p.s;
+__device__ __forceinline__ float quant_t(float t, float v, const Group& p, float qmin, float qmax,
+                                         float& code, float& inside) {
+  float x = t;
   if constexpr (HAS_V) x = x + v;
   float raw = rintf(x);
   if constexpr (MODE == MR_ASYM) raw = raw + p.zp;
@@ -105,6 +160,69 @@ __device__ __forceinline__ float quant_one(float w, float v, const Group& p, flo
   code = clampf(raw, qmin, qmax);
   if constexpr (MODE == MR_ASYM) return p.s * (code - p.zp);
   return p.s * code;
+}
+
+template <int MODE, bool HAS_V>
+__device__ __forceinline__ float quant_one(float w, float v, const Group& p, float qmin, float qmax,
+                                           float& code, float& inside) {
+  return quant_t<MODE, HAS_V>(w / p.s, v, p, qmin, qmax, code, inside);
+}
+
+// Quotients w / s of a lane's weights by their group's scale.
+//
+// The reference divides in float32, so every quotient must be the correctly
+// rounded one. An IEEE division costs about ten instructions and a hazard
+// stall; the fast kernels divide each of a lane's bfloat16 weights by the one
+// scale instead as
+//   y = RN(1/s) (one IEEE division per lane),  q0 = RN(w * y),
+//   r = RN(q0 * s - w) (fused),                 t = RN(q0 - r * y) (fused),
+// a one-step Markstein correction. For a numerator of at most 8 significant
+// bits (every bfloat16 value) and any float32 divisor t equals RN(w / s): the
+// identity depends only on the two significands while every intermediate
+// stays normal, and all 2^7 x 2^23 significand pairs are checked exhaustively
+// by the test suite. The lane takes this path only when each weight is zero
+// or has magnitude in [2^-60, 2^60] and so does the scale (then q0, r and t
+// are normal); otherwise, and for float32 weights, it divides. With s > 0
+// this form also gives the quotient of a signed zero its IEEE sign; a
+// negative symmetric scale divides -w by -s.
+constexpr float kQuotLo = 0x1p-60f, kQuotHi = 0x1p60f;
+// Smallest admissible (bits << 1) - 2 of a nonzero weight; both zeros wrap
+// above every key.
+constexpr uint32_t kQuotKeyLo = ((127u - 60u) << 24) - 2u;
+
+template <int WT, int N>
+__device__ __forceinline__ bool lane_quotients_fast(const float (&x)[N], float mx, float mn) {
+  if constexpr (WT != MR_BF16) {
+    return false;
+  } else {
+    uint32_t kmin = 0xffffffffu;
+#pragma unroll
+    for (int k = 0; k < N; ++k) kmin = min(kmin, (__float_as_uint(x[k]) << 1) - 2u);
+    return kmin >= kQuotKeyLo && fmaxf(mx, -mn) <= kQuotHi;
+  }
+}
+
+template <int WT, int MODE, int N>
+__device__ __forceinline__ void quotients(const float (&x)[N], float s, bool lane_fast,
+                                          float (&t)[N]) {
+  if constexpr (WT == MR_BF16) {
+    // The asymmetric scale is positive; should it not be, the lane divides.
+    const float sa = MODE == MR_ASYM ? s : fabsf(s);
+    if (lane_fast && sa >= kQuotLo && sa <= kQuotHi) {
+      const float y = 1.0f / sa;
+      const uint32_t sgn = MODE == MR_ASYM ? 0u : (__float_as_uint(s) & 0x80000000u);
+#pragma unroll
+      for (int k = 0; k < N; ++k) {
+        const float w = __uint_as_float(__float_as_uint(x[k]) ^ sgn);
+        const float q0 = w * y;
+        const float r = fmaf(q0, sa, -w);
+        t[k] = fmaf(-r, y, q0);
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) t[k] = x[k] / s;
 }
 
 __device__ __forceinline__ float group_max(float x, int tpg) {
@@ -173,7 +291,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
     const void* __restrict__ w, const float* __restrict__ v, const float* __restrict__ alpha,
     const float* __restrict__ beta, const float* __restrict__ init_scale, void* __restrict__ wq,
     uint8_t* __restrict__ codes, float* __restrict__ scale_out, float* __restrict__ zp_out,
-    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps,
+    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float inv_maxq, float qmin, float qmax, float eps,
     RowMap map) {
   int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const bool active = chunk < n_chunks;
@@ -201,7 +319,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
     b = beta[grp];
   }
   if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
-  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, inv_maxq, eps);
 
   float vv[8];
   if constexpr (HAS_V) {
@@ -210,11 +328,13 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
 #pragma unroll
     for (int k = 0; k < 8; ++k) vv[k] = 0.0f;
   }
+  float t[8];
+  quotients<WT, MODE>(x, p.s, lane_quotients_fast<WT>(x, mx, mn), t);
   float q[8], c[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     float in;
-    q[k] = quant_one<MODE, HAS_V>(x[k], vv[k], p, qmin, qmax, c[k], in);
+    q[k] = quant_t<MODE, HAS_V>(t[k], vv[k], p, qmin, qmax, c[k], in);
   }
   if (!active) return;
   if (wq) store8<OT>(wq, map.chunk_elem(chunk), q);
@@ -247,7 +367,7 @@ __global__ __launch_bounds__(kBlock) void fq_pack_fast(
     const void* __restrict__ w, const float* __restrict__ v, const float* __restrict__ alpha,
     const float* __restrict__ beta, const float* __restrict__ init_scale, uint32_t* __restrict__ packed,
     void* __restrict__ scales, void* __restrict__ biases, int64_t n_chunks, int tpg, int tpg_shift,
-    int bits, float maxq, float qmin, float qmax, float eps) {
+    int bits, float maxq, float inv_maxq, float qmin, float qmax, float eps) {
   int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const bool active = chunk < n_chunks;
   if (!active) chunk = n_chunks - 1;  // whole groups of inactive lanes stay for the shuffles
@@ -272,7 +392,7 @@ __global__ __launch_bounds__(kBlock) void fq_pack_fast(
     b = beta[grp];
   }
   if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
-  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, inv_maxq, eps);
   float vv[8];
   if constexpr (HAS_V) {
     load8_f32(v, e, vv);
@@ -282,11 +402,13 @@ __global__ __launch_bounds__(kBlock) void fq_pack_fast(
   }
   // stored (unsigned) codes: the symmetric ones offset by 2^(bits-1)
   const uint32_t off = MODE == MR_ASYM ? 0u : static_cast<uint32_t>(maxq);
+  float t[8];
+  quotients<WT, MODE>(x, p.s, lane_quotients_fast<WT>(x, mx, mn), t);
   uint64_t stream = 0;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     float c, in;
-    quant_one<MODE, HAS_V>(x[k], vv[k], p, qmin, qmax, c, in);
+    quant_t<MODE, HAS_V>(t[k], vv[k], p, qmin, qmax, c, in);
     const uint32_t u = static_cast<uint32_t>(static_cast<int>(c) + static_cast<int>(off));
     stream |= static_cast<uint64_t>(u) << (k * bits);
   }
@@ -339,7 +461,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_generic(
     const float* __restrict__ alpha, const float* __restrict__ beta,
     const float* __restrict__ init_scale, void* __restrict__ wq, int ot,
     uint8_t* __restrict__ codes, float* __restrict__ scale_out, float* __restrict__ zp_out,
-    int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float qmin, float qmax,
+    int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float inv_maxq, float qmin, float qmax,
     float eps, RowMap map) {
   const int64_t grp = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
@@ -363,7 +485,7 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_generic(
     b = beta[grp];
   }
   if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
-  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, inv_maxq, eps);
   for (int t = lane; t < gs; t += 64) {
     int64_t c = c0 + t;
     float x = c < cols ? load_any(w, wt, r * cols + c) : 0.0f;
@@ -398,9 +520,8 @@ struct BwdTerms {
 };
 
 template <int MODE>
-__device__ __forceinline__ BwdTerms<MODE> bwd_one(float x, float vv, float g, const Group& p,
+__device__ __forceinline__ BwdTerms<MODE> bwd_one(float t, float vv, float g, const Group& p,
                                                   float wmin_over_s, float qmin, float qmax) {
-  const float t = x / p.s;
   float raw = rintf(t + vv);
   if constexpr (MODE == MR_ASYM) raw = raw + p.zp;
   const bool in = raw >= qmin && raw <= qmax;
@@ -455,13 +576,17 @@ struct StepArgs {
   }
 };
 
+// Each lane owns one 8-weight chunk. (Two consecutive chunks a lane, which
+// halves the per-group work per weight, measured 30 % slower: each 16-byte
+// access of the wave then covers every other 16 bytes.)
 template <int WT, int GT, int MODE, bool UPDATE, int TPG>
 __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
     const void* __restrict__ w, float* __restrict__ v, float* __restrict__ alpha,
     float* __restrict__ beta, const float* __restrict__ init_scale, const void* __restrict__ g,
-    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float qmin, float qmax, float eps,
+    int64_t n_chunks, int tpg, int tpg_shift, float maxq, float inv_maxq, float qmin, float qmax, float eps,
     StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
     float* __restrict__ gb_out, RowMap map) {
+  constexpr int N = 8;
   if constexpr (UPDATE) st.lr = st.rate();
   int64_t chunk = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const bool active = chunk < n_chunks;
@@ -469,13 +594,13 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
   const int64_t grp = chunk >> tpg_shift;
   const int64_t e = chunk * 8;
 
-  float x[8], vv[8], gg[8];
+  float x[N], vv[N], gg[N];
   load8<WT>(w, e, x);
   load8_f32_cached(v, e, vv);
   load8<GT>(g, map.chunk_elem(chunk), gg);
   float mx = x[0], mn = x[0];
 #pragma unroll
-  for (int k = 1; k < 8; ++k) {
+  for (int k = 1; k < N; ++k) {
     mx = fmaxf(mx, x[k]);
     mn = fminf(mn, x[k]);
   }
@@ -487,14 +612,17 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
   const float b = beta[grp];
   float base = 0.0f;
   if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
-  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
-  const float wmin_over_s = p.wmin / p.s;
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, inv_maxq, eps);
+  const float wmin_over_s = p.wmin_s;
+  const bool lane_fast = lane_quotients_fast<WT>(x, mx, mn);
+  float tq[N];
+  quotients<WT, MODE>(x, p.s, lane_fast, tq);
 
   float sum_s = 0.0f, sum_d = 0.0f;
-  float gv[8];
+  float gv[N];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    BwdTerms<MODE> t = bwd_one<MODE>(x[k], vv[k], gg[k], p, wmin_over_s, qmin, qmax);
+  for (int k = 0; k < N; ++k) {
+    BwdTerms<MODE> t = bwd_one<MODE>(tq[k], vv[k], gg[k], p, wmin_over_s, qmin, qmax);
     gv[k] = t.gv;
     sum_s = sum_s + t.ts;
     if constexpr (MODE == MR_ASYM) sum_d = sum_d + t.td;
@@ -512,9 +640,9 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
     if (gb_out) gb_out[grp] = gb;
   }
   if constexpr (UPDATE) {
-    float nv[8];
+    float nv[N];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) nv[k] = clampf(vv[k] - st.lr * signf(gv[k]), -st.vb, st.vb);
+    for (int k = 0; k < N; ++k) nv[k] = clampf(vv[k] - st.lr * signf(gv[k]), -st.vb, st.vb);
     store8_f32_cached(v, e, nv);
     // Every lane of the group holds the group sums, so each forms the new
     // coefficients itself (the leader stores them).
@@ -527,16 +655,18 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_fast(
     if (st.wq) {
       // The next step's W': the forward's arithmetic on the same group
       // extremes and the parameters just written.
-      const Group p2 = group_params<MODE>(mx, mn, na, nb, base, maxq, eps);
-      float q[8];
+      const Group p2 = group_params<MODE>(mx, mn, na, nb, base, maxq, inv_maxq, eps);
+      quotients<WT, MODE>(x, p2.s, lane_fast, tq);
+      float q[N];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < N; ++k) {
         float code, in;
-        q[k] = quant_one<MODE, true>(x[k], nv[k], p2, qmin, qmax, code, in);
+        q[k] = quant_t<MODE, true>(tq[k], nv[k], p2, qmin, qmax, code, in);
       }
-      if (st.wq_dt == MR_BF16) store8<MR_BF16>(st.wq, map.chunk_elem(chunk), q);
-      else if (st.wq_dt == MR_F16) store8<MR_F16>(st.wq, map.chunk_elem(chunk), q);
-      else store8<MR_F32>(st.wq, map.chunk_elem(chunk), q);
+      const int64_t o = map.chunk_elem(chunk);
+      if (st.wq_dt == MR_BF16) store8<MR_BF16>(st.wq, o, q);
+      else if (st.wq_dt == MR_F16) store8<MR_F16>(st.wq, o, q);
+      else store8<MR_F32>(st.wq, o, q);
     }
   }
 }
@@ -545,7 +675,7 @@ template <int MODE, bool UPDATE>
 __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
     const void* __restrict__ w, int wt, float* __restrict__ v, float* __restrict__ alpha,
     float* __restrict__ beta, const float* __restrict__ init_scale, const void* __restrict__ g,
-    int gt, int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float qmin, float qmax,
+    int gt, int64_t rows, int64_t cols, int gs, int64_t ng, float maxq, float inv_maxq, float qmin, float qmax,
     float eps, StepArgs st, float* __restrict__ gv_out, float* __restrict__ ga_out,
     float* __restrict__ gb_out, RowMap map) {
   if constexpr (UPDATE) st.lr = st.rate();
@@ -569,8 +699,8 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
   const float b = beta[grp];
   float base = 0.0f;
   if constexpr (MODE == MR_SYM_SEARCHED) base = init_scale[grp];
-  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, eps);
-  const float wmin_over_s = p.wmin / p.s;
+  const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, inv_maxq, eps);
+  const float wmin_over_s = p.wmin_s;
   float sum_s = 0.0f, sum_d = 0.0f;
   for (int t = lane; t < gs; t += 64) {
     int64_t c = c0 + t;
@@ -578,7 +708,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
     float x = real ? load_any(w, wt, r * cols + c) : 0.0f;
     float gg = real ? load_any(g, gt, map.row(r) * cols + c) : 0.0f;
     float vv = v[grp * gs + t];
-    BwdTerms<MODE> tm = bwd_one<MODE>(x, vv, gg, p, wmin_over_s, qmin, qmax);
+    BwdTerms<MODE> tm = bwd_one<MODE>(x / p.s, vv, gg, p, wmin_over_s, qmin, qmax);
     sum_s = sum_s + tm.ts;
     if constexpr (MODE == MR_ASYM) sum_d = sum_d + tm.td;
     if (gv_out) gv_out[grp * gs + t] = tm.gv;
@@ -602,7 +732,7 @@ __global__ __launch_bounds__(kBlock) void fq_bwd_generic(
       // rereads the v entries it wrote itself).
       const float na = clampf(a - st.lr * signf(ga), st.lo, st.hi);
       const float nb = clampf(b - st.lr * signf(gb), st.lo, st.hi);
-      const Group p2 = group_params<MODE>(mx, mn, na, nb, base, maxq, eps);
+      const Group p2 = group_params<MODE>(mx, mn, na, nb, base, maxq, inv_maxq, eps);
       for (int t = lane; t < gs; t += 64) {
         const int64_t c = c0 + t;
         if (c >= cols) continue;
@@ -621,7 +751,7 @@ struct Shape {
   int64_t rows, cols, ng, n_groups;
   int gs, tpg, tpg_shift;
   bool fast;
-  float maxq, qmin, qmax;
+  float maxq, inv_maxq, qmin, qmax;  // inv_maxq = RN(1 / maxq)
 };
 
 int check_common(const char* fn, const void* w, int w_dtype, int64_t rows, int64_t cols,
@@ -658,6 +788,7 @@ int check_common(const char* fn, const void* w, int w_dtype, int64_t rows, int64
     sh.qmin = -sh.maxq;
     sh.qmax = sh.maxq - 1.0f;
   }
+  sh.inv_maxq = 1.0f / sh.maxq;
   return MR_OK;
 }
 
@@ -665,7 +796,7 @@ template <int MODE, bool HAS_V>
 int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const float* alpha,
                const float* beta, const float* init_scale, void* wq, int ot, uint8_t* codes,
                float* scale_out, float* zp_out, float eps, RowMap map, hipStream_t stream) {
-  map.cpr = static_cast<int>(sh.cols / 8);
+  map.prepare(sh.cols);
   const bool fast_types = (wt == MR_F32 || wt == MR_BF16) && (!wq || ot == MR_F32 || ot == MR_BF16);
   const bool fast_align = aligned16(w) && (!HAS_V || aligned16(v)) && (!wq || aligned16(wq)) &&
                           (!codes || (reinterpret_cast<uintptr_t>(codes) & 7u) == 0);
@@ -677,7 +808,7 @@ int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const flo
   hipLaunchKernelGGL((fq_fwd_fast<WT_, OT_, MODE, HAS_V, T_>),                             \
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, w, v, alpha, \
                      beta, init_scale, wq, codes, scale_out, zp_out, n_chunks, sh.tpg,       \
-                     sh.tpg_shift, sh.maxq, sh.qmin, sh.qmax, eps, map)
+                     sh.tpg_shift, sh.maxq, sh.inv_maxq, sh.qmin, sh.qmax, eps, map)
 #define MR_FWD_FAST(WT_, OT_)                                               \
   do {                                                                      \
     if (sh.tpg == 8) MR_FWD_FAST_T(WT_, OT_, 8);                            \
@@ -697,7 +828,7 @@ int launch_fwd(const Shape& sh, const void* w, int wt, const float* v, const flo
     if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_fq_forward: tensor too large");
     hipLaunchKernelGGL((fq_fwd_generic<MODE, HAS_V>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kBlock), 0, stream, w, wt, v, alpha, beta, init_scale, wq, ot, codes,
-                       scale_out, zp_out, sh.rows, sh.cols, sh.gs, sh.ng, sh.maxq, sh.qmin,
+                       scale_out, zp_out, sh.rows, sh.cols, sh.gs, sh.ng, sh.maxq, sh.inv_maxq, sh.qmin,
                        sh.qmax, eps, map);
   }
   MR_LAUNCH_CHECK("mr_fq_forward");
@@ -708,7 +839,7 @@ template <int MODE, bool UPDATE>
 int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, float* beta,
                const float* init_scale, const void* g, int gt, float eps, StepArgs st,
                float* gv_out, float* ga_out, float* gb_out, RowMap map, hipStream_t stream) {
-  map.cpr = static_cast<int>(sh.cols / 8);
+  map.prepare(sh.cols);
   const bool fast_types = (wt == MR_F32 || wt == MR_BF16) && (gt == MR_F32 || gt == MR_BF16);
   const bool fast_align = aligned16(w) && aligned16(v) && aligned16(g) && (!gv_out || aligned16(gv_out));
   if (sh.fast && fast_types && fast_align) {
@@ -718,8 +849,8 @@ int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, f
 #define MR_BWD_FAST_T(WT_, GT_, T_)                                                         \
   hipLaunchKernelGGL((fq_bwd_fast<WT_, GT_, MODE, UPDATE, T_>),                             \
                      dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, stream, w, v, alpha, \
-                     beta, init_scale, g, n_chunks, sh.tpg, sh.tpg_shift, sh.maxq, sh.qmin,   \
-                     sh.qmax, eps, st, gv_out, ga_out, gb_out, map)
+                     beta, init_scale, g, n_chunks, sh.tpg, sh.tpg_shift, sh.maxq, sh.inv_maxq,  \
+                     sh.qmin, sh.qmax, eps, st, gv_out, ga_out, gb_out, map)
 #define MR_BWD_FAST(WT_, GT_)                                               \
   do {                                                                      \
     if (sh.tpg == 8) MR_BWD_FAST_T(WT_, GT_, 8);                            \
@@ -738,7 +869,7 @@ int launch_bwd(const Shape& sh, const void* w, int wt, float* v, float* alpha, f
     if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_fq_backward_signsgd: tensor too large");
     hipLaunchKernelGGL((fq_bwd_generic<MODE, UPDATE>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kBlock), 0, stream, w, wt, v, alpha, beta, init_scale, g, gt, sh.rows,
-                       sh.cols, sh.gs, sh.ng, sh.maxq, sh.qmin, sh.qmax, eps, st, gv_out, ga_out,
+                       sh.cols, sh.gs, sh.ng, sh.maxq, sh.inv_maxq, sh.qmin, sh.qmax, eps, st, gv_out, ga_out,
                        gb_out, map);
   }
   MR_LAUNCH_CHECK("mr_fq_backward_signsgd");
@@ -755,7 +886,7 @@ int launch_pack(const Shape& sh, const void* w, int wt, const float* v, const fl
 #define MR_PACK_T(WT_, OT_, T_)                                                                    \
   hipLaunchKernelGGL((fq_pack_fast<WT_, OT_, MODE, HAS_V, T_>), dim3(static_cast<unsigned>(blocks)), \
                      dim3(kBlock), 0, stream, w, v, alpha, beta, init_scale, packed, scales, biases,   \
-                     n_chunks, sh.tpg, sh.tpg_shift, bits, sh.maxq, sh.qmin, sh.qmax, eps)
+                     n_chunks, sh.tpg, sh.tpg_shift, bits, sh.maxq, sh.inv_maxq, sh.qmin, sh.qmax, eps)
 #define MR_PACK_W(WT_, OT_)                             \
   do {                                                  \
     if (sh.tpg == 8) MR_PACK_T(WT_, OT_, 8);            \
@@ -846,7 +977,7 @@ static int fq_forward_impl(const char* fn, const void* w, int w_dtype, const flo
     return fail(MR_EINVAL, "%s: a zero point exists only in the asymmetric mode", fn);
   if (map.blk < 0 || map.stride < 0 || map.off < 0)
     return fail(MR_EINVAL, "%s: negative row placement", fn);
-  if (map.blk && rows * cols / 8 > 0x7fffffffLL)
+  if (map.blk && (rows * cols / 8 > 0x7fffffffLL || map.blk > 0x7fffffffLL))
     return fail(MR_EINVAL, "%s: placed tensor too large", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* codes = static_cast<uint8_t*>(codes_out);
@@ -867,7 +998,7 @@ int mr_fq_forward(const void* w, int w_dtype, const float* v, const float* alpha
                   void* codes_out, float* scale_out, float* zp_out, void* stream) {
   return fq_forward_impl("mr_fq_forward", w, w_dtype, v, alpha, beta, init_scale, rows, cols,
                          group_size, bits, mode, eps, wq_out, wq_dtype, codes_out, scale_out, zp_out,
-                         mr::RowMap{0, 0, 0, 0}, stream);
+                         mr::RowMap{0, 0, 0, 0, {}, {}}, stream);
 }
 
 int mr_fq_forward_mapped(const void* w, int w_dtype, const float* v, const float* alpha,
@@ -877,7 +1008,7 @@ int mr_fq_forward_mapped(const void* w, int w_dtype, const float* v, const float
   if (!wq_out) return mr::fail(MR_EINVAL, "mr_fq_forward_mapped: no output");
   return fq_forward_impl("mr_fq_forward_mapped", w, w_dtype, v, alpha, beta, init_scale, rows,
                          cols, group_size, bits, mode, eps, wq_out, wq_dtype, nullptr, nullptr,
-                         nullptr, mr::RowMap{row_block, row_stride, row_offset, 0}, stream);
+                         nullptr, mr::RowMap{row_block, row_stride, row_offset, 0, {}, {}}, stream);
 }
 
 static int fq_backward_impl(const char* fn, const void* w, int w_dtype, float* v, float* alpha,
@@ -903,7 +1034,7 @@ static int fq_backward_impl(const char* fn, const void* w, int w_dtype, float* v
   if (update && !(coef_lo <= coef_hi && v_bound >= 0.0f)) return fail(MR_EINVAL, "%s: bad bounds", fn);
   if (map.blk < 0 || map.stride < 0 || map.off < 0)
     return fail(MR_EINVAL, "%s: negative row placement", fn);
-  if (map.blk && rows * cols / 8 > 0x7fffffffLL)
+  if (map.blk && (rows * cols / 8 > 0x7fffffffLL || map.blk > 0x7fffffffLL))
     return fail(MR_EINVAL, "%s: placed tensor too large", fn);
   if (wq_out && !update) return fail(MR_EINVAL, "%s: W' is written only with the update", fn);
   if (lr_tab && (!step || lr_len < 1 || !update))
@@ -934,7 +1065,7 @@ int mr_fq_backward_signsgd(const void* w, int w_dtype, float* v, float* alpha, f
   return fq_backward_impl("mr_fq_backward_signsgd", w, w_dtype, v, alpha, beta, init_scale, g,
                           g_dtype, rows, cols, group_size, bits, mode, eps, update, lr, coef_lo,
                           coef_hi, v_bound, grad_v_out, grad_alpha_out, grad_beta_out,
-                          mr::RowMap{0, 0, 0, 0}, stream);
+                          mr::RowMap{0, 0, 0, 0, {}, {}}, stream);
 }
 
 int mr_fq_backward_signsgd_mapped(const void* w, int w_dtype, float* v, float* alpha, float* beta,
@@ -946,7 +1077,7 @@ int mr_fq_backward_signsgd_mapped(const void* w, int w_dtype, float* v, float* a
   return fq_backward_impl("mr_fq_backward_signsgd_mapped", w, w_dtype, v, alpha, beta, init_scale,
                           g, g_dtype, rows, cols, group_size, bits, mode, eps, 1, lr, coef_lo,
                           coef_hi, v_bound, nullptr, nullptr, nullptr,
-                          mr::RowMap{row_block, row_stride, row_offset, 0}, stream);
+                          mr::RowMap{row_block, row_stride, row_offset, 0, {}, {}}, stream);
 }
 
 int mr_fq_step_requant_mapped(const void* w, int w_dtype, float* v, float* alpha, float* beta,
@@ -962,7 +1093,7 @@ int mr_fq_step_requant_mapped(const void* w, int w_dtype, float* v, float* alpha
   return fq_backward_impl("mr_fq_step_requant_mapped", w, w_dtype, v, alpha, beta, init_scale, g,
                           g_dtype, rows, cols, group_size, bits, mode, eps, 1, lr, coef_lo, coef_hi,
                           v_bound, nullptr, nullptr, nullptr,
-                          mr::RowMap{row_block, row_stride, row_offset, 0}, stream, wq_out, wq_dtype);
+                          mr::RowMap{row_block, row_stride, row_offset, 0, {}, {}}, stream, wq_out, wq_dtype);
 }
 
 int mr_fq_step_requant_mapped_sched(const void* w, int w_dtype, float* v, float* alpha, float* beta,
@@ -979,7 +1110,7 @@ int mr_fq_step_requant_mapped_sched(const void* w, int w_dtype, float* v, float*
   return fq_backward_impl("mr_fq_step_requant_mapped_sched", w, w_dtype, v, alpha, beta, init_scale,
                           g, g_dtype, rows, cols, group_size, bits, mode, eps, 1, 0.0f, coef_lo,
                           coef_hi, v_bound, nullptr, nullptr, nullptr,
-                          mr::RowMap{row_block, row_stride, row_offset, 0}, stream, wq_out, wq_dtype,
+                          mr::RowMap{row_block, row_stride, row_offset, 0, {}, {}}, stream, wq_out, wq_dtype,
                           lr_table, step, lr_len);
 }
 

@@ -546,8 +546,9 @@ def profile_kernels(torch, K, dev, steps):
     projection, the SwiGLU-backward GEMM, the attention-output weight
     gradient, the fake-quant forward, the fused sign-SGD step with the next
     W' (gate_proj's placement) and the fused quantize + pack of the microbench,
-    and a 1 GiB copy that calibrates the traffic counters (read and written
-    bytes are known exactly)."""
+    the attention forward and backward of the 7B block (8 x 2048 tokens, 28 /
+    4 heads of 128), and a 1 GiB copy that calibrates the traffic counters
+    (read and written bytes are known exactly)."""
     T, h, mlp = 16384, SHAPE_7B["hidden"], SHAPE_7B["intermediate"]
     hq_d = SHAPE_7B["n_heads"] * SHAPE_7B["head_dim"]
     g = torch.Generator(device=dev).manual_seed(0)
@@ -569,6 +570,15 @@ def profile_kernels(torch, K, dev, steps):
     packed = torch.empty(ROWS, K.packed_width(COLS, BITS), dtype=torch.uint32, device=dev)
     qp_scales = torch.empty(ROWS, COLS // GROUP, dtype=torch.bfloat16, device=dev)
     qp_biases = torch.empty_like(qp_scales)
+    # attention of the 7B block: 8 x 2048 tokens, 28 query / 4 kv heads of 128
+    B_, S_, hq_, hkv_, d_ = 8, 2048, SHAPE_7B["n_heads"], SHAPE_7B["n_kv_heads"], SHAPE_7B["head_dim"]
+    qkv = (torch.randn(B_ * S_, (hq_ + 2 * hkv_) * d_, generator=g, device=dev)).to(torch.bfloat16)
+    a_out = torch.empty(B_ * S_, hq_ * d_, dtype=torch.bfloat16, device=dev)
+    a_lse = torch.empty(B_, hq_, S_, device=dev)
+    a_dsum = torch.empty_like(a_lse)
+    a_dout = torch.randn(B_ * S_, hq_ * d_, generator=g, device=dev).to(torch.bfloat16)
+    a_dqkv = torch.empty_like(qkv)
+    a_args = dict(batch=B_, seq_len=S_, n_heads=hq_, n_kv_heads=hkv_, head_dim=d_, scale=d_ ** -0.5)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(steps):
@@ -586,6 +596,8 @@ def profile_kernels(torch, K, dev, steps):
                                  wq_out=wq_fused)                                  # step_requant
         K.quantize_pack(w, v, a, b, bits=BITS, group_size=GROUP, mode="asym", eps=1e-8,
                         packed_out=packed, scales_out=qp_scales, biases_out=qp_biases)
+        K.attn_fwd(qkv, **a_args, out=a_out, lse=a_lse)                             # attn_fwd
+        K.attn_bwd(qkv, a_out, a_dout, a_lse, a_dsum, **a_args, dqkv=a_dqkv)         # attn_bwd
         K.copy_bytes(src, dst, src.numel())
     torch.cuda.synchronize(dev)
     print(json.dumps({"profile_kernels": True, "steps": steps}))

@@ -76,12 +76,13 @@ typedef __attribute__((address_space(1))) void gbl_void_t;
 // of it at physical chunk l % (D / 8), i.e. logical chunk (l % (D/8)) ^ swz_bits(row).
 template <int D, int NW = 4>
 __device__ __forceinline__ void dma_rowtile(const uint16_t* src, int64_t ld, int64_t r0, int col,
-                                            uint8_t* lds) {
+                                            uint8_t* lds, int wave = -1) {
   constexpr int CPR = D / 8;
   constexpr int RPI = 64 / CPR;
   constexpr int INSTR = 64 / RPI / NW;
   static_assert(INSTR * RPI * NW == 64, "the waves must split the tile evenly");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wave < 0) wave = threadIdx.x >> 6;  // else: this wave's index among the NW
   const int sub = lane / CPR, pchunk = lane % CPR;
 #pragma unroll
   for (int i = 0; i < INSTR; ++i) {
@@ -546,6 +547,260 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D == 6
     }
 }
 
+// dK, dV at D = 128 with each 32-key group's work split over two waves that
+// share a SIMD (waves w and w + 4): the P wave (w < 4) holds K, forms
+// S^T = K Q^T and the probabilities P and accumulates dV += P^T dO; the dS
+// wave holds V, forms dP^T = V dO^T and, with P from LDS, dS = P (dP -
+// rowsum(dO O)) and dK += dS^T Q. Each wave carries one operand and one
+// accumulator set, about half of the single-wave kernel's registers, so two
+// waves fit a SIMD and one's softmax or dS arithmetic runs under the other's
+// MFMAs. P crosses in fp32 in the accumulator layout both waves share (no
+// rounding, no shuffles): the products and their order are the single-wave
+// kernel's. Two barriers per query tile: one for the tile (the P wave's Q
+// and the dS wave's dO arrive by direct loads, double buffered), one for P.
+template <int D>
+__global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2))) void attn_bwd_dkdv_pair(
+    const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
+    const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
+    float scale, uint16_t* __restrict__ dqkv, int hsplit, float* __restrict__ part) {
+  constexpr int NS = D / 16, ND = D / 32;
+  constexpr int TILE = 64 * D * 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t Q0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t O0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t Q1[TILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t O1[TILE];
+  __shared__ __attribute__((aligned(16))) float LD0[128];  // lse (log2 domain) then rowsum(dO O) of the tile's 64 queries
+  __shared__ __attribute__((aligned(16))) float LD1[128];
+  // P of each key group: [half][register group][lane] float4, as the P wave holds it.
+  __shared__ __attribute__((aligned(16))) float Pb[4][2 * 4 * 64 * 4];
+  const int kb = blockIdx.z, g = blockIdx.x / hsplit, hs = blockIdx.x % hsplit, b = blockIdx.y;
+  const int G = Hq / Hkv;
+  const int h_lo = hs * G / hsplit, h_hi = (hs + 1) * G / hsplit;
+  const int hq0 = g * G + h_lo;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+  const bool pwave = wave < 4;
+  const int kw = wave & 3;
+  const int k0w = kb * QB + kw * 32;
+  const int kj = k0w + l32;  // this lane's key
+  const int64_t tok0 = static_cast<int64_t>(b) * S;
+  const int kcol = (Hq + g) * D, vcol = (Hq + Hkv + g) * D;
+  const float scale_log2 = scale * kLog2e;
+  const int first_q = kb * QB;
+  const int nqt = (S - first_q) / 64;
+  const int n_items = (h_hi - h_lo) * nqt;
+  float* const Pw = Pb[kw];
+
+  // Item i: query head hq0 + i / nqt, query tile first_q + 64 (i % nqt). The
+  // P waves bring Q, the dS waves dO.
+  auto issue = [&](int i, uint8_t* Qd, uint8_t* Od) {
+    const int hq = hq0 + i / nqt;
+    const int64_t r0 = tok0 + first_q + (i % nqt) * 64;
+    if (pwave) dma_rowtile<D>(qkv, ld, r0, hq * D, Qd, kw);
+    else dma_rowtile<D>(dout, ldo, r0, hq * D, Od, kw);
+  };
+  auto fetch_ld = [&](int i) -> float {  // threads 0..127: this item's lse / rowsum value
+    const int hq = hq0 + i / nqt;
+    const int q = first_q + (i % nqt) * 64 + (threadIdx.x & 63);
+    const int64_t at = (static_cast<int64_t>(b) * Hq + hq) * S + q;
+    return threadIdx.x < 64 ? lse[at] * kLog2e : dsum[at];
+  };
+
+  uint32_t row_off[NS], tr_off[2][ND];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    row_off[s] = rowtile_off<D>(l32, 2 * s + h);
+    asm volatile("" : "+v"(row_off[s]));
+  }
+#pragma unroll
+  for (int hv = 0; hv < 2; ++hv)
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      const int q = (lane >> 4) & 1, li = lane & 15;
+      tr_off[hv][dt] = rowtile_off<D>(4 * h + (li >> 2) + 8 * hv, (dt * 32 + q * 16) / 8 + ((li & 3) >> 1)) +
+                       (li & 1) * 8;
+      asm volatile("" : "+v"(tr_off[hv][dt]));
+    }
+  auto rd_row = [&](const uint8_t* t, int mq, int s) -> bf16x8 {
+    return *(const lds_bf16x8_t*)((lds_cptr)t + row_off[s] + mq * 32 * (2 * D));
+  };
+  auto rd_tr = [&](const uint8_t* t, int dt, int s) -> bf16x8 {
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((lds_cptr)t + tr_off[0][dt] + s * 16 * (2 * D)));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((lds_cptr)t + tr_off[1][dt] + s * 16 * (2 * D)));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) f32x4 lds_f4;
+  auto p_slot = [&](int mq, int rg) -> lds_f4* {
+    return (lds_f4*)((__attribute__((address_space(3))) float*)Pw + ((mq * 4 + rg) * 64 + lane) * 4);
+  };
+
+  issue(0, Q0, O0);
+  if (threadIdx.x < 128) LD0[threadIdx.x] = fetch_ld(0);
+
+  // The loop both roles run: the same barriers in the same order.
+  auto run = [&](auto& tile) {
+    auto step = [&](int i, const uint8_t* Qc, const uint8_t* Oc, const float* LDc, uint8_t* Qn,
+                    uint8_t* On, float* LDn) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      float next_ld = 0.0f;
+      const bool more = i + 1 < n_items;
+      if (more) {
+        issue(i + 1, Qn, On);
+        if (threadIdx.x < 128) next_ld = fetch_ld(i + 1);
+      }
+      const int t = i % nqt;
+      if (t < 2) tile(std::true_type{}, first_q + t * 64, Qc, Oc, LDc);
+      else tile(std::false_type{}, first_q + t * 64, Qc, Oc, LDc);
+      if (more && threadIdx.x < 128) LDn[threadIdx.x] = next_ld;
+    };
+    int i = 0;
+    for (; i + 1 < n_items; i += 2) {
+      step(i, Q0, O0, LD0, Q1, O1, LD1);
+      step(i + 1, Q1, O1, LD1, Q0, O0, LD0);
+    }
+    if (i < n_items) step(i, Q0, O0, LD0, Q1, O1, LD1);
+  };
+
+  // dk or dv [dt][r]: key k0w + acc_row(r, h), d = dt * 32 + l32, to the
+  // partials ([split][token][k heads | v heads][d]) or as bf16 into dqkv.
+  auto write_out = [&](const f32x16 (&acc)[ND], int col_part, int col_out, float mul) {
+    if (part) {
+      const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
+      float* pb = part + static_cast<int64_t>(hs) * gridDim.y * S * W;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = tok0 + k0w + acc_row(r, h);
+          pb[row * W + col_part + dt * 32 + l32] = acc[dt][r] * mul;
+        }
+      return;
+    }
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = tok0 + k0w + acc_row(r, h);
+        dqkv[row * ld + col_out + dt * 32 + l32] = f32_to_bf16(acc[dt][r] * mul);
+      }
+  };
+
+  if (pwave) {
+    bf16x8 kf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      kf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + kj) * ld + kcol + s * 16 + h * 8);
+    f32x16 dv[ND];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) dv[dt] = f32x16{};
+    auto tile = [&](auto diagc, int qt0, const uint8_t* Qc, const uint8_t* Oc, const float* LDc) {
+      constexpr bool DIAG = decltype(diagc)::value;
+      bf16x8 pa[2][2];  // P as the dV MFMA's bf16 operand, per half and k16 step
+      {
+        f32x16 sacc[2] = {f32x16{}, f32x16{}};
+        bf16x8 qa[2];
+        qa[0] = rd_row(Qc, 0, 0);
+        // The two halves' products alternate, so that consecutive MFMAs do
+        // not wait on each other's accumulator.
+        auto sm = [&](auto idxc) {
+          constexpr int idx = decltype(idxc)::value, mq = idx & 1, s = idx >> 1;
+          if constexpr (idx + 1 < 2 * NS) qa[(idx + 1) & 1] = rd_row(Qc, (idx + 1) & 1, (idx + 1) >> 1);
+          __builtin_amdgcn_sched_barrier(0);
+          sacc[mq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[idx & 1], kf[s], sacc[mq], 0, 0, 0);
+        };
+        StaticFor<0, 2 * NS>::run(sm);
+#pragma unroll
+        for (int mq = 0; mq < 2; ++mq) {
+          const float4* l4 = reinterpret_cast<const float4*>(LDc + mq * 32 + 4 * h);
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {  // rows 8 gq + 4 h + 0..3 of the half: registers 4 gq..
+            const float4 lv = l4[2 * gq];
+            const float lq[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * gq + j;
+              float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[mq][r], scale_log2, -lq[j]));
+              if (DIAG && kj > qt0 + mq * 32 + acc_row(r, h)) p = 0.0f;
+              sacc[mq][r] = p;
+            }
+            *p_slot(mq, gq) = f32x4{sacc[mq][4 * gq], sacc[mq][4 * gq + 1], sacc[mq][4 * gq + 2],
+                                    sacc[mq][4 * gq + 3]};
+          }
+          pa[mq][0] = cvt8(sacc[mq], 0);
+          pa[mq][1] = cvt8(sacc[mq], 8);
+        }
+      }
+      __syncthreads();  // P to the dS waves
+      auto half = [&](auto mqc) {
+        constexpr int mq = decltype(mqc)::value;
+        bf16x8 ta[2];
+        ta[0] = rd_tr(Oc, 0, 2 * mq);
+        auto acc = [&](auto idxc) {
+          constexpr int idx = decltype(idxc)::value, ss = idx / ND, dt = idx % ND;
+          if constexpr (idx + 1 < 2 * ND) ta[(idx + 1) & 1] = rd_tr(Oc, (idx + 1) % ND, 2 * mq + (idx + 1) / ND);
+          __builtin_amdgcn_sched_barrier(0);
+          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[mq][ss], ta[idx & 1], dv[dt], 0, 0, 0);
+        };
+        StaticFor<0, 2 * ND>::run(acc);
+      };
+      half(std::integral_constant<int, 0>{});
+      half(std::integral_constant<int, 1>{});
+    };
+    run(tile);
+    write_out(dv, (Hkv + g) * D, vcol, 1.0f);
+  } else {
+    bf16x8 vf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      vf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + kj) * ld + vcol + s * 16 + h * 8);
+    f32x16 dk[ND];
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) dk[dt] = f32x16{};
+    auto tile = [&](auto diagc, int qt0, const uint8_t* Qc, const uint8_t* Oc, const float* LDc) {
+      f32x16 dp[2] = {f32x16{}, f32x16{}};
+      {
+        bf16x8 oa[2];
+        oa[0] = rd_row(Oc, 0, 0);
+        auto dm = [&](auto idxc) {
+          constexpr int idx = decltype(idxc)::value, mq = idx & 1, s = idx >> 1;
+          if constexpr (idx + 1 < 2 * NS) oa[(idx + 1) & 1] = rd_row(Oc, (idx + 1) & 1, (idx + 1) >> 1);
+          __builtin_amdgcn_sched_barrier(0);
+          dp[mq] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[idx & 1], vf[s], dp[mq], 0, 0, 0);
+        };
+        StaticFor<0, 2 * NS>::run(dm);
+      }
+      __syncthreads();  // P from the P waves
+      auto half = [&](auto mqc) {
+        constexpr int mq = decltype(mqc)::value;
+        bf16x8 tb[2];
+        tb[0] = rd_tr(Qc, 0, 2 * mq);
+        const float4* d4 = reinterpret_cast<const float4*>(LDc + 64 + mq * 32 + 4 * h);
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const f32x4 pv = *p_slot(mq, gq);
+          const float4 dv4 = d4[2 * gq];
+          const float pq[4] = {pv.x, pv.y, pv.z, pv.w}, dq[4] = {dv4.x, dv4.y, dv4.z, dv4.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dp[mq][4 * gq + j] = pq[j] * (dp[mq][4 * gq + j] - dq[j]);
+        }
+        const bf16x8 da[2] = {cvt8(dp[mq], 0), cvt8(dp[mq], 8)};
+        auto acc = [&](auto idxc) {
+          constexpr int idx = decltype(idxc)::value, ss = idx / ND, dt = idx % ND;
+          if constexpr (idx + 1 < 2 * ND) tb[(idx + 1) & 1] = rd_tr(Qc, (idx + 1) % ND, 2 * mq + (idx + 1) / ND);
+          __builtin_amdgcn_sched_barrier(0);
+          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da[ss], tb[idx & 1], dk[dt], 0, 0, 0);
+        };
+        StaticFor<0, 2 * ND>::run(acc);
+      };
+      half(std::integral_constant<int, 0>{});
+      half(std::integral_constant<int, 1>{});
+    };
+    run(tile);
+    write_out(dk, g * D, kcol, scale);
+  }
+}
+
 // dK, dV of head-split blocks: the sum of the partials in split order, as
 // bf16 into the k and v columns of dqkv. One thread per 4 consecutive values.
 __global__ __launch_bounds__(kThreads) void attn_bwd_kv_reduce(const float* __restrict__ part,
@@ -705,8 +960,12 @@ int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint1
                      dim3(kThreads), 0, s, dout, out, ldo, T, S, Hq, dsum);
   const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
   if (hsplit == 1) part = nullptr;
-  hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv * hsplit, B, S / QB), dim3(kThreads), 0, s, qkv, ld,
-                     dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
+  if constexpr (D == 128)
+    hipLaunchKernelGGL(attn_bwd_dkdv_pair<D>, dim3(Hkv * hsplit, B, S / QB), dim3(2 * kThreads), 0, s, qkv,
+                       ld, dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
+  else
+    hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv * hsplit, B, S / QB), dim3(kThreads), 0, s, qkv, ld,
+                       dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
   if (part) {
     const int64_t threads = T * W / 4;
     hipLaunchKernelGGL(attn_bwd_kv_reduce, dim3(static_cast<unsigned>((threads + kThreads - 1) / kThreads)),

@@ -38,14 +38,14 @@ from mround_amd.pipeline.runner import QuantizationRunner, RunSummary
 from mround_amd import kernels as K
 from mround_amd.planner import memory as M
 from mround_amd.planner.allocator import allocate_bits
-from mround_amd.planner.sensitivity import (gradient_source_for, mixed_budget_bits,
-                                            score_layer_options, scoring_batch_size, storage_bits)
+from mround_amd.planner.timing import predict_run_time
+from mround_amd.planner.sensitivity import (SENSITIVITY_SAMPLES, SENSITIVITY_SEQ_LEN, gradient_source_for,
+                                            mixed_budget_bits, score_layer_options, scoring_batch_size,
+                                            storage_bits)
 from mround_amd.schemes import (LOW_BIT_THRESHOLD, QuantScheme, ScaleInit, Symmetry,
                                 TuningConfig)
 
 RUN_RECORD = "mround_run.json"
-SENSITIVITY_SAMPLES = 128  # mround/planner/sensitivity.py:91-92
-SENSITIVITY_SEQ_LEN = 1024
 
 
 @dataclasses.dataclass(frozen=True)
@@ -439,6 +439,32 @@ def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
     return M.check_memory(shape, run, budget=budget)
 
 
+def predict_time(model: str | Path, *, bits: int = 4, group_size: int = 64,
+                 symmetry: Symmetry = Symmetry.SYMMETRIC, average_bits: float | None = None,
+                 candidate_bits: Sequence[int] = (2, 3, 4), sensitivity_gradients: str = "auto",
+                 remainder_bits: int | None = None, scoring_samples: int | None = None,
+                 scoring_seq_len: int | None = None, scheme: QuantScheme | None = None,
+                 tuning: TuningConfig | None = None, scale_init: ScaleInit | str | None = None,
+                 per_layer_recipe: bool = False, holdout_batches: int = 0):
+    """Predict the seconds the run :func:`quantize` would make takes on one
+    MI355X (``mround_amd.planner.timing``), from ``config.json`` alone
+    (mround/cli/main.py:590-624)."""
+    config = _read_config(model)
+    resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry,
+                                       average_bits=average_bits, candidate_bits=candidate_bits,
+                                       remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
+    tuning = tuning or TuningConfig()
+    shape, run = _run_shape(config, resolved, tuning, average_bits=average_bits, plan=None,
+                            widths=candidate_bits if average_bits is not None else (resolved.bits,),
+                            gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
+                            scoring_seq_len=scoring_seq_len, scoring_batch=None, dense_remainder=False,
+                            quantized_inputs=True, holdout_batches=holdout_batches)
+    return predict_run_time(shape, run, tuning, resolved.bits,
+                            candidate_bits=candidate_bits if average_bits is not None else (),
+                            per_layer_recipe=per_layer_recipe, scoring_samples=scoring_samples,
+                            scoring_seq_len=scoring_seq_len, gradient_source=sensitivity_gradients)
+
+
 def _load_tokens(m: DecoderModel, calibration, tuning: TuningConfig, seed: int, device) -> torch.Tensor:
     vocab = int(m.config["vocab_size"])
     if isinstance(calibration, torch.Tensor):
@@ -510,6 +536,12 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     memory = M.check_memory(mshape, rshape, budget=budget)
     if memory_check:
         M.require_fits(memory)
+    # and how long it will take on one MI355X: said, never enforced (mround/api.py:624-633)
+    timing = predict_run_time(mshape, rshape, tuning, resolved.bits,
+                              candidate_bits=candidate_bits if average_bits is not None and plan is None else (),
+                              per_layer_recipe=per_layer_recipe, scoring_samples=scoring_samples,
+                              scoring_seq_len=scoring_seq_len, gradient_source=sensitivity_gradients)
+    print(f"  {timing.describe()}", flush=True)
     on_gpu = torch.cuda.is_available() and str(device).startswith("cuda")
     held_before = 0
     if on_gpu:  # the run's own peak: what the process already holds is left out
@@ -581,6 +613,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         "skipped": skipped,
         "storage": {"bits_per_weight": storage.bits_per_weight, "compression": storage.compression},
         "seconds": seconds,
+        "time_check": timing.record(),
         "memory": {**memory.record(),
                    "peak_allocated": int(torch.cuda.max_memory_allocated(device)) - held_before
                    if on_gpu else None},

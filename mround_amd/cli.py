@@ -144,6 +144,12 @@ def main(argv=None) -> int:
                 average_bits=args.average_bits, candidate_bits=_widths(args.options),
                 remainder_bits=args.remainder_bits, tuning=_tuning(args), memory_budget=budget)
             print(f"  {check.explain()}")
+            timing = api.predict_time(
+                args.model, bits=args.bits, group_size=args.group_size,
+                symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
+                average_bits=args.average_bits, candidate_bits=_widths(args.options),
+                remainder_bits=args.remainder_bits, tuning=_tuning(args))
+            print(f"  {timing.describe()}")
             return 0 if check.fits else 1
         plan = None
         if args.plan:

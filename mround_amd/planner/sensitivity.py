@@ -20,6 +20,8 @@ from mround_amd.exceptions import SchemeError
 from mround_amd.planner.allocator import LayerOption
 from mround_amd.schemes import DEFAULT_EPS_FP32, QuantScheme
 
+SENSITIVITY_SAMPLES = 128  # mround/planner/sensitivity.py:91-92
+SENSITIVITY_SEQ_LEN = 1024
 SENSITIVITY_BATCH_TOKENS = 2048
 OWN_WIDTH_FROM_WEIGHTS = 2_500_000_000
 GRADIENT_SOURCES = ("auto", "own_width", "widest")

@@ -20,14 +20,20 @@ SMALL = dict(model_type="qwen2", hidden_size=512, num_attention_heads=8, num_key
              vocab_size=4096, tie_word_embeddings=True)
 
 
-@pytest.mark.parametrize("mixed", [False, True])
-def test_prediction_bounds_the_measured_peak(tmp_path, mixed):
-    print("case memory", mixed, flush=True, file=sys.stderr)
+# (mixed, quantized_inputs, holdout_batches): the block loop holds three
+# calibration streams with quantized inputs and the fused advance, two
+# without quantized inputs (inputs, targets) or with held-out batches.
+CASES = [(False, True, 0), (True, True, 0), (False, False, 0), (False, True, 1)]
+
+
+@pytest.mark.parametrize("mixed,quantized_inputs,holdout", CASES)
+def test_prediction_bounds_the_measured_peak(tmp_path, mixed, quantized_inputs, holdout):
+    print("case memory", mixed, quantized_inputs, holdout, flush=True, file=sys.stderr)
     src = write_random_checkpoint(tmp_path / "m", SMALL, seed=1)
     tuning = TuningConfig(iters=2, batch_size=4, n_samples=8, seq_len=256)
     kw = dict(average_bits=3.0, candidate_bits=(2, 4), scoring_samples=8, scoring_seq_len=257) if mixed else {}
     res = api.quantize(src, output_dir=tmp_path / "q", bits=4, symmetry=Symmetry.ASYMMETRIC, tuning=tuning,
-                       seed=2, **kw)
+                       seed=2, quantized_inputs=quantized_inputs, holdout_batches=holdout, **kw)
     rec = json.loads(res.config_path.read_text())["memory"]
     predicted = rec["peak"]
     measured = rec["peak_allocated"]

@@ -126,6 +126,7 @@ def test_cli_dry_run(tmp_path, capsys):
     write_random_checkpoint(tmp_path / "m", TINY)
     assert main(["quantize", str(tmp_path / "m"), "-o", str(tmp_path / "o"), "--dry-run",
                  "--memory-budget", "1000"]) == 0
-    assert "predicted peak" in capsys.readouterr().out
+    out = capsys.readouterr().out
+    assert "predicted peak" in out and "time: predicted" in out and "MI355X" in out
     assert main(["quantize", str(tmp_path / "m"), "-o", str(tmp_path / "o"), "--dry-run",
                  "--memory-budget", "0.000001"]) == 1

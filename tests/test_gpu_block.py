@@ -262,3 +262,63 @@ def test_fused_advance_equals_separate_score(lr):
         assert torch.equal(c0[k][0], c1[k][0]) and torch.equal(c0[k][1], c1[k][1]), k
     for n in LAYERS:
         assert torch.equal(w0[n], w1_[n]), n
+
+
+def _rtn32(w: torch.Tensor, bits: int) -> torch.Tensor:
+    qdq, _, _, _ = OQ.fake_quantize(w.float().numpy(), None, None, None, bits=bits, group_size=64,
+                                    mode="asym", dtype=np.float32)
+    return torch.from_numpy(qdq)
+
+
+# Measured on both shapes: loss within 2.8e-4, 6.2e-4, 2.0e-3 of float64 at 2, 3,
+# 4 bits; dL/dW' within 4.2e-2 normwise; flipped gradient mass below 4.4e-4.
+PRECISION_BARS = {2: (1e-3, 3e-2, 2e-4), 3: (2e-3, 4e-2, 5e-4), 4: (5e-3, 6e-2, 1e-3)}
+
+
+@pytest.mark.parametrize("key", ["smollm", "d128"])
+def test_objective_precision_by_width(key):
+    """How far the bf16-operand block objective sits from the exact one, by
+    code width, the way the runner forms it: targets from the engine's own
+    forward of the original weights, W' the fp32 round-to-nearest
+    reconstruction (rounded to bf16 by the engine), against float64 with the
+    exact W'. The block residual shrinks about 4x per bit while the bf16
+    rounding of W' and of the activations does not: at 2-4 bits the objective
+    and its gradient are within the bars below; at 8 bits the rounding is as
+    large as the residual (measured: loss 29-34 % high, dL/dW' 63-65 % off
+    normwise, 8 % of its mass of the wrong sign, of which W''s own bf16
+    rounding alone is +13 % of the loss), which the test records and bounds
+    only loosely."""
+    print("case objective precision", key, flush=True, file=sys.stderr)
+    shape, B, S, w, x = _problem(key, seed=1)
+    t64 = _oracle_forward(shape, B, S, w, x).reshape(B * S, -1)
+    eng = BlockEngine(shape, batch=B, seq_len=S, device=dev())
+    eng.set_block(_to_dev(w))
+    eng.load_dense({n: t.to(dev()) for n, t in w.linears.items()})
+    target = torch.empty(B * S, shape.hidden, device=dev())
+    eng.forward(x.to(dev()), target, save=False)
+    place = placements(shape)
+    for bits in (2, 3, 4, 8):
+        wq = {n: _rtn32(w.linears[n], bits) for n in LAYERS}
+        lin = {n: wq[n].double().requires_grad_(True) for n in LAYERS}
+        loss = ((_oracle_forward(shape, B, S, w, x, linears=lin).reshape(B * S, -1) - t64) ** 2).mean()
+        loss.backward()
+        ref_loss = float(loss.detach())
+        eng.load_dense({n: t.to(dev()) for n, t in wq.items()})
+        out = torch.empty(B * S, shape.hidden, device=dev())
+        eng.forward(x.to(dev()), out, save=True)
+        got = float(eng.loss(out, target, suppress=False, with_grad=True))
+        eng.backward()
+        rel_loss = abs(got - ref_loss) / ref_loss
+        rels, flips = [], []
+        for n in LAYERS:
+            ref = lin[n].grad
+            g = unplace(eng.dw[place[n].operand], ref.shape[0], place[n]).double().cpu()
+            rels.append(float((g - ref).norm() / ref.norm()))
+            flips.append(float(ref.abs()[torch.sign(g) != torch.sign(ref)].sum() / ref.abs().sum()))
+        print(f"  {bits} bits: loss {rel_loss:.2e}, dW' {max(rels):.2e}, flipped {max(flips):.2e}",
+              file=sys.stderr)
+        if bits in PRECISION_BARS:
+            b_loss, b_dw, b_flip = PRECISION_BARS[bits]
+            assert rel_loss <= b_loss and max(rels) <= b_dw and max(flips) <= b_flip, bits
+        else:
+            assert np.isfinite(got) and rel_loss < 0.6 and max(flips) < 0.2

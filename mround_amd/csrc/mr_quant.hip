@@ -64,7 +64,7 @@ struct RowMap {
   // fewer than 2^31 chunks, so chunk and row indices fit 31 bits.
   void prepare(int64_t cols) {
     cpr = static_cast<int>(cols / 8);
-    if (blk) {
+    if (blk && cpr > 0) {  // (narrower rows take the generic kernels, which divide)
       by_cpr = FastDiv::make(static_cast<uint32_t>(cpr));
       by_blk = FastDiv::make(static_cast<uint32_t>(blk));
     }

@@ -170,7 +170,7 @@ def test_zero_rows_and_validation():
                          QuantScheme(bits=4, group_size=64, scale_init="searched"))
 
 
-@pytest.mark.parametrize("shape", [(64, 512, 64), (96, 256, 32), (32, 200, -1)])
+@pytest.mark.parametrize("shape", [(64, 512, 64), (96, 256, 32), (32, 200, -1), (16, 4, -1)])
 def test_mapped_placement(shape):
     """W' rows placed in a stacked / interleaved buffer, gradients read back the same way."""
     from mround_amd import kernels as K

@@ -315,6 +315,8 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
  *   dgate = dact * u * silu'(g), dup = dact * silu(g), written interleaved to
  *   dgu [M, 2N] bf16 (same layout as gu). The MLX autodiff of the mlp's
  *   silu(g) * u and down linear (mround/pipeline/runner.py:920).
+ * Every operand, gu and dgu 16-byte aligned with leading dimensions
+ * multiples of 8; M % 8, N % 32 and K % 64 zero.
  */
 int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t ldd,
                        const void* Wd, int64_t ldw, const void* gu, int64_t ldgu, void* dgu,

@@ -243,13 +243,13 @@ template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int WM = BM / kWaveRows, WN = BN / (kWaves / kWaveRows);
   constexpr int TM = WM / 32, TN = WN / 32;
-  // Every epilogue but the SwiGLU backward feeds the MFMA with B as the first
-  // operand and A as the second, so that each accumulator holds C
-  // transposed: lane l then owns row l % 32 of its 32 x 32 block and, in
-  // register group gi, the 4 consecutive columns 8 gi + 4 (l / 32) .. + 3,
-  // which the epilogue writes to LDS as one 8- or 16-byte piece. (Every
-  // output element is the same k-ordered sum either way.)
-  constexpr bool SWAP = EPI != EPI_SWIGLU_BWD;
+  // Every epilogue feeds the MFMA with B as the first operand and A as the
+  // second, so that each accumulator holds C transposed: lane l then owns row
+  // l % 32 of its 32 x 32 block and, in register group gi, the 4 consecutive
+  // columns 8 gi + 4 (l / 32) .. + 3, which the epilogue writes to LDS as one
+  // 8- or 16-byte piece. (Every output element is the same k-ordered sum
+  // either way.)
+  constexpr bool SWAP = true;
   // Two LDS stages as four distinct arrays, indexed only with compile-time
   // stage numbers (the k loop below is unrolled by two), so that the waits
   // for the direct-to-LDS loads into one stage are not placed in front of the
@@ -523,42 +523,81 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
       }
     }
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
-    // acc is dact[row, col]; gate and up of act column col sit at interleaved
-    // columns (col / 32) * 64 + col % 32 and +32 of gu; dgu uses the same places.
-    // Tiles are visited with compile-time indices: the unrolled body is too
-    // large for the loop unroller, and a runtime tile index would move acc to
-    // scratch memory.
+    // acc is dact transposed (SWAP): lane l holds row l % 32 of block (i, j)
+    // and, in register group gi, act columns j 32 + 8 gi + 4 (l / 32) .. + 3.
+    // Each 32-row slice of the wave's dact (JH column blocks at a time) is
+    // staged as fp32 in the wave's LDS share; then a lane takes 8 consecutive
+    // act columns of one row: their gate and up values are one 16-byte load
+    // each from the saved interleaved gate/up (gate of act column c at
+    // (c / 32) 64 + c % 32, up 32 further), all of a slice's loads in flight
+    // before any is used, and dgate and dup leave as one 16-byte store each
+    // at the same places.
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    constexpr int REGION = (BM + BN) * ROW_BYTES * 2 / kWaves;
+    constexpr int JH = (32 * (TN * 32 * 4 + 16) <= REGION) ? TN : (32 * (2 * 32 * 4 + 16) <= REGION ? 2 : 1);
+    constexpr int PITCH = JH * 32 * 4 + 16;
+    constexpr int CH = JH * 32 / 8;  // 8-column pieces per staged row
+    constexpr int NIT = 32 * CH / 64;
+    static_assert(32 * PITCH <= REGION && TN % JH == 0 && NIT * 64 == 32 * CH, "staging does not fit");
+    uint8_t* arr = wave < 2 ? As0 : wave < 4 ? As1 : wave < 6 ? Bs0 : Bs1;
+    lds_u8* st = (lds_u8*)(arr + (wave & 1) * REGION);
     uint16_t* dgu = static_cast<uint16_t*>(p.C);
-    auto tile = [&](auto ij) {
-      constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
-      const int col = n0 + wn * WN + j * 32 + lcol;
-      const int gcol = (col >> 5) * 64 + (col & 31);
-      // Loads go to clamped (always valid) addresses without a branch so that
-      // all 32 of them are in flight together; only the stores are guarded.
-      const int gcol_c = min(col, p.N - 1);
-      const int gcol_l = (gcol_c >> 5) * 64 + (gcol_c & 31);
-      float g[16], u[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = min(m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3), p.M - 1);
-        const int64_t o = static_cast<int64_t>(row) * p.ldgu + gcol_l;
-        g[r] = bf16_to_f32(p.gu[o]);
-        u[r] = bf16_to_f32(p.gu[o + 32]);
-      }
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + lrow + (r & 3);
-        const float sg = sigmoid(g[r]);
-        const float da = acc[i][j][r];
-        const float dsilu = sg * (1.0f + g[r] * (1.0f - sg));
-        if (row < p.M && col < p.N) {
-          const int64_t od = static_cast<int64_t>(row) * p.ldc + gcol;
-          dgu[od] = f32_to_bf16(da * u[r] * dsilu);
-          dgu[od + 32] = f32_to_bf16(da * g[r] * sg);
+      for (int jb = 0; jb < TN / JH; ++jb) {
+#pragma unroll
+        for (int jj = 0; jj < JH; ++jj) {
+          const int j = jb * JH + jj;
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi)
+            *(__attribute__((address_space(3))) f32x4*)(st + lcol * PITCH + (jj * 32 + gi * 8 + lrow) * 4) =
+                f32x4{acc[i][j][4 * gi], acc[i][j][4 * gi + 1], acc[i][j][4 * gi + 2], acc[i][j][4 * gi + 3]};
+        }
+        // The same wave reads back what it wrote (LDS keeps a wave's accesses
+        // in order). Loads go to clamped (always valid) places; only the
+        // stores are guarded.
+        const int row0 = m0 + wm * WM + i * 32;
+        const int col0 = n0 + wn * WN + jb * JH * 32;
+        u32x4 gv[NIT], uv[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
+          const int row = min(row0 + r, p.M - 1), col = min(col0 + ch * 8, p.N - 8);
+          const int64_t o = static_cast<int64_t>(row) * p.ldgu + (col >> 5) * 64 + (col & 31);
+          gv[it] = *reinterpret_cast<const u32x4*>(p.gu + o);
+          uv[it] = *reinterpret_cast<const u32x4*>(p.gu + o + 32);
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
+          const int row = row0 + r, col = col0 + ch * 8;
+          const f32x4 d0 = *(__attribute__((address_space(3))) f32x4*)(st + r * PITCH + ch * 32);
+          const f32x4 d1 = *(__attribute__((address_space(3))) f32x4*)(st + r * PITCH + ch * 32 + 16);
+          const float da[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
+          float dg[8], du[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t gw = gv[it][e >> 1], uw = uv[it][e >> 1];
+            const float g = __uint_as_float((e & 1) ? (gw & 0xffff0000u) : (gw << 16));
+            const float u = __uint_as_float((e & 1) ? (uw & 0xffff0000u) : (uw << 16));
+            const float sg = sigmoid(g);
+            const float dsilu = sg * (1.0f + g * (1.0f - sg));
+            dg[e] = da[e] * u * dsilu;
+            du[e] = da[e] * g * sg;
+          }
+          if (row < p.M && col < p.N) {
+            const int64_t od = static_cast<int64_t>(row) * p.ldc + (col >> 5) * 64 + (col & 31);
+            *reinterpret_cast<u32x4*>(dgu + od) = u32x4{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]),
+                                                        pack_bf16x2(dg[4], dg[5]), pack_bf16x2(dg[6], dg[7])};
+            *reinterpret_cast<u32x4*>(dgu + od + 32) = u32x4{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]),
+                                                             pack_bf16x2(du[4], du[5]), pack_bf16x2(du[6], du[7])};
+          }
         }
       }
-    };
-    StaticFor<0, TM * TN>::run(tile);
+    }
   } else {  // EPI_STORE, EPI_RESID
     // The transposed accumulators (plus bias) are staged per 32-row slice and
     // JH column blocks in the wave's LDS share, then leave as 16-byte row
@@ -970,8 +1009,9 @@ int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t 
   if (!dd || !Wd || !gu || !dgu) return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: null operand");
   if (M % 8 || N % 32 || K % BK || K == 0)
     return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: M %% 8, N %% 32 and K %% %d must be 0", BK);
-  if (!ok16(dd, ldd) || !ok16(Wd, ldw))
-    return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: operands must be 16-byte aligned");
+  if (!ok16(dd, ldd) || !ok16(Wd, ldw) || !ok16(gu, ldgu) || !ok16(dgu, lddgu))
+    return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: operands and gu/dgu must be 16-byte aligned with leading "
+                "dimensions multiples of 8");
   if (ldd < K || ldw < N || lddgu < 2 * N || ldd > kMaxLd || ldw > kMaxLd)
     return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: bad leading dimension");
   if (ldgu != lddgu) return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: gu and dgu must share a layout");

@@ -48,23 +48,23 @@ from mround_amd.planner.sensitivity import SENSITIVITY_SAMPLES, SENSITIVITY_SEQ_
 
 __all__ = ["MACHINE", "RULE_VERSION", "SPREAD", "TimePrediction", "predict_run_time", "predict_time"]
 
-RULE_VERSION = "2026-12-02"
+RULE_VERSION = "2026-12-02.2"
 MACHINE = "one AMD Instinct MI355X"
 
 # Recorded over predicted seconds of the measurement runs (block loop and
 # scoring pass), lowest and highest.
-SPREAD = (0.81, 1.05)
+SPREAD = (0.83, 1.04)
 
 # Fitted constants (seconds), timing_runs.fit.
-_STEP = (6.250e-4, 4.797e-15, 1.285e-14)       # fixed, per token x block weight, per attention flop
-_OUTLIER = 2.785e-12                            # per loss element (tokens x hidden)
-_FORWARD = (1.520e-4, 1.549e-15, 3.693e-15)     # one forward over a batch: the same three terms
-_PIECE = 7.427e-4                               # a step's every piece past the first
-_FORWARD_PIECE = 1.716e-4                       # a forward's every piece past the first
-_SEARCH = (1.431e-2, 4.966e-10)                 # per block: fixed, per block weight
+_STEP = (4.024e-04, 4.510e-15, 1.540e-14)       # fixed, per token x block weight, per attention flop
+_OUTLIER = 9.044e-13                            # per loss element (tokens x hidden)
+_FORWARD = (8.495e-05, 1.426e-15, 4.737e-15)     # one forward over a batch: the same three terms
+_PIECE = 6.967e-04                               # a step's every piece past the first
+_FORWARD_PIECE = 1.458e-04                       # a forward's every piece past the first
+_SEARCH = (1.355e-02, 4.735e-10)                 # per block: fixed, per block weight
 _COMMIT = 5.0e-4                                # per block
-_SCORING = (1.027e-1, 3.515e-2, 1.014e-9, 1.542e-10)  # fixed, per block, per block weight, per head weight
-_OWN_WIDTH = 2.74
+_SCORING = (9.927e-02, 3.454e-02, 8.859e-10, 1.649e-10)  # fixed, per block, per block weight, per head weight
+_OWN_WIDTH = 2.79
 _SCORING_TOKENS = SENSITIVITY_SAMPLES * SENSITIVITY_SEQ_LEN
 
 _MINUTE = 60

@@ -117,13 +117,15 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("out", help="JSON file for the records")
     ap.add_argument("--first", type=int, default=0, help="start at this entry of RUNS")
+    ap.add_argument("--count", type=int, default=0, help="run this many entries (0: to the end)")
     args = ap.parse_args(argv)
     records = []
     with tempfile.TemporaryDirectory() as tmp:
         root = Path(tmp)
         # one small run first, so that library loading and first launches stay out of the records
         run_one(root, "smollm2-135m", 1, dict(bits=4, iters=5))
-        for name, blocks, settings in RUNS[args.first:]:
+        last = args.first + args.count if args.count > 0 else len(RUNS)
+        for name, blocks, settings in RUNS[args.first:last]:
             t0 = time.perf_counter()
             rec = run_one(root, name, blocks, settings)
             records.append(rec)

@@ -96,6 +96,10 @@ def test_host_validation_refuses_before_launch(lib):
     assert rc == -22 and b"16-byte" in lib.mr_last_error()
     rc = lib.mr_gemm_swiglu(64, 64, 64, P(256), 64, P(256), 64, P(256), 68, None, 0, None, 0, None)
     assert rc == -22 and b"16-byte" in lib.mr_last_error()
+    # the SwiGLU backward reads gu and writes dgu as 16-byte pieces
+    for gu, ldgu, dgu in ((P(264), 128, P(256)), (P(256), 128, P(264)), (P(256), 132, P(256))):
+        rc = lib.mr_gemm_swiglu_bwd(64, 64, 64, P(256), 64, P(256), 64, gu, ldgu, dgu, ldgu, None, 0, None)
+        assert rc == -22 and b"16-byte" in lib.mr_last_error()
     # a misaligned k-split workspace
     rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_F32, 64, None, None, 0, P(264), 1024,
                      None)

@@ -29,6 +29,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kThreads = 256;
 constexpr int QB = 128;  // queries per block (4 waves x 32)
 constexpr int KT = 64;   // keys per LDS tile
+// Transposed operands of the dK/dV pair kernel are read this many MFMAs
+// ahead (3 and 7 measured no faster: they spill).
+constexpr int kAhead = 1;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -645,13 +648,16 @@ __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2)
       __syncthreads();
       float next_ld = 0.0f;
       const bool more = i + 1 < n_items;
-      if (more) {
-        issue(i + 1, Qn, On);
-        if (threadIdx.x < 128) next_ld = fetch_ld(i + 1);
-      }
+      if (more && threadIdx.x < 128) next_ld = fetch_ld(i + 1);
+      // The next item's direct loads go out after the P barrier: issued with
+      // the S^T / dP^T products they slowed those products' operand reads
+      // (measured: 9 % of the kernel).
+      auto issue_next = [&]() {
+        if (more) issue(i + 1, Qn, On);
+      };
       const int t = i % nqt;
-      if (t < 2) tile(std::true_type{}, first_q + t * 64, Qc, Oc, LDc);
-      else tile(std::false_type{}, first_q + t * 64, Qc, Oc, LDc);
+      if (t < 2) tile(std::true_type{}, first_q + t * 64, Qc, Oc, LDc, issue_next);
+      else tile(std::false_type{}, first_q + t * 64, Qc, Oc, LDc, issue_next);
       if (more && threadIdx.x < 128) LDn[threadIdx.x] = next_ld;
     };
     int i = 0;
@@ -694,7 +700,7 @@ __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2)
     f32x16 dv[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) dv[dt] = f32x16{};
-    auto tile = [&](auto diagc, int qt0, const uint8_t* Qc, const uint8_t* Oc, const float* LDc) {
+    auto tile = [&](auto diagc, int qt0, const uint8_t* Qc, const uint8_t* Oc, const float* LDc, auto& issue_next) {
       constexpr bool DIAG = decltype(diagc)::value;
       bf16x8 pa[2][2];  // P as the dV MFMA's bf16 operand, per half and k16 step
       {
@@ -732,15 +738,21 @@ __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
       }
       __syncthreads();  // P to the dS waves
+      issue_next();
       auto half = [&](auto mqc) {
         constexpr int mq = decltype(mqc)::value;
-        bf16x8 ta[2];
-        ta[0] = rd_tr(Oc, 0, 2 * mq);
+        // dO^T operands read kAhead MFMAs ahead through a ring of registers
+        bf16x8 ta[kAhead + 1];
+        auto pre = [&](auto xc) {
+          constexpr int x = decltype(xc)::value;
+          ta[x] = rd_tr(Oc, x % ND, 2 * mq + x / ND);
+        };
+        StaticFor<0, kAhead>::run(pre);
         auto acc = [&](auto idxc) {
-          constexpr int idx = decltype(idxc)::value, ss = idx / ND, dt = idx % ND;
-          if constexpr (idx + 1 < 2 * ND) ta[(idx + 1) & 1] = rd_tr(Oc, (idx + 1) % ND, 2 * mq + (idx + 1) / ND);
+          constexpr int idx = decltype(idxc)::value, ss = idx / ND, dt = idx % ND, nx = idx + kAhead;
+          if constexpr (nx < 2 * ND) ta[nx % (kAhead + 1)] = rd_tr(Oc, nx % ND, 2 * mq + nx / ND);
           __builtin_amdgcn_sched_barrier(0);
-          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[mq][ss], ta[idx & 1], dv[dt], 0, 0, 0);
+          dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[mq][ss], ta[idx % (kAhead + 1)], dv[dt], 0, 0, 0);
         };
         StaticFor<0, 2 * ND>::run(acc);
       };
@@ -757,7 +769,7 @@ __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2)
     f32x16 dk[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) dk[dt] = f32x16{};
-    auto tile = [&](auto diagc, int qt0, const uint8_t* Qc, const uint8_t* Oc, const float* LDc) {
+    auto tile = [&](auto diagc, int qt0, const uint8_t* Qc, const uint8_t* Oc, const float* LDc, auto& issue_next) {
       f32x16 dp[2] = {f32x16{}, f32x16{}};
       {
         bf16x8 oa[2];
@@ -771,10 +783,17 @@ __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2)
         StaticFor<0, 2 * NS>::run(dm);
       }
       __syncthreads();  // P from the P waves
+      issue_next();
       auto half = [&](auto mqc) {
         constexpr int mq = decltype(mqc)::value;
-        bf16x8 tb[2];
-        tb[0] = rd_tr(Qc, 0, 2 * mq);
+        // Q^T operands read kAhead MFMAs ahead through a ring of registers;
+        // the first ones go out before the dS arithmetic, which covers them
+        bf16x8 tb[kAhead + 1];
+        auto pre = [&](auto xc) {
+          constexpr int x = decltype(xc)::value;
+          tb[x] = rd_tr(Qc, x % ND, 2 * mq + x / ND);
+        };
+        StaticFor<0, kAhead>::run(pre);
         const float4* d4 = reinterpret_cast<const float4*>(LDc + 64 + mq * 32 + 4 * h);
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
@@ -786,10 +805,10 @@ __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
         const bf16x8 da[2] = {cvt8(dp[mq], 0), cvt8(dp[mq], 8)};
         auto acc = [&](auto idxc) {
-          constexpr int idx = decltype(idxc)::value, ss = idx / ND, dt = idx % ND;
-          if constexpr (idx + 1 < 2 * ND) tb[(idx + 1) & 1] = rd_tr(Qc, (idx + 1) % ND, 2 * mq + (idx + 1) / ND);
+          constexpr int idx = decltype(idxc)::value, ss = idx / ND, dt = idx % ND, nx = idx + kAhead;
+          if constexpr (nx < 2 * ND) tb[nx % (kAhead + 1)] = rd_tr(Qc, nx % ND, 2 * mq + nx / ND);
           __builtin_amdgcn_sched_barrier(0);
-          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da[ss], tb[idx & 1], dk[dt], 0, 0, 0);
+          dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da[ss], tb[idx % (kAhead + 1)], dk[dt], 0, 0, 0);
         };
         StaticFor<0, 2 * ND>::run(acc);
       };

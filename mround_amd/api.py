@@ -32,7 +32,7 @@ from mround_amd.exceptions import (ArchitectureError, CalibrationError, SchemeEr
                                    UnsupportedSchemeError)
 from mround_amd.formats.mlx_export import (MLX_GROUP_SIZES, QuantizedLayer, export_mlx, narrow_codes,
                                            require_mlx_representable)
-from mround_amd.pipeline.block import LAYERS
+from mround_amd.pipeline.block import LAYERS, aligned_length
 from mround_amd.pipeline.checkpoint import DecoderModel, block_shape, dense_tensors, load_model
 from mround_amd.pipeline.runner import QuantizationRunner, RunSummary
 from mround_amd import kernels as K
@@ -329,12 +329,21 @@ def calibration_tokens(vocab: int, n_samples: int, seq_len: int, *, seed: int, d
 
 def _entrance(model: DecoderModel, tokens: torch.Tensor, batch_size: int) -> list[torch.Tensor]:
     """The block-0 input stream: embedding rows in float32 (``mr_embed_rows``),
-    one ``[batch * seq_len, hidden]`` tensor per batch."""
+    one ``[batch * rows, hidden]`` tensor per batch, ``rows`` being the
+    sequence length rounded up to a multiple of 128 and each sequence's rows
+    past its tokens zero (padding the block engine keeps out of the loss)."""
+    n_seq, length = tokens.shape
+    rows = aligned_length(length)
     out = []
-    for i in range(0, tokens.shape[0], batch_size):
-        ids = tokens[i:i + batch_size].reshape(-1).to(torch.int32)
+    for i in range(0, n_seq, batch_size):
+        ids = tokens[i:i + batch_size]
+        if rows != length:
+            ids = torch.nn.functional.pad(ids, (0, rows - length))  # token 0 at the padding rows
+        ids = ids.reshape(-1).to(torch.int32)
         x = torch.empty(ids.numel(), model.embed.shape[1], dtype=torch.float32, device=model.embed.device)
         K.embed_rows(model.embed, ids, x)
+        if rows != length:
+            x.view(-1, rows, x.shape[1])[:, length:].zero_()
         out.append(x)
     return out
 

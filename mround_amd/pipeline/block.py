@@ -42,6 +42,14 @@ LAYERS = ("mlp.down_proj", "mlp.gate_proj", "mlp.up_proj", "self_attn.k_proj",
           "self_attn.o_proj", "self_attn.q_proj", "self_attn.v_proj")
 QKV = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")
 SWIGLU_ROWS = 32  # gate/up interleave period in the fused operand
+SEQ_ALIGN = 128  # the attention kernels' query/key tile: rows per sequence are a multiple
+
+
+def aligned_length(n: int) -> int:
+    """Rows per sequence the engine runs for sequences of ``n`` tokens: ``n``
+    rounded up to the attention tile. The rows past ``n`` are padding at the
+    end of each sequence, which the causal mask keeps out of every real row."""
+    return -(-int(n) // SEQ_ALIGN) * SEQ_ALIGN
 
 
 @dataclass(frozen=True)
@@ -225,12 +233,21 @@ def rope_table(seq_len: int, head_dim: int, theta: float, device, scaling: tuple
 
 class BlockEngine:
     """Forward, loss and backward of one block over ``batch`` sequences of
-    ``seq_len`` tokens, with every buffer allocated once."""
+    ``seq_len`` rows, with every buffer allocated once.
+
+    ``real_len`` (default ``seq_len``) is how many of a sequence's rows are
+    tokens; the rest are padding at its end (``aligned_length``). Causal
+    attention keeps padding rows out of every token row, and ``loss`` counts
+    token rows only, so the loss and every gradient are those of the
+    ``real_len``-token sequences."""
 
     def __init__(self, shape: BlockShape, *, batch: int, seq_len: int, device,
-                 extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> None:
+                 extra_gemms: tuple[tuple[int, int, int], ...] = (), real_len: int | None = None) -> None:
         shape.validate(seq_len)
         self.shape, self.batch, self.seq_len = shape, batch, seq_len
+        self.real_len = seq_len if real_len is None else int(real_len)
+        if not 1 <= self.real_len <= seq_len:
+            raise ArchitectureError(f"{self.real_len} tokens do not fit sequences of {seq_len} rows")
         self.device = torch.device(device)
         T, h, mlp = batch * seq_len, shape.hidden, shape.intermediate
         self.tokens = T
@@ -401,9 +418,17 @@ class BlockEngine:
         """Reconstruction loss of one batch (device scalar), and dL/dout when asked:
         mean squared error, or with the top 0.1 % of |residuals| excluded
         (mround/core/losses.py:42-107). A piece of a batch passes the whole
-        batch's element count as ``denom`` and, with the outlier rule, the
-        whole batch's ``threshold`` (``piece_loss``, mround/core/losses.py:110-130)."""
-        n = out.numel()
+        batch's element count (``real_elements``) as ``denom`` and, with the
+        outlier rule, the whole batch's ``threshold`` (``piece_loss``,
+        mround/core/losses.py:110-130). With padded sequences the padding rows
+        of ``out`` take ``target``'s values first: their residuals are zero,
+        so they add nothing to the loss or its gradient and, lying below every
+        kept magnitude, leave the k-th largest |residual| unchanged."""
+        if self.real_len < self.seq_len:
+            S, r = self.seq_len, self.real_len
+            n_seq = out.shape[0] // S
+            out.view(n_seq, S, -1)[:, r:].copy_(target.view(n_seq, S, -1)[:, r:])
+        n = self.real_elements(out)
         denom = n if denom is None else denom
         grad = self.grad_out if with_grad else None
         if suppress and threshold is not None:
@@ -416,6 +441,15 @@ class BlockEngine:
             K.loss_mse(out, target, denom=denom, loss_out=self.loss_val, grad_out=grad,
                        workspace=self.loss_ws)
         return self.loss_val
+
+    def real_elements(self, t: torch.Tensor) -> int:
+        """Elements of the token rows of ``t`` (whole sequences of ``seq_len`` rows)."""
+        return t.numel() // self.seq_len * self.real_len
+
+    def zero_padding(self, t: torch.Tensor) -> None:
+        """Clear the padding rows of ``t`` (whole sequences of ``seq_len`` rows)."""
+        if self.real_len < self.seq_len:
+            t.view(t.shape[0] // self.seq_len, self.seq_len, -1)[:, self.real_len:].zero_()
 
     # --------------------------------------------------------------- backward --
     def backward(self, dx_out: torch.Tensor | None = None, *, accumulate: bool = False) -> None:

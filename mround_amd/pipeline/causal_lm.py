@@ -47,16 +47,13 @@ import torch
 from mround_amd import kernels as K
 from mround_amd.core.quantizer import mode_of
 from mround_amd.exceptions import ArchitectureError, CalibrationError
-from mround_amd.pipeline.block import LAYERS, BlockEngine, place, placements
+from mround_amd.pipeline.block import LAYERS, BlockEngine, aligned_length, place, placements
 from mround_amd.schemes import DEFAULT_EPS_FP32, QuantScheme
-
-SEQ_ALIGN = 128
 
 
 def padded_length(seq_len: int) -> int:
     """Positions the engine runs for sequences of ``seq_len`` tokens."""
-    n_in = seq_len - 1
-    return -(-n_in // SEQ_ALIGN) * SEQ_ALIGN
+    return aligned_length(seq_len - 1)
 
 
 class CausalLM:

@@ -23,7 +23,8 @@ from mround_amd.core.scale_search import search_scales
 from mround_amd.core.signsgd import LinearDecay
 from mround_amd.exceptions import ArchitectureError, CalibrationError
 from mround_amd.formats.mlx_export import QuantizedLayer
-from mround_amd.pipeline.block import LAYERS, BlockEngine, BlockShape, BlockWeights, placements, unplace
+from mround_amd.pipeline.block import (LAYERS, BlockEngine, BlockShape, BlockWeights, aligned_length, placements,
+                                       unplace)
 from mround_amd.pipeline.block import place as place_rows
 from mround_amd.schemes import DEFAULT_EPS_FP32, QuantScheme, ScaleInit, TuningConfig
 
@@ -165,6 +166,9 @@ class QuantizationRunner:
         # taken from the advance pass (see run); False scores separately.
         self.fused_advance = fused_advance
         self._engines: dict = {}
+        # rows per sequence in the streams: seq_len rounded up to the attention
+        # tile, the rows past seq_len padding (see BlockEngine)
+        self.rows = aligned_length(tuning.seq_len)
 
     def _scheme_for(self, path: str, overrides: Mapping[str, QuantScheme] | None) -> QuantScheme:
         if overrides is None:
@@ -175,27 +179,27 @@ class QuantizationRunner:
         """The block engine for this geometry, built once per run: for a batch
         of ``tokens`` tokens, or for its largest piece when steps run in
         pieces (``TuningConfig.micro_batches``)."""
-        seq = self.tuning.seq_len
+        seq = self.rows
         if tokens % seq:
-            raise CalibrationError(f"a batch of {tokens} tokens is not whole sequences of {seq}")
+            raise CalibrationError(f"a batch of {tokens} rows is not whole sequences of {seq}")
         n_seq = tokens // seq
         capacity = max(hi - lo for lo, hi in piece_bounds(n_seq, self.tuning.micro_batches))
         key = (shape, capacity, str(device))
         eng = self._engines.get(key)
         if eng is None:
-            eng = BlockEngine(shape, batch=capacity, seq_len=seq, device=device)
+            eng = BlockEngine(shape, batch=capacity, seq_len=seq, device=device, real_len=self.tuning.seq_len)
             self._engines = {key: eng}
         return eng
 
     def _pieces(self, x: torch.Tensor) -> list[tuple[int, int]]:
-        """Token row ranges of a batch's pieces."""
-        seq = self.tuning.seq_len
+        """Row ranges of a batch's pieces."""
+        seq = self.rows
         return [(lo * seq, hi * seq) for lo, hi in piece_bounds(x.shape[0] // seq, self.tuning.micro_batches)]
 
     def _forward(self, eng: BlockEngine, x: torch.Tensor, out: torch.Tensor) -> None:
         """``out = block(x)`` for a whole batch (no activations kept), a piece at
         a time when the engine holds pieces; ``out`` may be ``x``."""
-        seq = self.tuning.seq_len
+        seq = self.rows
         for lo, hi in self._pieces(x):
             eng.set_sequences((hi - lo) // seq)
             eng.forward(x[lo:hi], out[lo:hi], save=False)
@@ -206,8 +210,10 @@ class QuantizationRunner:
         """Quantize every block in place (mround/pipeline/runner.py:493-625).
 
         ``entrance`` holds the first block's input hidden states, one float32
-        ``[batch * seq_len, hidden]`` device tensor per calibration batch; the
-        list is consumed (its tensors are overwritten by the streams).
+        ``[batch * rows, hidden]`` device tensor per calibration batch, where
+        ``rows`` (``self.rows``) is ``seq_len`` rounded up to a multiple of 128
+        and each sequence's rows past ``seq_len`` are padding; the list is
+        consumed (its tensors are overwritten by the streams).
         """
         started = time.perf_counter()
         if not entrance:
@@ -397,11 +403,13 @@ class QuantizationRunner:
                "x2": torch.zeros(s.hidden, device=dev), "act": torch.zeros(s.intermediate, device=dev)}
         eng.load_dense(block.weights.linears)
         scratch = torch.empty_like(inputs[0])
-        seq = self.tuning.seq_len
+        seq = self.rows
         for x in inputs:
             for lo, hi in self._pieces(x):
                 eng.set_sequences((hi - lo) // seq)
                 eng.forward(x[lo:hi], scratch[lo:hi], save=False)
+                for t in (eng.x1, eng.attn, eng.x2, eng.act):
+                    eng.zero_padding(t)  # token rows only
                 K.colsumsq(eng.x1, imp["x1"])
                 K.colsumsq(eng.attn, imp["attn"])
                 K.colsumsq(eng.x2, imp["x2"])
@@ -489,14 +497,14 @@ class QuantizationRunner:
             loss_out.copy_(eng.loss(scratch, target, suppress=suppress, with_grad=True))
             eng.backward()
             return
-        n = x.numel()
+        n = eng.real_elements(x)
         threshold = None
         if suppress:
             self._forward(eng, x, scratch)
             eng.loss(scratch, target, suppress=True, with_grad=False)
             threshold = eng.threshold
         loss_out.zero_()
-        seq = self.tuning.seq_len
+        seq = self.rows
         for i, (lo, hi) in enumerate(pieces):
             eng.set_sequences((hi - lo) // seq)
             eng.forward(x[lo:hi], scratch[lo:hi], save=True)

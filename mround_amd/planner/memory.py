@@ -38,7 +38,7 @@ from mround_amd.exceptions import ArchitectureError, MemoryBudgetError
 
 GIB = 1 << 30
 LOSS_WORKSPACE = 401_424  # mr_loss_workspace_bytes
-SEQ_ALIGN = 128
+SEQ_ALIGN = 128  # block.SEQ_ALIGN (this module imports no torch at load time)
 _DTYPE_BYTES = {"bfloat16": 2, "float16": 2, "float32": 4}
 
 
@@ -191,6 +191,11 @@ class MemoryPrediction:
         return {"stages": dict(self.stages), "peak": self.peak, "peak_stage": self.stage}
 
 
+def aligned_rows(n: int) -> int:
+    """Rows per sequence of ``n`` positions (``block.aligned_length``)."""
+    return -(-n // SEQ_ALIGN) * SEQ_ALIGN
+
+
 def _groups(m: ModelShape, gs: int) -> int:
     return sum(o * (i // gs if gs > 0 else 1) for o, i in m.layer_shapes())
 
@@ -201,8 +206,7 @@ def predict_memory(m: ModelShape, run: RunShape) -> MemoryPrediction:
     stages = {"load": base}
     L, h = m.layers, m.hidden
     if run.mixed:
-        n_in = run.scoring_seq_len - 1
-        S = -(-n_in // SEQ_ALIGN) * SEQ_ALIGN
+        S = aligned_rows(run.scoring_seq_len - 1)
         T = run.scoring_batch * S
         Vp = -(-m.vocab // 64) * 64
         lm = (engine_bytes(m, T, S, input_grads=True, extra_gemms=((T, Vp, h), (T, h, Vp)))
@@ -216,14 +220,15 @@ def predict_memory(m: ModelShape, run: RunShape) -> MemoryPrediction:
             grids = per_width * (run.widths if run.gradient_source == "widest" else 1)
         tokens = run.scoring_samples * run.scoring_seq_len * 8
         stages["scoring"] = base + lm + grids + tokens + run.n_samples * run.seq_len * 8
-    T = run.batch_size * run.seq_len
-    streams = run.streams * run.n_samples * run.seq_len * h * 4
+    S = aligned_rows(run.seq_len)  # rows per sequence in the streams and the engine
+    T = run.batch_size * S
+    streams = run.streams * run.n_samples * S * h * 4
     groups = _groups(m, run.group_size)
     learn = m.block_weights * 4 * 2 + groups * 4 * 4 + (groups * 4 if run.searched else 0)
     committed = L * (m.block_weights + groups * 8)
     transient = m.largest_layer * (1 + 4) + T * h * 4
-    piece = run.piece_sequences * run.seq_len
-    stages["blocks"] = (base + run.n_samples * run.seq_len * 8 + streams + engine_bytes(m, piece, run.seq_len)
+    piece = run.piece_sequences * S
+    stages["blocks"] = (base + run.n_samples * run.seq_len * 8 + streams + engine_bytes(m, piece, S)
                         + learn + committed + transient)
     rem = 0
     if not run.dense_remainder:

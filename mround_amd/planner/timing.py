@@ -43,7 +43,7 @@ import dataclasses
 from collections.abc import Collection
 from typing import Any
 
-from mround_amd.planner.memory import ModelShape, RunShape
+from mround_amd.planner.memory import ModelShape, RunShape, aligned_rows
 from mround_amd.planner.sensitivity import SENSITIVITY_SAMPLES, SENSITIVITY_SEQ_LEN, gradient_source_for
 
 __all__ = ["MACHINE", "RULE_VERSION", "SPREAD", "TimePrediction", "predict_run_time", "predict_time"]
@@ -122,7 +122,9 @@ class TimePrediction:
 
 
 def _work(model: ModelShape, batch: int, seq_len: int) -> tuple[float, float]:
-    """(tokens x block weights, attention forward flops) of one batch."""
+    """(tokens x block weights, attention forward flops) of one batch, over the
+    rows the engine runs (sequences padded to the attention tile)."""
+    seq_len = aligned_rows(seq_len)
     tokens = batch * seq_len
     attention = 4.0 * batch * seq_len * seq_len / 2 * model.heads * model.head_dim
     return tokens * model.block_weights, attention
@@ -142,7 +144,7 @@ def predict_time(model: ModelShape, run: RunShape, *, iters: int, outlier_rule: 
     forward = _FORWARD[0] + _FORWARD[1] * tw + _FORWARD[2] * att + (pieces - 1) * _FORWARD_PIECE
     step = _STEP[0] + _STEP[1] * tw + _STEP[2] * att + (pieces - 1) * _PIECE
     if outlier_rule:
-        step += _OUTLIER * run.batch_size * run.seq_len * model.hidden
+        step += _OUTLIER * run.batch_size * aligned_rows(run.seq_len) * model.hidden
         if pieces > 1:
             step += forward
     batches = max(1, run.n_samples // run.batch_size)

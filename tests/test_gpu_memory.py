@@ -20,17 +20,19 @@ SMALL = dict(model_type="qwen2", hidden_size=512, num_attention_heads=8, num_key
              vocab_size=4096, tie_word_embeddings=True)
 
 
-# (mixed, quantized_inputs, holdout_batches): the block loop holds three
-# calibration streams with quantized inputs and the fused advance, two
-# without quantized inputs (inputs, targets) or with held-out batches.
-CASES = [(False, True, 0), (True, True, 0), (False, False, 0), (False, True, 1)]
+# (mixed, quantized_inputs, holdout_batches, seq_len): the block loop holds
+# three calibration streams with quantized inputs and the fused advance, two
+# without quantized inputs (inputs, targets) or with held-out batches; 200
+# tokens run on sequences padded to 256 rows.
+CASES = [(False, True, 0, 256), (True, True, 0, 256), (False, False, 0, 256), (False, True, 1, 256),
+         (False, True, 0, 200)]
 
 
-@pytest.mark.parametrize("mixed,quantized_inputs,holdout", CASES)
-def test_prediction_bounds_the_measured_peak(tmp_path, mixed, quantized_inputs, holdout):
-    print("case memory", mixed, quantized_inputs, holdout, flush=True, file=sys.stderr)
+@pytest.mark.parametrize("mixed,quantized_inputs,holdout,seq_len", CASES)
+def test_prediction_bounds_the_measured_peak(tmp_path, mixed, quantized_inputs, holdout, seq_len):
+    print("case memory", mixed, quantized_inputs, holdout, seq_len, flush=True, file=sys.stderr)
     src = write_random_checkpoint(tmp_path / "m", SMALL, seed=1)
-    tuning = TuningConfig(iters=2, batch_size=4, n_samples=8, seq_len=256)
+    tuning = TuningConfig(iters=2, batch_size=4, n_samples=8, seq_len=seq_len)
     kw = dict(average_bits=3.0, candidate_bits=(2, 4), scoring_samples=8, scoring_seq_len=257) if mixed else {}
     res = api.quantize(src, output_dir=tmp_path / "q", bits=4, symmetry=Symmetry.ASYMMETRIC, tuning=tuning,
                        seed=2, quantized_inputs=quantized_inputs, holdout_batches=holdout, **kw)

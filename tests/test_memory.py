@@ -10,8 +10,8 @@ import torch
 
 from mround_amd import api
 from mround_amd.cli import GEOMETRIES, main
-from mround_amd.exceptions import MemoryBudgetError
-from mround_amd.pipeline.block import BlockEngine
+from mround_amd.exceptions import ArchitectureError, MemoryBudgetError
+from mround_amd.pipeline.block import BlockEngine, aligned_length
 from mround_amd.pipeline.causal_lm import CausalLM, padded_length
 from mround_amd.pipeline.checkpoint import block_shape, load_model, write_random_checkpoint
 from mround_amd.planner import memory as M
@@ -94,6 +94,27 @@ def test_blocks_stage_counts_the_calibration_streams():
     assert with_q - blocks(holdout_batches=1) == one
     assert with_q - blocks(half=True) == one
     assert blocks(quantized_inputs=False) == blocks(quantized_inputs=False, holdout_batches=2)
+
+
+def test_a_length_off_the_tile_counts_padded_rows():
+    """Sequences of 200 tokens run on 256 rows each: the streams and the
+    engine are those of 256-token sequences, the calibration token ids those
+    of 200; the engine the runner builds for them is the formula's."""
+    m = M.ModelShape.from_config(GEOMETRIES["qwen2.5-0.5b"])
+    run = lambda L: M.RunShape(n_samples=8, seq_len=L, batch_size=4, group_size=64)  # noqa: E731
+    padded, aligned = M.predict_memory(m, run(200)), M.predict_memory(m, run(256))
+    assert aligned.stages["blocks"] - padded.stages["blocks"] == 8 * (256 - 200) * 8
+    assert M.aligned_rows(200) == aligned_length(200) == 256 and M.aligned_rows(256) == 256
+    eng = BlockEngine(block_shape(GEOMETRIES["smollm2-135m"]), batch=2, seq_len=aligned_length(200),
+                      device="cpu", real_len=200)
+    assert _bytes(eng) == M.engine_bytes(M.ModelShape.from_config(GEOMETRIES["smollm2-135m"]), 512, 256)
+
+
+def test_engine_refuses_more_tokens_than_rows():
+    with pytest.raises(ArchitectureError):
+        BlockEngine(block_shape(GEOMETRIES["smollm2-135m"]), batch=1, seq_len=128, device="cpu", real_len=129)
+    with pytest.raises(ArchitectureError):
+        BlockEngine(block_shape(GEOMETRIES["smollm2-135m"]), batch=1, seq_len=200, device="cpu")
 
 
 def test_micro_batches_shrink_the_engine():

@@ -335,6 +335,33 @@ int mr_rmsnorm_bwd(const float* dy, const float* h, const float* w, const float*
                    void* stream);
 
 /*
+ * Split-precision operands: the reference's remedy for the block objective's
+ * subtraction of two block outputs (mround DOCUMENTATION.md:885-925, three
+ * products A_hi B_hi + A_hi B_lo + A_lo B_hi), which its code documents but
+ * does not ship; these have no counterpart in the reference's code. An fp32
+ * value y is carried as hi = bf16(y) and lo = bf16(y - hi). A product runs as
+ * one bf16 GEMM over K' = 3K with A' = [A_hi | A_hi | A_lo] (order 0, for
+ * activations) and B' = [B_hi | B_lo | B_hi] (order 1, for weights) along K.
+ *
+ * mr_rmsnorm_fwd_split: mr_rmsnorm_fwd with y also written split, order 0,
+ *   into rows of 3H bf16 (y_split); y_bf16 (hi alone) and rstd_out optional.
+ *   H a multiple of 4 up to 16384, h and w 16-byte aligned, outputs 8-byte.
+ * mr_split_bf16: fp32 rows [rows, cols] (ld_src) into split rows (ld_dst >=
+ *   3 cols) in the given order, hi alone into plain (ld_plain) when given;
+ *   cols and the leading dimensions multiples of 4.
+ * mr_swiglu_split: act = silu(g) u from fp32 gate/up rows [T, 2N] interleaved
+ *   every 32 columns (the gate/up GEMM's layout), written split (order 0,
+ *   rows of 3N), hi alone into act [T, N], and the gate/up values in bf16
+ *   into gu [T, 2N] for the backward; N a multiple of 32.
+ */
+int mr_rmsnorm_fwd_split(const float* h, const float* w, int64_t T, int64_t H, float eps, void* y_split,
+                         void* y_bf16, float* rstd_out, void* stream);
+int mr_split_bf16(const float* src, int64_t ld_src, int64_t rows, int64_t cols, int order, void* dst,
+                  int64_t ld_dst, void* plain, int64_t ld_plain, void* stream);
+int mr_swiglu_split(const float* gu32, int64_t T, int64_t N, void* act_split, void* act, void* gu,
+                    void* stream);
+
+/*
  * Rotary embedding (non-interleaved halves) in place on the first n_heads
  * heads of rows of x (bf16, leading dimension ld), position = row % S, with
  * cos/sin from cos_sin [S, head_dim/2, 2] fp32; backward = 1 applies the

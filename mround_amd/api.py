@@ -405,7 +405,7 @@ def _read_config(model: str | Path) -> dict[str, Any]:
 
 def _run_shape(config, resolved: QuantScheme, tuning: TuningConfig, *, average_bits, plan, widths,
                gradient_source, scoring_samples, scoring_seq_len, scoring_batch, dense_remainder,
-               quantized_inputs, holdout_batches=0) -> tuple[M.ModelShape, M.RunShape]:
+               quantized_inputs, holdout_batches=0, split_precision=False) -> tuple[M.ModelShape, M.RunShape]:
     shape = M.ModelShape.from_config(config)
     mixed = average_bits is not None and plan is None
     samples = SENSITIVITY_SAMPLES if scoring_samples is None else int(scoring_samples)
@@ -418,7 +418,8 @@ def _run_shape(config, resolved: QuantScheme, tuning: TuningConfig, *, average_b
                      quantized_inputs=quantized_inputs, mixed=mixed, widths=len(widths),
                      gradient_source=source, scoring_samples=samples, scoring_seq_len=sequence,
                      scoring_batch=batch, dense_remainder=dense_remainder, holdout_batches=holdout_batches,
-                     micro_batches=tuning.micro_batches, half=str(config.get("torch_dtype")) == "float16")
+                     micro_batches=tuning.micro_batches, half=str(config.get("torch_dtype")) == "float16",
+                     split=bool(split_precision))
     return shape, run
 
 
@@ -430,7 +431,8 @@ def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
                    scoring_batch_size: int | None = None, scheme: QuantScheme | None = None,
                    tuning: TuningConfig | None = None, scale_init: ScaleInit | str | None = None,
                    quantized_inputs: bool = True, holdout_batches: int = 0,
-                   memory_budget: int | None = None, device: str = "cuda") -> M.MemoryCheck:
+                   memory_budget: int | None = None, device: str = "cuda",
+                   split_precision: bool = False) -> M.MemoryCheck:
     """Predict the device memory of the run :func:`quantize` would make, and
     stop (mround/api.py:1088-1192). Reads ``config.json`` and nothing else.
     ``memory_budget`` defaults to 90 % of the device's memory."""
@@ -443,7 +445,7 @@ def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
                             gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
                             scoring_seq_len=scoring_seq_len, scoring_batch=scoring_batch_size,
                             dense_remainder=dense_remainder, quantized_inputs=quantized_inputs,
-                            holdout_batches=holdout_batches)
+                            holdout_batches=holdout_batches, split_precision=split_precision)
     budget = M.default_budget(device) if memory_budget is None else memory_budget
     return M.check_memory(shape, run, budget=budget)
 
@@ -454,7 +456,7 @@ def predict_time(model: str | Path, *, bits: int = 4, group_size: int = 64,
                  remainder_bits: int | None = None, scoring_samples: int | None = None,
                  scoring_seq_len: int | None = None, scheme: QuantScheme | None = None,
                  tuning: TuningConfig | None = None, scale_init: ScaleInit | str | None = None,
-                 per_layer_recipe: bool = False, holdout_batches: int = 0):
+                 per_layer_recipe: bool = False, holdout_batches: int = 0, split_precision: bool = False):
     """Predict the seconds the run :func:`quantize` would make takes on one
     MI355X (``mround_amd.planner.timing``), from ``config.json`` alone
     (mround/cli/main.py:590-624)."""
@@ -467,7 +469,8 @@ def predict_time(model: str | Path, *, bits: int = 4, group_size: int = 64,
                             widths=candidate_bits if average_bits is not None else (resolved.bits,),
                             gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
                             scoring_seq_len=scoring_seq_len, scoring_batch=None, dense_remainder=False,
-                            quantized_inputs=True, holdout_batches=holdout_batches)
+                            quantized_inputs=True, holdout_batches=holdout_batches,
+                            split_precision=split_precision)
     return predict_run_time(shape, run, tuning, resolved.bits,
                             candidate_bits=candidate_bits if average_bits is not None else (),
                             per_layer_recipe=per_layer_recipe, scoring_samples=scoring_samples,
@@ -501,7 +504,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
              per_layer_recipe: bool = False, plan: Mapping[str, int] | None = None,
              scale_init: ScaleInit | str | None = None, seed: int | None = None,
              memory_budget: int | None = None, memory_check: bool = True,
-             min_block_coverage: float = MIN_BLOCK_COVERAGE,
+             min_block_coverage: float = MIN_BLOCK_COVERAGE, split_precision: bool = False,
              device: str = "cuda", progress=None, scoring_progress=None) -> QuantizeResult:
     """Quantize the local checkpoint ``model`` into ``output_dir``.
 
@@ -518,7 +521,12 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     ``memory_check`` is off. A group size that reaches less than
     ``min_block_coverage`` of the block stack's linears is refused with
     ``UnsupportedSchemeError`` (``block_coverage``); the layers it cannot
-    reach are left dense and reported in ``skipped``. Raises the reference's exceptions for
+    reach are left dense and reported in ``skipped``. ``split_precision``
+    runs the block forward's products as three bf16 products of hi and lo
+    halves (the reference's documented remedy for the block objective's
+    precision, mround DOCUMENTATION.md:885-925): about 16 significant bits
+    in place of 8 for 1.6-1.8x the block tune time, for wide codes (8 bits),
+    whose residual bf16 products swamp. Raises the reference's exceptions for
     unrepresentable schemes, bad calibration, unusable plans and unsupported
     architectures.
     """
@@ -540,7 +548,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
                                 gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
                                 scoring_seq_len=scoring_seq_len, scoring_batch=scoring_batch_size,
                                 dense_remainder=dense_remainder, quantized_inputs=quantized_inputs,
-                                holdout_batches=holdout_batches)
+                                holdout_batches=holdout_batches, split_precision=split_precision)
     budget = M.default_budget(device) if memory_budget is None else memory_budget
     memory = M.check_memory(mshape, rshape, budget=budget)
     if memory_check:
@@ -586,7 +594,8 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         remainder_scheme = resolved.with_bits(int(mixed["remainder_bits"]))
         plan_s = time.perf_counter() - tp
     runner = QuantizationRunner(resolved, tuning, progress=progress, quantized_inputs=quantized_inputs,
-                                holdout_batches=holdout_batches, per_layer_recipe=per_layer_recipe)
+                                holdout_batches=holdout_batches, per_layer_recipe=per_layer_recipe,
+                                split_precision=split_precision)
     entrance = _entrance(m, tokens, tuning.batch_size)
     summary, quantized = runner.run(m.blocks, entrance, scheme_by_layer=schemes_by_layer)
     del entrance
@@ -616,6 +625,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         "mixed": mixed,
         "quantized_inputs": quantized_inputs,
         "holdout_batches": holdout_batches,
+        "split_precision": bool(split_precision),
         "blocks": [{"index": b.index, "name": b.name, "initial_loss": b.initial_loss,
                     "final_loss": b.final_loss, "reverted": b.reverted, "seconds": b.seconds,
                     "search_seconds": b.search_seconds} for b in summary.blocks],

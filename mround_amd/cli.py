@@ -54,6 +54,9 @@ def _parser() -> argparse.ArgumentParser:
                    help="run each step's batch in this many pieces, summing their gradients (default: 1)")
     q.add_argument("--allow-dense", action="store_true",
                    help="proceed even when the group size reaches under half of the block stack's layers")
+    q.add_argument("--split-precision", action="store_true",
+                   help="run the block forward's products as three bf16 products of hi and lo halves "
+                        "(about 16-bit operands, 1.6-1.8x the tune time; for 8-bit codes)")
     q.add_argument("--memory-budget", type=float, default=None,
                    help="GB the run may use on the device (default: 90 %% of its memory)")
     q.add_argument("--skip-memory-check", action="store_true",
@@ -142,13 +145,15 @@ def main(argv=None) -> int:
                 args.model, bits=args.bits, group_size=args.group_size,
                 symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
                 average_bits=args.average_bits, candidate_bits=_widths(args.options),
-                remainder_bits=args.remainder_bits, tuning=_tuning(args), memory_budget=budget)
+                remainder_bits=args.remainder_bits, tuning=_tuning(args), memory_budget=budget,
+                split_precision=args.split_precision)
             print(f"  {check.explain()}")
             timing = api.predict_time(
                 args.model, bits=args.bits, group_size=args.group_size,
                 symmetry=Symmetry.ASYMMETRIC if args.asym else Symmetry.SYMMETRIC,
                 average_bits=args.average_bits, candidate_bits=_widths(args.options),
-                remainder_bits=args.remainder_bits, tuning=_tuning(args))
+                remainder_bits=args.remainder_bits, tuning=_tuning(args),
+                split_precision=args.split_precision)
             print(f"  {timing.describe()}")
             return 0 if check.fits else 1
         plan = None
@@ -162,7 +167,7 @@ def main(argv=None) -> int:
                               remainder_bits=args.remainder_bits, plan=plan, tuning=_tuning(args),
                               calibration=args.calibration, export_format=args.format,
                               min_block_coverage=0.0 if args.allow_dense else api.MIN_BLOCK_COVERAGE,
-                              seed=args.seed, memory_budget=budget,
+                              split_precision=args.split_precision, seed=args.seed, memory_budget=budget,
                               memory_check=not args.skip_memory_check,
                               progress=lambda b: print(f"  block {b.index}: loss {b.initial_loss:.4g} -> "
                                                        f"{b.final_loss:.4g} in {b.seconds:.2f} s", flush=True),

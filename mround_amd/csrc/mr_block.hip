@@ -252,7 +252,116 @@ __global__ __launch_bounds__(kBlock) void cast_v(const float4* __restrict__ x, u
   }
 }
 
+// ---- Split-precision operands -----------------------------------------------
+//
+// An fp32 value y is carried as two bfloat16 halves: hi = bf16(y) and
+// lo = bf16(y - hi) (y - hi is exact in fp32), so hi + lo holds y to about 16
+// significant bits. A product A B^T then runs as one bf16 GEMM over K' = 3K
+// with A' = [A_hi | A_hi | A_lo] and B' = [B_hi | B_lo | B_hi] along K: the
+// three products A_hi B_hi + A_hi B_lo + A_lo B_hi, the low-by-low term left
+// out. Rows of activation operands are written in the first order, rows of
+// weights in the second.
+__device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+__device__ __forceinline__ uint2 pack4_bf16_lo(float a, float b, float c, float d) {
+  return pack4_bf16(a - bf16_round(a), b - bf16_round(b), c - bf16_round(c), d - bf16_round(d));
+}
+
+// Three 8-byte pieces of one split row: segment s of SEGS at column group i
+// (n4 groups of 4 per segment).
+__device__ __forceinline__ void store_split4(uint2* row, int64_t n4, int64_t i, float a, float b, float c,
+                                             float d, bool weight_order) {
+  const uint2 hi = pack4_bf16(a, b, c, d);
+  const uint2 lo = pack4_bf16_lo(a, b, c, d);
+  row[i] = hi;
+  row[n4 + i] = weight_order ? lo : hi;
+  row[2 * n4 + i] = weight_order ? hi : lo;
+}
+
+// RMSNorm forward whose output is also written split, [hi | hi | lo] per row
+// of 3H (and hi alone into y when given).
+template <int NV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_fwd_split_v(const float* __restrict__ h,
+                                                              const float* __restrict__ w, int64_t H,
+                                                              float eps, uint16_t* __restrict__ ys,
+                                                              uint16_t* __restrict__ y,
+                                                              float* __restrict__ rstd) {
+  __shared__ float smem[kBlock / 64];
+  const int64_t row = blockIdx.x;
+  const int n4 = static_cast<int>(H / 4);
+  const float4* hr = reinterpret_cast<const float4*>(h + row * H);
+  float4 v[NV];
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    v[k] = i < n4 ? hr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+  }
+  ss = block_sum_f32(ss, smem);
+  const float r = rsqrtf(ss / static_cast<float>(H) + eps);
+  if (threadIdx.x == 0 && rstd) rstd[row] = r;
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  uint2* ysr = reinterpret_cast<uint2*>(ys + row * 3 * H);
+  uint2* yr = y ? reinterpret_cast<uint2*>(y + row * H) : nullptr;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (i < n4) {
+      const float4 g = w4[i];
+      const float a = v[k].x * r * g.x, b = v[k].y * r * g.y, c = v[k].z * r * g.z, d = v[k].w * r * g.w;
+      store_split4(ysr, n4, i, a, b, c, d, false);
+      if (yr) yr[i] = pack4_bf16(a, b, c, d);
+    }
+  }
+}
+
+// fp32 rows -> split rows (activation or weight order), hi alone into plain
+// when given. One block per row.
+__global__ __launch_bounds__(kBlock) void split_rows(const float* __restrict__ src, int64_t ld_src,
+                                                     int64_t n4, bool weight_order, uint16_t* __restrict__ dst,
+                                                     int64_t ld_dst, uint16_t* __restrict__ plain,
+                                                     int64_t ld_plain) {
+  const int64_t row = blockIdx.x;
+  const float4* sr = reinterpret_cast<const float4*>(src + row * ld_src);
+  uint2* dr = reinterpret_cast<uint2*>(dst + row * ld_dst);
+  uint2* pr = plain ? reinterpret_cast<uint2*>(plain + row * ld_plain) : nullptr;
+  for (int64_t i = threadIdx.x; i < n4; i += kBlock) {
+    const float4 x = sr[i];
+    store_split4(dr, n4, i, x.x, x.y, x.z, x.w, weight_order);
+    if (pr) pr[i] = pack4_bf16(x.x, x.y, x.z, x.w);
+  }
+}
+
+// act = silu(g) * u from fp32 gate/up rows interleaved every 32 columns
+// (columns 64 b .. 64 b + 31 gate, the next 32 up, for act columns
+// 32 b .. 32 b + 31), written split [hi | hi | lo] per row of 3N, hi alone
+// into act, and the gate/up values in bf16 for the backward. One block per row.
+__global__ __launch_bounds__(kBlock) void swiglu_split_rows(const float* __restrict__ gu32, int64_t N,
+                                                            uint16_t* __restrict__ act_split,
+                                                            uint16_t* __restrict__ act,
+                                                            uint16_t* __restrict__ gu) {
+  const int64_t row = blockIdx.x;
+  const int64_t n4 = N / 4;
+  const float4* src = reinterpret_cast<const float4*>(gu32 + row * 2 * N);
+  uint2* sr = reinterpret_cast<uint2*>(act_split + row * 3 * N);
+  uint2* ar = reinterpret_cast<uint2*>(act + row * N);
+  uint2* gr = reinterpret_cast<uint2*>(gu + row * 2 * N);
+  for (int64_t i = threadIdx.x; i < n4; i += kBlock) {
+    // act columns 4 i .. 4 i + 3 lie in interleave block b = 4 i / 32
+    const int64_t b = i >> 3, j4 = i & 7;
+    const int64_t gi = b * 16 + j4, ui = gi + 8;  // float4 indices of the gate and up values
+    const float4 g = src[gi], u = src[ui];
+    const float a = silu(g.x) * u.x, bb = silu(g.y) * u.y, c = silu(g.z) * u.z, d = silu(g.w) * u.w;
+    store_split4(sr, n4, i, a, bb, c, d, false);
+    ar[i] = pack4_bf16(a, bb, c, d);
+    gr[gi] = pack4_bf16(g.x, g.y, g.z, g.w);
+    gr[ui] = pack4_bf16(u.x, u.y, u.z, u.w);
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 // float4 columns per thread for a row of H floats, or 0 when H is too wide.
 int row_nv(int64_t H) {
@@ -314,6 +423,70 @@ int mr_rmsnorm_fwd(const float* h, const float* w, int64_t T, int64_t H, float e
   hipLaunchKernelGGL(rmsnorm_fwd, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0, s, h, w, H, eps,
                      y, rstd_out);
   MR_LAUNCH_CHECK("mr_rmsnorm_fwd");
+  return MR_OK;
+}
+
+int mr_rmsnorm_fwd_split(const float* h, const float* w, int64_t T, int64_t H, float eps, void* y_split,
+                         void* y_bf16, float* rstd_out, void* stream) {
+  using namespace mr;
+  clear_error();
+  if (T <= 0 || H <= 0) return MR_OK;
+  if (!h || !w || !y_split) return fail(MR_EINVAL, "mr_rmsnorm_fwd_split: null pointer");
+  if (T > 0x7fffffff) return fail(MR_EINVAL, "mr_rmsnorm_fwd_split: too many rows");
+  const int nv = row_nv(H);
+  if (H % 4 || !nv || !al16(h) || !al16(w) || !al8(y_split) || (y_bf16 && !al8(y_bf16)))
+    return fail(MR_EINVAL, "mr_rmsnorm_fwd_split: the width must be a multiple of 4 up to %d, h and w "
+                "16-byte aligned, the outputs 8-byte aligned", 16 * kBlock * 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* ys = static_cast<uint16_t*>(y_split);
+  uint16_t* y = static_cast<uint16_t*>(y_bf16);
+  const dim3 g(static_cast<unsigned>(T));
+  switch (nv) {
+    case 1: hipLaunchKernelGGL(rmsnorm_fwd_split_v<1>, g, dim3(kBlock), 0, s, h, w, H, eps, ys, y, rstd_out); break;
+    case 2: hipLaunchKernelGGL(rmsnorm_fwd_split_v<2>, g, dim3(kBlock), 0, s, h, w, H, eps, ys, y, rstd_out); break;
+    case 4: hipLaunchKernelGGL(rmsnorm_fwd_split_v<4>, g, dim3(kBlock), 0, s, h, w, H, eps, ys, y, rstd_out); break;
+    case 8: hipLaunchKernelGGL(rmsnorm_fwd_split_v<8>, g, dim3(kBlock), 0, s, h, w, H, eps, ys, y, rstd_out); break;
+    default: hipLaunchKernelGGL(rmsnorm_fwd_split_v<16>, g, dim3(kBlock), 0, s, h, w, H, eps, ys, y, rstd_out); break;
+  }
+  MR_LAUNCH_CHECK("mr_rmsnorm_fwd_split");
+  return MR_OK;
+}
+
+int mr_split_bf16(const float* src, int64_t ld_src, int64_t rows, int64_t cols, int order, void* dst,
+                  int64_t ld_dst, void* plain, int64_t ld_plain, void* stream) {
+  using namespace mr;
+  clear_error();
+  if (rows <= 0 || cols <= 0) return MR_OK;
+  if (!src || !dst) return fail(MR_EINVAL, "mr_split_bf16: null pointer");
+  if (order != 0 && order != 1) return fail(MR_EINVAL, "mr_split_bf16: order must be 0 or 1, got %d", order);
+  if (rows > 0x7fffffff) return fail(MR_EINVAL, "mr_split_bf16: too many rows");
+  if (cols % 4 || ld_src < cols || ld_src % 4 || ld_dst < 3 * cols || ld_dst % 4 ||
+      (plain && (ld_plain < cols || ld_plain % 4)))
+    return fail(MR_EINVAL, "mr_split_bf16: cols and every leading dimension must be multiples of 4, "
+                "ld_src >= cols, ld_dst >= 3 cols, ld_plain >= cols");
+  if (!al16(src) || !al8(dst) || (plain && !al8(plain)))
+    return fail(MR_EINVAL, "mr_split_bf16: src must be 16-byte and the outputs 8-byte aligned");
+  hipLaunchKernelGGL(split_rows, dim3(static_cast<unsigned>(rows)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), src, ld_src, cols / 4, order == 1,
+                     static_cast<uint16_t*>(dst), ld_dst, static_cast<uint16_t*>(plain), ld_plain);
+  MR_LAUNCH_CHECK("mr_split_bf16");
+  return MR_OK;
+}
+
+int mr_swiglu_split(const float* gu32, int64_t T, int64_t N, void* act_split, void* act, void* gu,
+                    void* stream) {
+  using namespace mr;
+  clear_error();
+  if (T <= 0 || N <= 0) return MR_OK;
+  if (!gu32 || !act_split || !act || !gu) return fail(MR_EINVAL, "mr_swiglu_split: null pointer");
+  if (T > 0x7fffffff) return fail(MR_EINVAL, "mr_swiglu_split: too many rows");
+  if (N % 32) return fail(MR_EINVAL, "mr_swiglu_split: N must be a multiple of 32 (the gate/up interleave)");
+  if (!al16(gu32) || !al8(act_split) || !al8(act) || !al8(gu))
+    return fail(MR_EINVAL, "mr_swiglu_split: gu32 must be 16-byte and the outputs 8-byte aligned");
+  hipLaunchKernelGGL(swiglu_split_rows, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), gu32, N, static_cast<uint16_t*>(act_split),
+                     static_cast<uint16_t*>(act), static_cast<uint16_t*>(gu));
+  MR_LAUNCH_CHECK("mr_swiglu_split");
   return MR_OK;
 }
 

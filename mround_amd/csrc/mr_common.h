@@ -57,6 +57,13 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return __half_as_ushort(__float2half_rn(f));
 }
 
+// Logistic function with the hardware reciprocal (1 ulp), shared by the
+// SwiGLU GEMM epilogues and the split-precision SwiGLU kernel: the epilogues
+// are tolerance-checked, not bit-exact, and an IEEE division per element keeps
+// the unrolled epilogue from fitting in registers.
+__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
+
 template <int DT>
 __device__ __forceinline__ float load_elem(const void* p, int64_t i) {
   if constexpr (DT == MR_F32) {

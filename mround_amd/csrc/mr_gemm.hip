@@ -233,12 +233,6 @@ struct MNMajorDirect {
   }
 };
 
-// Logistic function with the hardware reciprocal (1 ulp); the epilogues are
-// tolerance-checked, not bit-exact, and an IEEE division per element keeps the
-// unrolled epilogue from fitting in registers.
-__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
-__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
-
 template <int BM, int BN, bool A_KMAJOR, bool B_KMAJOR, int EPI, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int WM = BM / kWaveRows, WN = BN / (kWaves / kWaveRows);

@@ -83,6 +83,9 @@ _SIGNATURES = {
     "mr_gemm_swiglu_bwd": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P, ctypes.c_size_t, _P]),
     "mr_rmsnorm_fwd": (_I, [_P, _P, _L, _L, _F, _P, _P, _P]),
     "mr_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _L, _L, _P, _P, _P]),
+    "mr_rmsnorm_fwd_split": (_I, [_P, _P, _L, _L, _F, _P, _P, _P, _P]),
+    "mr_split_bf16": (_I, [_P, _L, _L, _L, _I, _P, _L, _P, _L, _P]),
+    "mr_swiglu_split": (_I, [_P, _L, _L, _P, _P, _P, _P]),
     "mr_rope": (_I, [_P, _L, _L, _I, _I, _I, _P, _I, _P]),
     "mr_attn_fwd": (_I, [_P, _L, _I, _I, _I, _I, _I, _F, _P, _L, _P, _P]),
     "mr_attn_bwd_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I, _I, _I, _I]),
@@ -161,6 +164,18 @@ def _ptr(t: torch.Tensor | None) -> int | None:
         raise KernelError("tensors passed to the HIP library must live on a ROCm device")
     if not t.is_contiguous():
         raise KernelError("tensors passed to the HIP library must be contiguous")
+    return t.data_ptr()
+
+
+def _rows_ptr(t: torch.Tensor | None) -> int | None:
+    """A 2-D operand whose rows may be strided (a column range of a wider
+    matrix): unit stride along the row, the leading dimension passed apart."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise KernelError("tensors passed to the HIP library must live on a ROCm device")
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise KernelError("a matrix operand must be 2-D with contiguous rows")
     return t.data_ptr()
 
 
@@ -408,9 +423,9 @@ def gemm(layout: str, a, b, c, *, M, N, K, bias=None, resid=None, workspace=None
     ``workspace``: the k-split partials (a device tensor of at least
     ``gemm_workspace_bytes(M, N, K)`` bytes); None uses the binding's own."""
     ws_ptr, ws_bytes = _ws_args(_gemm_ws(a.device, M, N, K, workspace))
-    rc = lib().mr_gemm(GEMM_LAYOUT[layout], M, N, K, _ptr(a), a.stride(0), _ptr(b), b.stride(0),
-                       _ptr(c), dtype_code(c.dtype), c.stride(0), _ptr(_f32(bias, "bias")),
-                       _ptr(_f32(resid, "resid")), resid.stride(0) if resid is not None else 0,
+    rc = lib().mr_gemm(GEMM_LAYOUT[layout], M, N, K, _rows_ptr(a), a.stride(0), _rows_ptr(b), b.stride(0),
+                       _rows_ptr(c), dtype_code(c.dtype), c.stride(0), _ptr(_f32(bias, "bias")),
+                       _rows_ptr(_f32(resid, "resid")), resid.stride(0) if resid is not None else 0,
                        ws_ptr, ws_bytes, _stream(a))
     _check(rc, "mr_gemm")
 
@@ -441,6 +456,43 @@ def rmsnorm_fwd(h, w, eps, y, rstd=None) -> None:
     rc = lib().mr_rmsnorm_fwd(_ptr(_f32(h, "h")), _ptr(_f32(w, "w")), T, H, eps, _ptr(y),
                               _ptr(_f32(rstd, "rstd")), _stream(h))
     _check(rc, "mr_rmsnorm_fwd")
+
+
+def rmsnorm_fwd_split(h, w, eps, y_split, y=None, rstd=None) -> None:
+    """``mr_rmsnorm_fwd_split``: ``y_split`` [T, 3H] bf16 as [hi | hi | lo]."""
+    T, H = h.shape
+    if tuple(y_split.shape) != (T, 3 * H):
+        raise KernelError(f"y_split must be [{T}, {3 * H}]")
+    rc = lib().mr_rmsnorm_fwd_split(_ptr(_f32(h, "h")), _ptr(_f32(w, "w")), T, H, eps, _ptr(y_split), _ptr(y),
+                                    _ptr(_f32(rstd, "rstd")), _stream(h))
+    _check(rc, "mr_rmsnorm_fwd_split")
+
+
+SPLIT_ACTIVATION, SPLIT_WEIGHT = 0, 1
+
+
+def split_bf16(src, dst, *, order, plain=None) -> None:
+    """``mr_split_bf16``: fp32 ``src`` [rows, cols] into ``dst`` [rows, >= 3 cols]
+    (activation order [hi | hi | lo], weight order [hi | lo | hi]), hi alone
+    into ``plain`` when given. Rows may be strided."""
+    rows, cols = src.shape
+    if dst.shape[0] != rows or (plain is not None and plain.shape[0] != rows):
+        raise KernelError("split outputs must have the source's rows")
+    rc = lib().mr_split_bf16(_rows_ptr(_f32(src, "src")), src.stride(0), rows, cols, order, _rows_ptr(dst),
+                             dst.stride(0), _rows_ptr(plain), plain.stride(0) if plain is not None else 0,
+                             _stream(src))
+    _check(rc, "mr_split_bf16")
+
+
+def swiglu_split(gu32, act_split, act, gu) -> None:
+    """``mr_swiglu_split``: act from fp32 interleaved gate/up rows, split and plain."""
+    T, N2 = gu32.shape
+    N = N2 // 2
+    if tuple(act_split.shape) != (T, 3 * N) or tuple(act.shape) != (T, N) or tuple(gu.shape) != (T, N2):
+        raise KernelError("swiglu_split: act_split [T, 3N], act [T, N], gu [T, 2N]")
+    rc = lib().mr_swiglu_split(_ptr(_f32(gu32, "gu32")), T, N, _ptr(act_split), _ptr(act), _ptr(gu),
+                               _stream(gu32))
+    _check(rc, "mr_swiglu_split")
 
 
 def rmsnorm_bwd(dy, h, w, rstd, dres, dh_bf16=None, dh_f32=None) -> None:

@@ -181,6 +181,14 @@ def gemm_problems(shape: BlockShape, tokens: int) -> list[tuple[int, int, int]]:
             (T, h, 2 * mlp), (2 * mlp, h, T), (T, hq_d, h), (h, hq_d, T), (q, h, T), (T, h, q)]
 
 
+def split_gemm_problems(shape: BlockShape, tokens: int) -> list[tuple[int, int, int]]:
+    """(M, N, K) of the forward products that split precision runs over K' = 3K
+    (the q/k/v projection, the gate/up pair and down; the attention output
+    projection runs as two products of its own K)."""
+    T, h, mlp, q = tokens, shape.hidden, shape.intermediate, shape.qkv_rows
+    return [(T, q, 3 * h), (T, 2 * mlp, 3 * h), (T, h, 3 * mlp)]
+
+
 def workspace_bytes(shape: BlockShape, batch: int, seq_len: int,
                     extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> tuple[int, int]:
     """Bytes of the GEMM k-split workspace (the largest any of the block's
@@ -239,15 +247,28 @@ class BlockEngine:
     tokens; the rest are padding at its end (``aligned_length``). Causal
     attention keeps padding rows out of every token row, and ``loss`` counts
     token rows only, so the loss and every gradient are those of the
-    ``real_len``-token sequences."""
+    ``real_len``-token sequences.
+
+    ``split`` runs the forward's products in split precision (the reference's
+    three-product remedy for the block objective, mround DOCUMENTATION.md:
+    885-925): the normalized inputs, the SwiGLU output and every W' are
+    carried as bf16 hi and lo halves, and each product is one bf16 GEMM over
+    K' = 3K of [A_hi | A_hi | A_lo] and [B_hi | B_lo | B_hi] (the attention
+    output projection as A (B_hi + B_lo), two products). The attention itself,
+    the stored q/k/v and the backward stay in bf16. Weights are written
+    through ``w32`` (fp32) and ``split_weights``."""
 
     def __init__(self, shape: BlockShape, *, batch: int, seq_len: int, device,
-                 extra_gemms: tuple[tuple[int, int, int], ...] = (), real_len: int | None = None) -> None:
+                 extra_gemms: tuple[tuple[int, int, int], ...] = (), real_len: int | None = None,
+                 split: bool = False) -> None:
         shape.validate(seq_len)
         self.shape, self.batch, self.seq_len = shape, batch, seq_len
         self.real_len = seq_len if real_len is None else int(real_len)
         if not 1 <= self.real_len <= seq_len:
             raise ArchitectureError(f"{self.real_len} tokens do not fit sequences of {seq_len} rows")
+        self.split = bool(split)
+        if self.split:
+            extra_gemms = tuple(extra_gemms) + tuple(split_gemm_problems(shape, batch * seq_len))
         self.device = torch.device(device)
         T, h, mlp = batch * seq_len, shape.hidden, shape.intermediate
         self.tokens = T
@@ -275,6 +296,14 @@ class BlockEngine:
         self.dqkv = e(T, shape.qkv_rows)
         self.loss_val = e(1, dt=f32)
         self.threshold = e(1, dt=f32)
+        # split precision: fp32 W' and the split operands
+        self.w32 = self.wqs = None
+        self.x1s = self.x2s = self.acts = self.gu32 = None
+        if self.split:
+            self.w32 = {k: torch.empty(v.shape, dtype=f32, device=self.device) for k, v in self.wq.items()}
+            self.wqs = {k: e(v.shape[0], 3 * v.shape[1]) for k, v in self.wq.items()}
+            self.x1s, self.x2s = e(T, 3 * h), e(T, 3 * h)
+            self.acts, self.gu32 = e(T, 3 * mlp), e(T, 2 * mlp, dt=f32)
         self.cos_sin = rope_table(seq_len, shape.head_dim, shape.rope_theta, self.device, shape.rope_scaling)
         self.scale = 1.0 / math.sqrt(shape.head_dim)
         self.place = placements(shape)
@@ -288,7 +317,8 @@ class BlockEngine:
         self.x_in: torch.Tensor | None = None  # block input of the last saving forward
         self.dh32: torch.Tensor | None = None  # fp32 residual gradient, for input gradients
         self.capacity = batch  # sequences the buffers hold (see set_sequences)
-        self._full = {n: getattr(self, n) for n in self.PER_TOKEN + self.PER_SEQUENCE}
+        self._per_token = self.PER_TOKEN + (self.SPLIT_PER_TOKEN if self.split else ())
+        self._full = {n: getattr(self, n) for n in self._per_token + self.PER_SEQUENCE}
         # name -> [(start, end) HIP events] for the launches being timed, or None
         self.timers: dict[str, list] | None = None
 
@@ -298,6 +328,7 @@ class BlockEngine:
     PER_TOKEN = ("x1", "rstd1", "qkv", "attn", "h2", "x2", "rstd2", "act", "gu", "grad_out",
                  "grad_out16", "dgu", "dx2", "dh2", "dattn", "dqkv")
     PER_SEQUENCE = ("lse", "dsum")
+    SPLIT_PER_TOKEN = ("x1s", "x2s", "acts", "gu32")
 
     def set_sequences(self, n: int) -> None:
         """Run the next passes over ``n`` sequences (at most the capacity the
@@ -309,7 +340,7 @@ class BlockEngine:
         if n == self.batch:
             return
         T = n * self.seq_len
-        for name in self.PER_TOKEN:
+        for name in self._per_token:
             setattr(self, name, self._full[name][:T])
         for name in self.PER_SEQUENCE:
             setattr(self, name, self._full[name][:n])
@@ -380,9 +411,21 @@ class BlockEngine:
 
     def load_dense(self, linears: dict[str, torch.Tensor]) -> None:
         """W' = the given weights rounded to bf16 (the targets pass, and the
-        advance pass over committed reconstructions)."""
+        advance pass over committed reconstructions); in split precision the
+        weights as they are (hi and lo halves, lo zero for bf16 weights)."""
+        if self.split:
+            for name, p in self.place.items():
+                place(self.w32[p.operand], linears[name].float(), p)
+            self.split_weights()
+            return
         for name, p in self.place.items():
             place(self.wq[p.operand], linears[name].to(torch.bfloat16), p)
+
+    def split_weights(self) -> None:
+        """Split precision: every fused fp32 W' in ``w32`` into its split
+        operand, and its hi half into ``wq`` (what the backward reads)."""
+        for k, w in self.w32.items():
+            K.split_bf16(w, self.wqs[k], order=K.SPLIT_WEIGHT, plain=self.wq[k])
 
     # ---------------------------------------------------------------- forward --
     def forward(self, x: torch.Tensor, out: torch.Tensor, *, save: bool) -> None:
@@ -397,6 +440,9 @@ class BlockEngine:
             if out.data_ptr() == x.data_ptr():
                 raise ArchitectureError("a saving forward needs its input kept: out must not be x")
             self.x_in = x
+        if self.split:
+            self._forward_split(x, out)
+            return
         K.rmsnorm_fwd(x, self.norm_in, s.norm_eps, self.x1, self.rstd1)
         self._run("gemm_qkv", lambda: K.gemm("nt", self.x1, self.wq["qkv"], self.qkv, M=T, N=s.qkv_rows,
                                              K=h, bias=self.bias_qkv, workspace=ws))
@@ -411,6 +457,36 @@ class BlockEngine:
         self._run("gemm_gate_up", lambda: K.gemm_swiglu(self.x2, self.wq["gu"], self.act,
                                                         self.gu if save else None, workspace=ws))
         self._run("gemm_down", lambda: K.gemm("nt", self.act, self.wq["down"], out, M=T, N=h, K=mlp,
+                                              resid=self.h2, workspace=ws))
+
+    def _forward_split(self, x: torch.Tensor, out: torch.Tensor) -> None:
+        """``forward`` with the products in split precision (see the class);
+        leaves the same saved activations (x1, x2 and act as their hi halves)."""
+        s, T = self.shape, self.tokens
+        h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
+        ws = self.gemm_ws
+        K.rmsnorm_fwd_split(x, self.norm_in, s.norm_eps, self.x1s, self.x1, self.rstd1)
+        self._run("gemm_qkv", lambda: K.gemm("nt", self.x1s, self.wqs["qkv"], self.qkv, M=T, N=s.qkv_rows,
+                                             K=3 * h, bias=self.bias_qkv, workspace=ws))
+        K.rope(self.qkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads, head_dim=s.head_dim,
+               cos_sin=self.cos_sin)
+        self._run("attn_fwd", lambda: K.attn_fwd(
+            self.qkv, batch=self.batch, seq_len=self.seq_len, n_heads=s.n_heads,
+            n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, scale=self.scale, out=self.attn, lse=self.lse))
+        wo = self.wqs["o"]
+
+        def o_proj():
+            K.gemm("nt", self.attn, wo[:, :hq_d], self.h2, M=T, N=h, K=hq_d, resid=x, workspace=ws)
+            K.gemm("nt", self.attn, wo[:, hq_d:2 * hq_d], self.h2, M=T, N=h, K=hq_d, resid=self.h2,
+                   workspace=ws)
+        self._run("gemm_o", o_proj)
+        K.rmsnorm_fwd_split(self.h2, self.norm_post, s.norm_eps, self.x2s, self.x2, self.rstd2)
+
+        def gate_up():
+            K.gemm("nt", self.x2s, self.wqs["gu"], self.gu32, M=T, N=2 * mlp, K=3 * h, workspace=ws)
+            K.swiglu_split(self.gu32, self.acts, self.act, self.gu)
+        self._run("gemm_gate_up", gate_up)
+        self._run("gemm_down", lambda: K.gemm("nt", self.acts, self.wqs["down"], out, M=T, N=h, K=3 * mlp,
                                               resid=self.h2, workspace=ws))
 
     def loss(self, out: torch.Tensor, target: torch.Tensor, *, suppress: bool, with_grad: bool,

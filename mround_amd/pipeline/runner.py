@@ -150,7 +150,8 @@ class QuantizationRunner:
                  progress: Callable[[BlockResult], None] | None = None,
                  eps: float = DEFAULT_EPS_FP32, quantized_inputs: bool = True,
                  holdout_batches: int = 0, per_layer_recipe: bool = False,
-                 graphs: bool | None = None, fused_advance: bool = True) -> None:
+                 graphs: bool | None = None, fused_advance: bool = True,
+                 split_precision: bool = False) -> None:
         if holdout_batches < 0:
             msg = f"holdout_batches must be zero or more, got {holdout_batches}"
             raise CalibrationError(msg)
@@ -165,6 +166,9 @@ class QuantizationRunner:
         # With a quantized stream and no held-out batches, the final score is
         # taken from the advance pass (see run); False scores separately.
         self.fused_advance = fused_advance
+        # The forward's products in split precision (BlockEngine's split): the
+        # block objective to about 16 significant bits in place of bf16's 8.
+        self.split = bool(split_precision)
         self._engines: dict = {}
         # rows per sequence in the streams: seq_len rounded up to the attention
         # tile, the rows past seq_len padding (see BlockEngine)
@@ -187,7 +191,8 @@ class QuantizationRunner:
         key = (shape, capacity, str(device))
         eng = self._engines.get(key)
         if eng is None:
-            eng = BlockEngine(shape, batch=capacity, seq_len=seq, device=device, real_len=self.tuning.seq_len)
+            eng = BlockEngine(shape, batch=capacity, seq_len=seq, device=device, real_len=self.tuning.seq_len,
+                              split=self.split)
             self._engines = {key: eng}
         return eng
 
@@ -228,10 +233,12 @@ class QuantizationRunner:
         # untouched inputs. Identical losses, codes and streams, one pass over
         # the calibration set fewer per block. (A float16 model's committed
         # reconstruction is rounded through float16, so its W' is not the
-        # tuned one: there the final score is taken separately.)
+        # tuned one: there the final score is taken separately. So it is in
+        # split precision, whose scores read W' to about 16 bits while the
+        # committed reconstruction is bf16.)
         half = any(w.dtype == torch.float16 for b in blocks for w in b.weights.linears.values())
         fused = (quantized_stream is not None and self.fused_advance and self.holdout_batches == 0
-                 and not half)
+                 and not half and not self.split)
         spare = [torch.empty_like(x) for x in quantized_stream] if fused else None
         # Without a quantized stream the targets are a second stream; the two
         # trade places after each block, so two streams are held in all.
@@ -341,7 +348,10 @@ class QuantizationRunner:
         # operands; the tuned layers' rows are rewritten every step.
         for name, _ in skipped:
             p = place[name]
-            place_rows(eng.wq[p.operand], block.weights.linears[name].to(torch.bfloat16), p)
+            if eng.split:
+                place_rows(eng.w32[p.operand], block.weights.linears[name].float(), p)
+            else:
+                place_rows(eng.wq[p.operand], block.weights.linears[name].to(torch.bfloat16), p)
         outcome = self._tune(eng, layers, inputs, targets, defer_final=defer_final)
         t_commit = time.perf_counter()
         exported = {}
@@ -426,19 +436,29 @@ class QuantizationRunner:
 
     # ------------------------------------------------------------------ tune --
     def _quantize_all(self, eng: BlockEngine, layers: Mapping[str, _Layer]) -> None:
+        """Every tuned layer's W' into the engine's fused operands (in split
+        precision as fp32 into ``w32``, then split)."""
         for layer in layers.values():
             p = layer.placement
             K.fq_forward_mapped(layer.weight, layer.v, layer.alpha, layer.beta,
                                 bits=layer.scheme.bits, group_size=layer.scheme.group_size,
-                                mode=layer.mode, eps=self.eps, wq_out=eng.wq[p.operand],
+                                mode=layer.mode, eps=self.eps,
+                                wq_out=eng.w32[p.operand] if eng.split else eng.wq[p.operand],
                                 row_block=p.row_block, row_stride=p.row_stride,
                                 row_offset=p.row_offset, init_scale=layer.init_scale)
+        if eng.split:
+            eng.split_weights()
 
     def _step_all(self, eng: BlockEngine, layers: Mapping[str, _Layer], rates: Mapping[str, float],
                   step: int, *, requant: bool = False) -> None:
         """The fused sign-SGD step of every layer; with ``requant`` the same
         kernels also write the new W' into the engine's fused operands (the
-        next step's forward, made without rereading W and v)."""
+        next step's forward, made without rereading W and v; in split
+        precision W' is made afterwards in fp32 and split)."""
+        if requant and eng.split:
+            self._step_all(eng, layers, rates, step)
+            self._quantize_all(eng, layers)
+            return
         iters = self.tuning.iters
         for name, layer in layers.items():
             p = layer.placement
@@ -462,8 +482,8 @@ class QuantizationRunner:
         graph is recorded once per block and replayed on every later step
         that uses the batch; the rates come from a schedule in device memory
         indexed by a device step counter the graph advances."""
-        if eng.capacity * eng.seq_len != self._batch_tokens:
-            return False  # steps in pieces run from the host
+        if eng.capacity * eng.seq_len != self._batch_tokens or eng.split:
+            return False  # steps in pieces, and split precision, run from the host
         if self.graphs is not None:
             return bool(self.graphs) and eng.timers is None
         small = eng.tokens * eng.shape.hidden <= GRAPH_MAX_ELEMENTS

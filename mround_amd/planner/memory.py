@@ -106,20 +106,31 @@ class ModelShape:
 
 
 def library_workspace_bytes(m: ModelShape, tokens: int, seq_len: int,
-                            extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> int:
+                            extra_gemms: tuple[tuple[int, int, int], ...] = (), split: bool = False) -> int:
     """The GEMM k-split and attention dK/dV workspaces a ``BlockEngine`` at
     ``tokens`` tokens owns (the library's size queries)."""
-    from mround_amd.pipeline.block import BlockShape, workspace_bytes
+    from mround_amd.pipeline.block import BlockShape, split_gemm_problems, workspace_bytes
 
     shape = BlockShape(hidden=m.hidden, n_heads=m.heads, n_kv_heads=m.kv_heads, head_dim=m.head_dim,
                        intermediate=m.intermediate)
+    if split:
+        extra_gemms = tuple(extra_gemms) + tuple(split_gemm_problems(shape, tokens))
     return sum(workspace_bytes(shape, tokens // seq_len, seq_len, extra_gemms))
 
 
+def split_bytes(m: ModelShape, tokens: int) -> int:
+    """What split precision adds to a ``BlockEngine``: fp32 W' and the split
+    W' operands, the split normalized inputs and SwiGLU output, and the fp32
+    gate/up pair."""
+    T, h, mlp = tokens, m.hidden, m.intermediate
+    return m.block_weights * (4 + 6) + 2 * T * 3 * h * 2 + T * 3 * mlp * 2 + T * 2 * mlp * 4
+
+
 def engine_bytes(m: ModelShape, tokens: int, seq_len: int, *, input_grads: bool = False,
-                 extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> int:
+                 extra_gemms: tuple[tuple[int, int, int], ...] = (), split: bool = False) -> int:
     """``BlockEngine`` at ``tokens`` tokens: fused W' (bf16) and dL/dW' (fp32),
-    the saved activations, the backward's buffers and the library workspaces."""
+    the saved activations, the backward's buffers and the library workspaces
+    (and with ``split``, the split-precision operands)."""
     T, h, q, mlp = tokens, m.hidden, m.qkv_rows, m.intermediate
     hq_d = m.heads * m.head_dim
     weights = m.block_weights * (2 + 4)
@@ -128,8 +139,9 @@ def engine_bytes(m: ModelShape, tokens: int, seq_len: int, *, input_grads: bool 
     rope = seq_len * (m.head_dim // 2) * 2 * 4
     extra = T * h * 4 if input_grads else 0
     scalars = 2 * 4  # loss value and outlier threshold
-    ws = library_workspace_bytes(m, tokens, seq_len, extra_gemms)
-    return weights + acts + bwd + rope + LOSS_WORKSPACE + scalars + extra + ws
+    ws = library_workspace_bytes(m, tokens, seq_len, extra_gemms, split)
+    return (weights + acts + bwd + rope + LOSS_WORKSPACE + scalars + extra + ws
+            + (split_bytes(m, tokens) if split else 0))
 
 
 def activation_bytes(m: ModelShape, tokens: int) -> int:
@@ -160,11 +172,12 @@ class RunShape:
     holdout_batches: int = 0
     micro_batches: int = 1
     half: bool = False  # float16 model: the final score is taken apart from the advance
+    split: bool = False  # split-precision products (the final score apart from the advance too)
 
     @property
     def streams(self) -> int:
         """Calibration streams the block loop holds at once."""
-        fused = self.quantized_inputs and self.holdout_batches == 0 and not self.half
+        fused = self.quantized_inputs and self.holdout_batches == 0 and not self.half and not self.split
         return 3 if fused else 2
 
     @property
@@ -228,7 +241,8 @@ def predict_memory(m: ModelShape, run: RunShape) -> MemoryPrediction:
     committed = L * (m.block_weights + groups * 8)
     transient = m.largest_layer * (1 + 4) + T * h * 4
     piece = run.piece_sequences * S
-    stages["blocks"] = (base + run.n_samples * run.seq_len * 8 + streams + engine_bytes(m, piece, S)
+    stages["blocks"] = (base + run.n_samples * run.seq_len * 8 + streams
+                        + engine_bytes(m, piece, S, split=run.split)
                         + learn + committed + transient)
     rem = 0
     if not run.dense_remainder:

@@ -130,6 +130,22 @@ def _work(model: ModelShape, batch: int, seq_len: int) -> tuple[float, float]:
     return tokens * model.block_weights, attention
 
 
+# Split precision's measured cost over its extra GEMM work: 7B-, 3B- and
+# 0.5B-shaped block tunes (2-bit, 200 steps, 16 batches of 8 x 2048) ran
+# 8.33, 3.13 and 0.83 s against 4.54, 1.75 and 0.53 s in bf16; the extra
+# GEMM work alone predicts 0.55-0.68 of the difference (the rest is the split
+# operands' writes, the fp32 gate/up pair and W' made in fp32 each step).
+# Scaled by 1.75 the rule puts the three at 0.93, 0.97 and 1.04 of it.
+_SPLIT_EXTRA = 1.75
+
+
+def split_forward_factor(model: ModelShape) -> float:
+    """How much more GEMM work the forward does in split precision: 3x for
+    every product but the attention output projection's 2x."""
+    o = model.hidden * model.heads * model.head_dim
+    return (3.0 * model.block_weights - o) / model.block_weights
+
+
 def predict_time(model: ModelShape, run: RunShape, *, iters: int, outlier_rule: bool,
                  scoring_tokens: int | None = None, scoring_source: str | None = None) -> TimePrediction:
     """Predict the seconds a run records on one MI355X (``mround/planner/timing.py:209-282``).
@@ -141,8 +157,17 @@ def predict_time(model: ModelShape, run: RunShape, *, iters: int, outlier_rule: 
         raise ValueError(f"a run takes a positive number of steps, got {iters}")
     pieces = max(1, min(int(run.micro_batches), int(run.batch_size)))
     tw, att = _work(model, run.batch_size, run.seq_len)
-    forward = _FORWARD[0] + _FORWARD[1] * tw + _FORWARD[2] * att + (pieces - 1) * _FORWARD_PIECE
-    step = _STEP[0] + _STEP[1] * tw + _STEP[2] * att + (pieces - 1) * _PIECE
+    tw_forward = tw_step = tw
+    if getattr(run, "split", False):
+        # split precision: the forward's products over 3K (the attention
+        # output projection over 2K, weighted by its share of the weights),
+        # the backward's unchanged; the extra work's cost scaled by what the
+        # split operands' own passes add (_SPLIT_EXTRA)
+        f = split_forward_factor(model)
+        tw_forward = tw * (1.0 + _SPLIT_EXTRA * (f - 1.0))
+        tw_step = tw * (1.0 + _SPLIT_EXTRA * (f - 1.0) / 3.0)
+    forward = _FORWARD[0] + _FORWARD[1] * tw_forward + _FORWARD[2] * att + (pieces - 1) * _FORWARD_PIECE
+    step = _STEP[0] + _STEP[1] * tw_step + _STEP[2] * att + (pieces - 1) * _PIECE
     if outlier_rule:
         step += _OUTLIER * run.batch_size * aligned_rows(run.seq_len) * model.hidden
         if pieces > 1:

@@ -106,6 +106,26 @@ def test_host_validation_refuses_before_launch(lib):
     assert rc == -22 and b"workspace" in lib.mr_last_error()
 
 
+def test_split_entry_points_refuse_bad_arguments(lib):
+    P = ctypes.c_void_p
+    rc = lib.mr_split_bf16(P(256), 64, 4, 64, 2, P(256), 192, None, 0, None)
+    assert rc == -22 and b"order" in lib.mr_last_error()
+    rc = lib.mr_split_bf16(P(256), 64, 4, 64, 0, P(256), 128, None, 0, None)  # ld_dst < 3 cols
+    assert rc == -22 and b"ld_dst" in lib.mr_last_error()
+    rc = lib.mr_split_bf16(P(264), 64, 4, 64, 0, P(256), 192, None, 0, None)
+    assert rc == -22 and b"aligned" in lib.mr_last_error()
+    rc = lib.mr_split_bf16(None, 64, 4, 64, 0, P(256), 192, None, 0, None)
+    assert rc == -22 and b"null" in lib.mr_last_error()
+    rc = lib.mr_rmsnorm_fwd_split(P(256), P(256), 4, 66, 1e-6, P(256), None, None, None)
+    assert rc == -22 and b"multiple of 4" in lib.mr_last_error()
+    rc = lib.mr_swiglu_split(P(256), 4, 48, P(256), P(256), P(256), None)
+    assert rc == -22 and b"multiple of 32" in lib.mr_last_error()
+    rc = lib.mr_swiglu_split(P(256), 4, 64, P(256), None, P(256), None)
+    assert rc == -22 and b"null" in lib.mr_last_error()
+    # nothing to do is not an error
+    assert lib.mr_split_bf16(None, 0, 0, 0, 0, None, 0, None, 0, None) == 0
+
+
 def test_workspace_sizes(lib):
     assert lib.mr_loss_workspace_bytes(1 << 26) > 0
     assert lib.mr_delta_loss_workspace_bytes(3584, 18944, 3) > 0

@@ -110,6 +110,20 @@ def test_a_length_off_the_tile_counts_padded_rows():
     assert _bytes(eng) == M.engine_bytes(M.ModelShape.from_config(GEOMETRIES["smollm2-135m"]), 512, 256)
 
 
+def test_split_engine_formula_is_the_engine():
+    """Split precision adds fp32 and split W', the split normalized inputs and
+    SwiGLU output and the fp32 gate/up pair (and the workspace of the 3K
+    products) to the engine; the prediction counts exactly what it allocates,
+    and the blocks stage holds two streams (the final score apart)."""
+    cfg = GEOMETRIES["smollm2-135m"]
+    m = M.ModelShape.from_config(cfg)
+    eng = BlockEngine(block_shape(cfg), batch=2, seq_len=256, device="cpu", split=True)
+    assert _bytes(eng) == M.engine_bytes(m, 512, 256, split=True)
+    assert M.engine_bytes(m, 512, 256, split=True) - M.engine_bytes(m, 512, 256) >= M.split_bytes(m, 512)
+    run = M.RunShape(n_samples=8, seq_len=256, batch_size=2, group_size=64, split=True)
+    assert run.streams == 2
+
+
 def test_engine_refuses_more_tokens_than_rows():
     with pytest.raises(ArchitectureError):
         BlockEngine(block_shape(GEOMETRIES["smollm2-135m"]), batch=1, seq_len=128, device="cpu", real_len=129)

@@ -1,0 +1,125 @@
+"""Where the bf16 block objective loses its precision, in float64 on the CPU.
+
+The oracle's block forward, restated here with switchable rounding points, is
+run at 8 and 4 bits on a SmolLM2-shaped block: the loss of round-to-nearest W'
+against targets from the original weights, each side computed with the same
+roundings, compared with the exact float64 loss. The rounding points are the
+GPU path's: GEMM activation operands (x1, x2, act) and W' in bf16, the stored
+q/k/v, the attention's P and its output O. Split precision keeps the GEMM
+operands as hi + lo bf16 halves. This pins the figures the split-precision
+design rests on: one bf16 product reads the 8-bit objective about a third
+high; split GEMM operands leave about a tenth, nearly all of it the bf16
+q/k/v the attention reads.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import block as OB
+from oracle import quantize as OQ
+
+SHAPE = OB.Shape(hidden=576, n_heads=9, n_kv_heads=3, head_dim=64, intermediate=1536, norm_eps=1e-5)
+NAMES = ("mlp.down_proj", "mlp.gate_proj", "mlp.up_proj", "self_attn.k_proj", "self_attn.o_proj",
+         "self_attn.q_proj", "self_attn.v_proj")
+
+
+def _bf(t):
+    return t.to(torch.bfloat16).to(t.dtype)
+
+
+def _split(t):
+    hi = _bf(t)
+    return hi + _bf(t - hi)
+
+
+def _forward(x, lin, norms, mode):
+    """The oracle block (``oracle.block.block_forward``) with the GPU path's
+    rounding points: ``act`` and ``w`` (GEMM operands, bf16 or with ``split``
+    hi + lo), ``qkv`` (stored q/k/v), ``p`` (attention probabilities), ``o``
+    (attention output, bf16 whatever ``split`` says)."""
+    gem = (lambda t: t) if "act" not in mode else (_split if "split" in mode else _bf)
+    wr = (lambda t: t) if "w" not in mode else (_split if "split" in mode else _bf)
+    B, S, _ = x.shape
+    d, hq, hkv = SHAPE.head_dim, SHAPE.n_heads, SHAPE.n_kv_heads
+    x1 = gem(OB.rms_norm(x, norms[0], SHAPE.norm_eps))
+
+    def proj(name, inp):
+        return inp @ wr(lin[name]).transpose(0, 1)
+
+    q, k, v = proj("self_attn.q_proj", x1), proj("self_attn.k_proj", x1), proj("self_attn.v_proj", x1)
+    if "qkv" in mode:
+        q, k, v = _bf(q), _bf(k), _bf(v)
+    q = q.reshape(B, S, hq, d).transpose(1, 2)
+    k = k.reshape(B, S, hkv, d).transpose(1, 2)
+    v = v.reshape(B, S, hkv, d).transpose(1, 2)
+    cos, sin = OB.rope_cos_sin(S, d, SHAPE.rope_theta)
+    q, k = OB.rope(q, cos.double(), sin.double()), OB.rope(k, cos.double(), sin.double())
+    if "qkv" in mode:
+        q, k = _bf(q), _bf(k)
+    k, v = k.repeat_interleave(hq // hkv, 1), v.repeat_interleave(hq // hkv, 1)
+    s = (q @ k.transpose(-1, -2)) * d ** -0.5
+    s = s.masked_fill(~torch.ones(S, S, dtype=torch.bool).tril(), float("-inf"))
+    p = torch.exp(s - s.amax(-1, keepdim=True))
+    denom = p.sum(-1, keepdim=True)
+    if "p" in mode:
+        p = _bf(p)
+    o = ((p @ v) / denom).transpose(1, 2).reshape(B, S, hq * d)
+    o = _bf(o) if "o" in mode else gem(o)
+    h = x + proj("self_attn.o_proj", o)
+    x2 = gem(OB.rms_norm(h, norms[1], SHAPE.norm_eps))
+    act = gem(torch.nn.functional.silu(proj("mlp.gate_proj", x2)) * proj("mlp.up_proj", x2))
+    return h + proj("mlp.down_proj", act)
+
+
+@pytest.fixture(scope="module")
+def problem():
+    g = torch.Generator().manual_seed(1)
+    h, mlp, hq, hkv, d = SHAPE.hidden, SHAPE.intermediate, SHAPE.n_heads, SHAPE.n_kv_heads, SHAPE.head_dim
+    shapes = {"mlp.down_proj": (h, mlp), "mlp.gate_proj": (mlp, h), "mlp.up_proj": (mlp, h),
+              "self_attn.k_proj": (hkv * d, h), "self_attn.o_proj": (h, hq * d),
+              "self_attn.q_proj": (hq * d, h), "self_attn.v_proj": (hkv * d, h)}
+    w = {n: _bf(torch.randn(*shapes[n], generator=g, dtype=torch.float64) * 0.05) for n in NAMES}
+    norms = tuple(1 + 0.1 * torch.randn(h, generator=g, dtype=torch.float64) for _ in range(2))
+    x = torch.randn(2, 256, h, generator=g, dtype=torch.float64)
+    return w, norms, x
+
+
+def _errors(problem, bits, modes):
+    w, norms, x = problem
+    wq = {}
+    for n in NAMES:
+        qdq, _, _, _ = OQ.fake_quantize(w[n].float().numpy(), None, None, None, bits=bits, group_size=64,
+                                        mode="asym", dtype=np.float32)
+        wq[n] = torch.from_numpy(qdq).double()
+    exact = float(((_forward(x, wq, norms, set()) - _forward(x, w, norms, set())) ** 2).mean())
+    out = {}
+    for name, mode in modes.items():
+        loss = float(((_forward(x, wq, norms, mode) - _forward(x, w, norms, mode)) ** 2).mean())
+        out[name] = (loss - exact) / exact
+    return out
+
+
+MODES = {
+    "bf16": {"act", "w", "qkv", "p", "o"},
+    "split": {"act", "w", "split", "qkv", "p", "o"},
+    "split, exact q/k/v": {"act", "w", "split", "p"},
+    "W' alone": {"w"},
+}
+
+
+def test_rounding_budget_at_8_bits(problem):
+    e = _errors(problem, 8, MODES)
+    assert 0.25 < e["bf16"] < 0.45, e
+    assert 0.05 < e["split"] < 0.15, e
+    assert e["split"] < 0.4 * e["bf16"], e
+    assert abs(e["split, exact q/k/v"]) < 0.02, e
+    assert 0.08 < e["W' alone"] < 0.2, e
+
+
+def test_rounding_budget_at_4_bits(problem):
+    e = _errors(problem, 4, MODES)
+    assert 0 < e["bf16"] < 3e-3, e
+    assert abs(e["split"]) < 1e-3 and abs(e["split"]) < e["bf16"], e

@@ -111,6 +111,29 @@ def test_scaling():
     assert o.stages["scoring"] == pytest.approx(TM._OWN_WIDTH * w.stages["scoring"])
 
 
+SPLIT_RUNS = json.loads((Path(__file__).parent / "golden" / "mi355x_split_runs.json").read_text())["runs"]
+
+
+@pytest.mark.parametrize("r", SPLIT_RUNS, ids=lambda r: r["model"])
+def test_split_precision_runs_inside_the_spread(r):
+    """Block tunes measured in bf16 and in split precision (2-bit, 200 steps,
+    16 batches of 8 x 2048, outlier rule on): both inside the rule's spread."""
+    model = ModelShape.from_config({**r["config"], "num_hidden_layers": 1, "vocab_size": 151936,
+                                    "tie_word_embeddings": True})
+    for split, key in ((False, "bf16_seconds"), (True, "split_seconds")):
+        run = RunShape(n_samples=128, seq_len=2048, batch_size=8, group_size=64, split=split)
+        ratio = r[key] / TM.predict_time(model, run, iters=200, outlier_rule=True).block
+        assert TM.SPREAD[0] <= ratio <= TM.SPREAD[1], (key, ratio)
+
+
+def test_split_precision_costs_more():
+    model = _shape("qwen2.5-3b")
+    plain = TM.predict_time(model, RunShape(128, 2048, 8, 64), iters=200, outlier_rule=False)
+    split = TM.predict_time(model, RunShape(128, 2048, 8, 64, split=True), iters=200, outlier_rule=False)
+    assert 1.4 * plain.block < split.block < 2.2 * plain.block
+    assert 2.8 < TM.split_forward_factor(model) < 3.0
+
+
 def test_refuses_no_steps():
     with pytest.raises(ValueError):
         TM.predict_time(_shape("qwen2.5-0.5b"), RunShape(128, 2048, 8, 64), iters=0, outlier_rule=False)

@@ -171,20 +171,40 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_v(const float* __restrict_
   const float4* dyr = reinterpret_cast<const float4*>(dy + row * H);
   const float4* hr = reinterpret_cast<const float4*>(h + row * H);
   const float4* w4 = reinterpret_cast<const float4*>(w);
-  float4 gy[NV], hv[NV];
+  const float4* qr = dres ? reinterpret_cast<const float4*>(dres + row * H) : nullptr;
+  const float r = rstd[row];
+  float4 gy[NV], hv[NV], rq[NV];
+  // Every load of the row is issued before any is used (indices clamped into
+  // the row, the excess lanes' values zeroed afterwards): predicated loads
+  // made the compiler wait for each column group's loads before issuing the
+  // next group's. The residual gradient comes with them, ahead of the
+  // reduction.
+  float4 dv[NV], wv[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int i = min(static_cast<int>(threadIdx.x) + k * kBlock, n4 - 1);
+    hv[k] = hr[i];
+    dv[k] = dyr[i];
+    wv[k] = w4[i];
+  }
+  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (qr) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) rq[k] = qr[min(static_cast<int>(threadIdx.x) + k * kBlock, n4 - 1)];
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) rq[k] = z;
+  }
   float dot = 0.0f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    const int i = threadIdx.x + k * kBlock;
-    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    hv[k] = i < n4 ? hr[i] : z;
-    const float4 d = i < n4 ? dyr[i] : z;
-    const float4 g = i < n4 ? w4[i] : z;
-    gy[k] = make_float4(d.x * g.x, d.y * g.y, d.z * g.z, d.w * g.w);  // dy w
+    const bool in = static_cast<int>(threadIdx.x) + k * kBlock < n4;
+    if (!in) hv[k] = z;
+    const float4 d = in ? dv[k] : z;
+    gy[k] = make_float4(d.x * wv[k].x, d.y * wv[k].y, d.z * wv[k].z, d.w * wv[k].w);  // dy w
     dot += gy[k].x * hv[k].x + gy[k].y * hv[k].y + gy[k].z * hv[k].z + gy[k].w * hv[k].w;
   }
   dot = block_sum_f32(dot, smem);
-  const float r = rstd[row];
   const float c = r * r * r * dot / static_cast<float>(H);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -192,10 +212,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_v(const float* __restrict_
     if (i >= n4) continue;
     float4 g = make_float4(r * gy[k].x - c * hv[k].x, r * gy[k].y - c * hv[k].y,
                            r * gy[k].z - c * hv[k].z, r * gy[k].w - c * hv[k].w);
-    if (dres) {
-      const float4 q = reinterpret_cast<const float4*>(dres + row * H)[i];
-      g.x += q.x; g.y += q.y; g.z += q.z; g.w += q.w;
-    }
+    g.x += rq[k].x; g.y += rq[k].y; g.z += rq[k].z; g.w += rq[k].w;  // zero without dres
     if (dh_bf16) reinterpret_cast<uint2*>(dh_bf16 + row * H)[i] = pack4_bf16(g.x, g.y, g.z, g.w);
     if (dh_f32) reinterpret_cast<float4*>(dh_f32 + row * H)[i] = g;
   }

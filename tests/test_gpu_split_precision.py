@@ -292,16 +292,52 @@ def test_split_tune_follows_the_oracle():
         assert np.array_equal(q.scale.cpu().numpy(), scale.reshape(q.scale.shape))
 
 
+@pytest.mark.parametrize("suppress", [False, True])
+def test_split_step_in_pieces_is_the_batch_step(suppress):
+    """A split-precision step in pieces: the whole batch's outlier threshold,
+    its loss to the order of additions, its weight gradients within fp32
+    summation order, as in bf16."""
+    _case("split pieces", suppress)
+    B, S = 4, 128
+    w = _weights(TINY, seed=8)
+    x = torch.randn(B * S, TINY.hidden, generator=torch.Generator().manual_seed(9))
+    t = _oracle(TINY, w, x, B, S).float()
+    scheme = QuantScheme(bits=2, group_size=64, symmetry=Symmetry.ASYMMETRIC)
+    out = {}
+    for pieces in (1, 3):
+        runner = QuantizationRunner(scheme, TuningConfig(iters=2, batch_size=B, n_samples=B, seq_len=S,
+                                                         micro_batches=pieces), split_precision=True)
+        eng = runner.engine(TINY, B * S, dev())
+        assert eng.split
+        eng.set_block(_dev(w))
+        eng.load_dense({n: (w.linears[n].float() * 1.01).to(dev()) for n in LAYERS})
+        loss = torch.zeros(1, device=dev())
+        xd, td = x.to(dev()), t.to(dev())
+        runner._gradients(eng, xd, td, torch.empty_like(xd), suppress, loss)
+        torch.cuda.synchronize()
+        out[pieces] = (float(loss), float(eng.threshold), {k: v.clone() for k, v in eng.dw.items()})
+    (l1, t1, d1), (l3, t3, d3) = out[1], out[3]
+    if suppress:
+        assert t3 == t1
+    assert l3 == pytest.approx(l1, rel=1e-6)
+    for k in d1:
+        assert float((d3[k] - d1[k]).norm() / d1[k].norm()) < 1e-5, k
+
+
 TINY_MODEL = dict(model_type="qwen2", hidden_size=256, num_attention_heads=4, num_key_value_heads=2,
                   intermediate_size=512, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=2,
                   vocab_size=512, tie_word_embeddings=True)
 
 
-def test_quantize_in_split_precision(tmp_path):
-    _case("api split precision")
+@pytest.mark.parametrize(("bits", "symmetry"), [(8, Symmetry.ASYMMETRIC), (2, Symmetry.SYMMETRIC)])
+def test_quantize_in_split_precision(tmp_path, bits, symmetry):
+    """End to end at 200-token sequences: 8-bit asymmetric, and 2-bit
+    symmetric with the searched scales (whose input statistics come from a
+    split-precision forward)."""
+    _case("api split precision", bits, symmetry)
     src = write_random_checkpoint(tmp_path / "m", TINY_MODEL, seed=1, std=0.05)
     tuning = TuningConfig(iters=6, batch_size=2, n_samples=4, seq_len=200)
-    res = api.quantize(src, output_dir=tmp_path / "q", bits=8, symmetry=Symmetry.ASYMMETRIC, tuning=tuning,
+    res = api.quantize(src, output_dir=tmp_path / "q", bits=bits, symmetry=symmetry, tuning=tuning,
                        seed=5, split_precision=True)
     assert len(res.summary.blocks) == 2
     for b in res.summary.blocks:

@@ -440,7 +440,9 @@ def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
     resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry,
                                        average_bits=average_bits, candidate_bits=candidate_bits,
                                        remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
-    shape, run = _run_shape(config, resolved, tuning or TuningConfig(), average_bits=average_bits, plan=None,
+    tuning = tuning or TuningConfig()
+    _check_calibration_sizes(tuning)
+    shape, run = _run_shape(config, resolved, tuning, average_bits=average_bits, plan=None,
                             widths=candidate_bits if average_bits is not None else (resolved.bits,),
                             gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
                             scoring_seq_len=scoring_seq_len, scoring_batch=scoring_batch_size,
@@ -465,6 +467,7 @@ def predict_time(model: str | Path, *, bits: int = 4, group_size: int = 64,
                                        average_bits=average_bits, candidate_bits=candidate_bits,
                                        remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
     tuning = tuning or TuningConfig()
+    _check_calibration_sizes(tuning)
     shape, run = _run_shape(config, resolved, tuning, average_bits=average_bits, plan=None,
                             widths=candidate_bits if average_bits is not None else (resolved.bits,),
                             gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
@@ -475,6 +478,13 @@ def predict_time(model: str | Path, *, bits: int = 4, group_size: int = 64,
                             candidate_bits=candidate_bits if average_bits is not None else (),
                             per_layer_recipe=per_layer_recipe, scoring_samples=scoring_samples,
                             scoring_seq_len=scoring_seq_len, gradient_source=sensitivity_gradients)
+
+
+def _check_calibration_sizes(tuning: TuningConfig) -> None:
+    """mround/pipeline/calibration.py:442-447, before anything is predicted or loaded."""
+    if tuning.n_samples < 1 or tuning.seq_len < 1 or tuning.batch_size < 1:
+        raise CalibrationError(f"n_samples, seq_len, and batch_size must all be positive; got "
+                               f"{tuning.n_samples}, {tuning.seq_len}, {tuning.batch_size}")
 
 
 def _load_tokens(m: DecoderModel, calibration, tuning: TuningConfig, seed: int, device) -> torch.Tensor:
@@ -542,6 +552,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     for w in sorted(widths):
         require_mlx_representable(resolved.with_bits(w))
     tuning = tuning or TuningConfig()
+    _check_calibration_sizes(tuning)
     seed = 0 if seed is None else int(seed)
     mshape, rshape = _run_shape(_read_config(model), resolved, tuning, average_bits=average_bits, plan=plan,
                                 widths=candidate_bits if average_bits is not None else (resolved.bits,),

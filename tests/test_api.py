@@ -72,6 +72,9 @@ def test_quantize_refusals(tmp_path):
         api.quantize(tmp_path / "m", output_dir=tmp_path / "o", bits=7, device="cpu")
     with pytest.raises(CalibrationError, match="corpus"):
         api.quantize(tmp_path / "m", output_dir=tmp_path / "o", calibration="pile-10k", device="cpu")
+    with pytest.raises(CalibrationError, match="must all be positive"):
+        api.quantize(tmp_path / "m", output_dir=tmp_path / "o", device="cpu",
+                     tuning=TuningConfig(n_samples=2, batch_size=2, seq_len=0))
 
 
 def test_cli_random_model_and_errors(tmp_path, capsys):

@@ -12,7 +12,7 @@ from mround_amd import api
 from mround_amd.cli import GEOMETRIES, main
 from mround_amd.exceptions import ArchitectureError, MemoryBudgetError
 from mround_amd.pipeline.block import BlockEngine, aligned_length
-from mround_amd.pipeline.causal_lm import CausalLM, padded_length
+from mround_amd.pipeline.causal_lm import CausalLM
 from mround_amd.pipeline.checkpoint import block_shape, load_model, write_random_checkpoint
 from mround_amd.planner import memory as M
 

@@ -15,6 +15,7 @@ from mround_amd.pipeline.block import BlockEngine, aligned_length
 from mround_amd.pipeline.causal_lm import CausalLM
 from mround_amd.pipeline.checkpoint import block_shape, load_model, write_random_checkpoint
 from mround_amd.planner import memory as M
+from mround_amd.schemes import TuningConfig
 
 TINY = dict(model_type="qwen2", hidden_size=128, num_attention_heads=2, num_key_value_heads=1,
             intermediate_size=256, rms_norm_eps=1e-6, rope_theta=1e6, num_hidden_layers=2,
@@ -165,3 +166,11 @@ def test_cli_dry_run(tmp_path, capsys):
     assert "predicted peak" in out and "time: predicted" in out and "MI355X" in out
     assert main(["quantize", str(tmp_path / "m"), "-o", str(tmp_path / "o"), "--dry-run",
                  "--memory-budget", "0.000001"]) == 1
+    # split precision and a sequence length off the 128-row tile: accepted, and
+    # the prediction grows with both
+    assert main(["quantize", str(tmp_path / "m"), "-o", str(tmp_path / "o"), "--dry-run", "--memory-budget",
+                 "1000", "--split-precision", "--seq-len", "200", "--samples", "8", "--batch-size", "4"]) == 0
+    peaks = [api.predict_memory(tmp_path / "m", tuning=TuningConfig(n_samples=8, batch_size=4, seq_len=seq),
+                                split_precision=split, memory_budget=1 << 40, device="cpu").prediction.peak
+             for split, seq in ((False, 128), (True, 128), (True, 200))]
+    assert peaks[0] < peaks[1] < peaks[2], peaks

@@ -26,11 +26,16 @@ Printed as one JSON line:
              entries x10), 2-bit gs64; forward, backward + update, the update
              that also writes the next W', packing, and the fused quantize +
              pack of the export, against 8 TB/s;
+  like_for_like  the same block tuned with the reference's measured scheme
+             (symmetric codes, searched scale), one timed tune;
+  split_precision  the same block tuned with split-precision forward
+             products (bf16 hi/lo halves), one timed tune after one warm-up;
   cpu_baseline  the CPU path measured on the host's cores: the whole 200-step
              tune of one SmolLM2-135M-shaped block (8 x 512 tokens, 4-bit) in
              float32 (the oracle's PyTorch block under its NumPy fake
-             quantization and straight-through gradient), beside the same tune
-             on the GPU; the microbench kernels in NumPy; and, labelled as
+             quantization and straight-through gradient), median of 3 after a
+             warm-up, beside the same tune on the GPU; the microbench kernels
+             in NumPy over the whole matrix on every core; and, labelled as
              such, the 7B block tune extrapolated from a timed sample.
 
 ``--gpus N`` with N > 1 exits: the benchmark runs on one GPU only.
@@ -54,6 +59,10 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # Pro, MLX, symmetric with searched scale, 4 micro-batches (ledger row 130).
 REFERENCE_SEC_PER_BLOCK = 2119.5
 HBM_PEAK_GBPS = 8000.0
+# The whole default run (the timed tunes, the extra tunes, the microbench and
+# the CPU baseline) must end well inside the 600 s a benchmark run is given.
+DRIVER_LIMIT_S = 600.0
+T_START = time.perf_counter()
 
 # fake-quant microbench matrix (a 7B gate/up projection)
 ROWS, COLS = 18944, 3584
@@ -77,7 +86,7 @@ def block_workload(torch, dev, *, n_samples, seq_len, batch):
 
 
 def time_block_tune(torch, dev, args, *, workload=None, symmetric=False, steps=None, warmup=None,
-                    instrument=True):
+                    instrument=True, split=False):
     from mround_amd.pipeline.block import BlockWeights
     from mround_amd.pipeline.runner import DecoderBlock, QuantizationRunner
     from mround_amd.schemes import QuantScheme, ScaleInit, Symmetry, TuningConfig
@@ -94,7 +103,7 @@ def time_block_tune(torch, dev, args, *, workload=None, symmetric=False, steps=N
         scheme = QuantScheme(bits=BITS, group_size=GROUP, symmetry=Symmetry.ASYMMETRIC)
     tuning = TuningConfig(iters=args.iters, batch_size=args.batch, n_samples=args.samples,
                           seq_len=args.seq_len)
-    runner = QuantizationRunner(scheme, tuning)
+    runner = QuantizationRunner(scheme, tuning, split_precision=split)
     streams = [torch.empty_like(x) for x in entrance]
 
     def one():
@@ -109,7 +118,7 @@ def time_block_tune(torch, dev, args, *, workload=None, symmetric=False, steps=N
         torch.cuda.synchronize(dev)
         return time.perf_counter() - t0, summary.blocks[0]
 
-    tag = "sym searched" if symmetric else "asym"
+    tag = ("sym searched" if symmetric else "asym") + (", split precision" if split else "")
     eng = runner.engine(shape, entrance[0].shape[0], dev)
     flops = eng.flops()
 
@@ -337,10 +346,15 @@ def cpu_baseline(args, tokens_per_batch, batches):
                    f"(attention's quadratic term undercounted); x {args.iters} steps + {passes} forward "
                    f"passes"),
     }
-    print("bench: cpu baseline, SmolLM2-shaped block tune", file=sys.stderr, flush=True)
-    secs, initial, final = smollm2_cpu_tune(torch, threads)
+    print("bench: cpu baseline, SmolLM2-shaped block tune (warm-up, 20 steps)", file=sys.stderr, flush=True)
+    smollm2_cpu_tune(torch, threads, steps=20)
+    runs = []
+    for i in range(CPU_REPS):
+        print(f"bench: cpu baseline, SmolLM2-shaped block tune {i + 1}/{CPU_REPS}", file=sys.stderr, flush=True)
+        runs.append(smollm2_cpu_tune(torch, threads))
+    secs, initial, final = sorted(runs)[CPU_REPS // 2]
     print("bench: cpu baseline, microbench kernels", file=sys.stderr, flush=True)
-    kern = cpu_kernels(torch)
+    kern = cpu_kernels(threads)
     return {
         "value": round(secs, 2),
         "unit": "s per SmolLM2-135M-shaped block tune (measured)",
@@ -349,12 +363,13 @@ def cpu_baseline(args, tokens_per_batch, batches):
         "sample": ("the whole 200-step tune of one SmolLM2-135M-shaped block (hidden 576, 9/3 heads x 64, "
                    "SwiGLU 1536; 8 x 512 tokens, 4-bit asym gs64, lr 5e-3): targets, score, 200 steps, "
                    f"score, in float32 on {threads} host threads (PyTorch block, NumPy fake quantization "
-                   "and straight-through gradient)"),
+                   f"and straight-through gradient); median of {CPU_REPS} after a 20-step warm-up"),
+        "runs_s": [round(r[0], 2) for r in runs],
         "loss": {"initial": initial, "final": final},
         "cpu": _cpu_model(),
         "kernels_18944x3584_2bit_gs64": kern,
-        "kernels_note": ("NumPy float32 on one thread, median of 3 over a quarter of the rows, scaled; GB/s "
-                         "over the algorithmic bytes of the GPU figures"),
+        "kernels_note": (f"NumPy float32 over the whole matrix, its rows dealt to {threads} threads, median of "
+                         "3 after a warm-up; GB/s over the algorithmic bytes of the GPU figures"),
         "extrapolated_7b_block": extrapolated,
     }
 
@@ -367,6 +382,7 @@ def cpu_baseline(args, tokens_per_batch, batches):
 SHAPE_135M = dict(hidden=576, n_heads=9, n_kv_heads=3, head_dim=64, intermediate=1536, norm_eps=1e-5,
                   rope_theta=1e4)
 SMOL_B, SMOL_S, SMOL_LR, SMOL_BITS = 8, 512, 5e-3, 4
+CPU_REPS = 3  # the CPU tune's repetitions (median reported)
 
 
 def smollm2_workload(torch):
@@ -410,11 +426,12 @@ def smollm2_gpu_tune(torch, dev, reps=3):
     return sorted(times[1:])[len(times[1:]) // 2]
 
 
-def smollm2_cpu_tune(torch, threads):
+def smollm2_cpu_tune(torch, threads, steps=200):
     """The same tune on the host in float32: the oracle's block (PyTorch, all
     threads) under the oracle's NumPy fake quantization and straight-through
-    gradient, the sign step and projection; targets, score, 200 steps, score.
-    Returns (seconds, initial loss, final loss)."""
+    gradient, the sign step and projection; targets, score, ``steps`` steps
+    (of a 200-step schedule), score. Returns (seconds, initial loss, final
+    loss)."""
     import numpy as np
 
     from oracle import block as OB
@@ -457,7 +474,7 @@ def smollm2_cpu_tune(torch, threads):
 
     with torch.no_grad():
         initial = float(loss_at(params, False)[0])
-    for step in range(200):
+    for step in range(steps):
         loss, leaf = loss_at(params, True)
         loss.backward()
         rate = SMOL_LR * (1.0 - step / 200)
@@ -471,47 +488,57 @@ def smollm2_cpu_tune(torch, threads):
     return time.perf_counter() - t0, initial, final
 
 
-def cpu_kernels(torch, sample_div=4, reps=3):
-    """The microbench kernels on the host (NumPy float32, one thread) at 2-bit
-    gs64: fake-quant forward, straight-through gradient + sign step, packing;
-    median of reps over the matrix's first rows / sample_div, scaled to the
-    matrix, with the same algorithmic bytes the GPU figures use."""
+def cpu_kernels(threads, reps=3):
+    """The microbench kernels on the host at 2-bit gs64 over the whole
+    18944 x 3584 matrix: the oracle's NumPy float32 fake-quant forward,
+    straight-through gradient + sign step + projection, and packing, the
+    matrix's rows dealt to ``threads`` threads (NumPy's array operations run
+    outside the interpreter lock); median of ``reps`` after a warm-up, with
+    the same algorithmic bytes the GPU figures use."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
 
     from oracle import packing as OP
     from oracle import quantize as OQ
 
-    rows = ROWS // sample_div
     gen = np.random.default_rng(0)
-    w = (gen.standard_normal((rows, COLS), dtype=np.float32) * 0.02)
-    v = gen.random((rows, COLS), dtype=np.float32) - 0.5
-    g = gen.standard_normal((rows, COLS), dtype=np.float32)
-    ones = np.ones((rows, COLS // GROUP), np.float32)
+    w = (gen.standard_normal((ROWS, COLS), dtype=np.float32) * 0.02)
+    v = gen.random((ROWS, COLS), dtype=np.float32) - 0.5
+    g = gen.standard_normal((ROWS, COLS), dtype=np.float32)
+    ones = np.ones((ROWS, COLS // GROUP), np.float32)
+    cuts = [ROWS * i // threads for i in range(threads + 1)]
+    chunks = [slice(a, b) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
+    codes = np.empty((ROWS, COLS), np.int64)
+    pool = ThreadPoolExecutor(len(chunks))
+
+    def run(fn):
+        list(pool.map(fn, chunks))
 
     def med(fn):
+        run(fn)  # warm-up
         ts = []
         for _ in range(reps):
             t0 = time.perf_counter()
-            fn()
+            run(fn)
             ts.append(time.perf_counter() - t0)
-        return sorted(ts)[reps // 2] * sample_div
+        return sorted(ts)[reps // 2]
 
-    out = {}
-    codes = None
+    def fwd(r):
+        c = OQ.fake_quantize(w[r], v[r], ones[r], ones[r], bits=BITS, group_size=GROUP, mode="asym")[1]
+        codes[r] = c.reshape(codes[r].shape)
 
-    def fwd():
-        nonlocal codes
-        codes = OQ.fake_quantize(w, v, ones, ones, bits=BITS, group_size=GROUP, mode="asym")[1]
+    def bwd(r):
+        gv, ga, gb = OQ.quantize_grad(w[r], v[r], ones[r], ones[r], g[r], bits=BITS, group_size=GROUP,
+                                      mode="asym")
+        o = ones[r]
+        OQ.project_params(OQ.sign_step(v[r].reshape(gv.shape), gv, 0.005),
+                          OQ.sign_step(o, ga.reshape(o.shape), 0.005),
+                          OQ.sign_step(o, gb.reshape(o.shape), 0.005), "asym")
 
-    def bwd():
-        gv, ga, gb = OQ.quantize_grad(w, v, ones, ones, g, bits=BITS, group_size=GROUP, mode="asym")
-        OQ.project_params(OQ.sign_step(v.reshape(gv.shape), gv, 0.005), OQ.sign_step(ones, ga.reshape(ones.shape), 0.005),
-                          OQ.sign_step(ones, gb.reshape(ones.shape), 0.005), "asym")
-
-    out["fwd"] = med(fwd)
-    out["bwd_update"] = med(bwd)
-    flat = codes.reshape(rows, COLS).astype(np.int64)
-    out["pack"] = med(lambda: OP.pack_codes(flat, BITS))
+    out = {"fwd": med(fwd), "bwd_update": med(bwd)}
+    out["pack"] = med(lambda r: OP.pack_codes(codes[r], BITS))
+    pool.shutdown()
     n, ng = ROWS * COLS, ROWS * COLS // GROUP
     nbytes = {"fwd": n * 8 + 8 * ng, "bwd_update": n * 14 + 16 * ng, "pack": n * (1 + BITS / 8)}
     return {k: {"s": round(t, 3), "gbps": round(nbytes[k] / t / 1e9, 2)} for k, t in out.items()}
@@ -603,6 +630,90 @@ def profile_kernels(torch, K, dev, steps):
     print(json.dumps({"profile_kernels": True, "steps": steps}))
 
 
+def gemm_vs_library(torch, K, dev, reps=20):
+    """The 7B block's twelve GEMMs (16384 tokens) three ways, each timed with
+    HIP events over ``reps`` launches after 3 untimed ones: the in-tree
+    kernel as the block launches it (its epilogue and output type), the
+    in-tree kernel with a plain bf16 store, and the vendor library through
+    ``torch.matmul`` on the same operands and layout (bf16 out). One JSON
+    line per product, then a summary line."""
+    T, h, mlp = 16384, SHAPE_7B["hidden"], SHAPE_7B["intermediate"]
+    hq_d = SHAPE_7B["n_heads"] * SHAPE_7B["head_dim"]
+    q = (SHAPE_7B["n_heads"] + 2 * SHAPE_7B["n_kv_heads"]) * SHAPE_7B["head_dim"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *s_: (torch.randn(*s_, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    f32 = lambda *s_: torch.empty(*s_, device=dev)
+    bf = lambda *s_: torch.empty(*s_, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(128 << 20, dtype=torch.uint8, device=dev)
+    x, wqkv, bias = rnd(T, h), rnd(q, h), torch.randn(q, device=dev) * 0.02
+    attn, wo, resid = rnd(T, hq_d), rnd(h, hq_d), torch.randn(T, h, device=dev)
+    wgu, wd, act, gu = rnd(2 * mlp, h), rnd(h, mlp), rnd(T, mlp), rnd(T, 2 * mlp)
+    dout, dgu, dh, dqkv = rnd(T, h), rnd(T, 2 * mlp), rnd(T, h), rnd(T, q)
+    # name: (layout, A, B, M, N, K, the block's own launch)
+    probs = {
+        "gemm_qkv": ("nt", x, wqkv, T, q, h, lambda: K.gemm("nt", x, wqkv, bf(T, q), M=T, N=q, K=h, bias=bias,
+                                                            workspace=ws)),
+        "gemm_o": ("nt", attn, wo, T, h, hq_d, lambda: K.gemm("nt", attn, wo, f32(T, h), M=T, N=h, K=hq_d,
+                                                              resid=resid, workspace=ws)),
+        "gemm_gate_up": ("nt", x, wgu, T, 2 * mlp, h, lambda: K.gemm_swiglu(x, wgu, bf(T, mlp), bf(T, 2 * mlp),
+                                                                            workspace=ws)),
+        "gemm_down": ("nt", act, wd, T, h, mlp, lambda: K.gemm("nt", act, wd, f32(T, h), M=T, N=h, K=mlp,
+                                                               resid=resid, workspace=ws)),
+        "gemm_dact": ("nn", dout, wd, T, mlp, h, lambda: K.gemm_swiglu_bwd(dout, wd, gu, bf(T, 2 * mlp),
+                                                                           workspace=ws)),
+        "gemm_dw_down": ("tn", dout, act, h, mlp, T, lambda: K.gemm("tn", dout, act, f32(h, mlp), M=h, N=mlp,
+                                                                    K=T, workspace=ws)),
+        "gemm_dx_gate_up": ("nn", dgu, wgu, T, h, 2 * mlp, lambda: K.gemm("nn", dgu, wgu, f32(T, h), M=T, N=h,
+                                                                          K=2 * mlp, workspace=ws)),
+        "gemm_dw_gate_up": ("tn", dgu, x, 2 * mlp, h, T, lambda: K.gemm("tn", dgu, x, f32(2 * mlp, h),
+                                                                        M=2 * mlp, N=h, K=T, workspace=ws)),
+        "gemm_dattn": ("nn", dh, wo, T, hq_d, h, lambda: K.gemm("nn", dh, wo, bf(T, hq_d), M=T, N=hq_d, K=h,
+                                                                workspace=ws)),
+        "gemm_dw_o": ("tn", dh, attn, h, hq_d, T, lambda: K.gemm("tn", dh, attn, f32(h, hq_d), M=h, N=hq_d,
+                                                                 K=T, workspace=ws)),
+        "gemm_dw_qkv": ("tn", dqkv, x, q, h, T, lambda: K.gemm("tn", dqkv, x, f32(q, h), M=q, N=h, K=T,
+                                                               workspace=ws)),
+        "gemm_dx_qkv": ("nn", dqkv, wqkv, T, h, q, lambda: K.gemm("nn", dqkv, wqkv, f32(T, h), M=T, N=h, K=q,
+                                                                  workspace=ws)),
+    }
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) / reps
+
+    rows = {}
+    for name, (lay, A, B, M, N, Kd, own) in probs.items():
+        c = bf(M, N)
+        if lay == "nt":
+            lib_fn, plain = (lambda A=A, B=B: torch.matmul(A, B.t())), (lambda: K.gemm("nt", A, B, c, M=M, N=N, K=Kd,
+                                                                                      workspace=ws))
+        elif lay == "nn":
+            lib_fn, plain = (lambda A=A, B=B: torch.matmul(A, B)), (lambda: K.gemm("nn", A, B, c, M=M, N=N, K=Kd,
+                                                                                  workspace=ws))
+        else:
+            lib_fn, plain = (lambda A=A, B=B: torch.matmul(A.t(), B)), (lambda: K.gemm("tn", A, B, c, M=M, N=N,
+                                                                                      K=Kd, workspace=ws))
+        fl = 2.0 * M * N * Kd
+        r = {"layout": lay, "M": M, "N": N, "K": Kd}
+        for key, fn in (("in_tree_block_epilogue", own), ("in_tree_plain_bf16", plain), ("library_bf16", lib_fn)):
+            ms = timed(fn)
+            r[key] = {"ms": round(ms, 4), "tflops": round(fl / ms / 1e9, 1)}
+        r["in_tree_over_library"] = round(r["library_bf16"]["ms"] / r["in_tree_plain_bf16"]["ms"], 3)
+        rows[name] = r
+        print(json.dumps({name: r}), flush=True)
+    tot = {k: sum(r[k]["ms"] for r in rows.values()) for k in ("in_tree_block_epilogue", "in_tree_plain_bf16",
+                                                                "library_bf16")}
+    print(json.dumps({"gemm_vs_library_total_ms": {k: round(v, 3) for k, v in tot.items()}}), flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -619,9 +730,13 @@ def main(argv=None):
     ap.add_argument("--no-microbench", action="store_true")
     ap.add_argument("--no-like-for-like", action="store_true",
                     help="skip the extra symmetric searched-scale tune")
+    ap.add_argument("--no-split-extra", action="store_true",
+                    help="skip the extra split-precision tune")
     ap.add_argument("--kernel-sweep", action="store_true",
                     help="only the fake-quant / update / pack microbench at bits 2, 3, 4, 8 x group "
                          "sizes 32, 64, 128 (one JSON line each)")
+    ap.add_argument("--gemm-vs-library", action="store_true",
+                    help="only the 7B block's twelve GEMMs, in-tree against the vendor library")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only launch the fake-quant forward and a copy of known size (counter runs)")
     args = ap.parse_args(argv)
@@ -643,6 +758,9 @@ def main(argv=None):
 
     if args.profile_kernels:
         profile_kernels(torch, K, dev, args.steps)
+        return 0
+    if args.gemm_vs_library:
+        gemm_vs_library(torch, K, dev)
         return 0
     if args.kernel_sweep:
         for bits in (2, 3, 4, 8):
@@ -670,6 +788,17 @@ def main(argv=None):
                 "reference_published_s": REFERENCE_SEC_PER_BLOCK,
                 "reference_setting": "Apple M5 MacBook Pro 32 GB, MLX 0.32, same scheme, 4 micro-batches",
                 "speedup_vs_reference": round(REFERENCE_SEC_PER_BLOCK / sym["times"][0], 1)}
+    split = None
+    if not args.no_split_extra:
+        # the block objective in split precision (bf16 hi/lo halves carried
+        # through every forward product, the reference's three-product remedy)
+        sp = time_block_tune(torch, dev, args, workload=tune["workload"], split=True, steps=1, warmup=1,
+                             instrument=False)
+        spr = sp["results"][-1]
+        split = {"scheme": f"{BITS}-bit asymmetric, gs{GROUP}, split-precision forward products",
+                 "value": round(sp["times"][0], 3), "unit": "s",
+                 "over_default": round(sp["times"][0] / sec, 3),
+                 "loss": {"initial": spr.initial_loss, "final": spr.final_loss, "reverted": spr.reverted}}
     del tune["workload"]
     fq = None
     if not args.no_microbench:
@@ -729,10 +858,13 @@ def main(argv=None):
             "avg_launch_ms": dk["avg_ms"],
         },
         "like_for_like": like,
+        "split_precision": split,
         "kernels": kernels,
         "fake_quant": fq,
         "cpu_baseline": cpu,
     }
+    line["bench_wall_s"] = round(time.perf_counter() - T_START, 1)
+    line["fits_in_driver_run"] = line["bench_wall_s"] < DRIVER_LIMIT_S
     print(json.dumps(line))
     return 0
 

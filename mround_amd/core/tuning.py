@@ -15,6 +15,9 @@ loss and dL/dr by the loss kernels (the outlier rule's threshold on the
 device), and the straight-through gradient, sign step and projection in one
 fused kernel on ``v``, ``alpha`` and ``beta`` in place. The loss is read
 back once per step, as the reference evaluates once per step.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

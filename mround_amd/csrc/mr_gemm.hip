@@ -148,6 +148,7 @@ __device__ __forceinline__ void load_lds16(rsrc_t r, uint8_t* lds, int voff) {
 template <int ROWS>
 struct KMajorDirect {
   static constexpr int INSTR = ROWS * 8 / 64 / kLoaders;  // instructions per loading wave
+  static_assert(INSTR * kLoaders * 64 == ROWS * 8, "the loading waves must cover every chunk of the tile");
   int voff[INSTR];
   __device__ __forceinline__ void init(int64_t ld, int row0, int rows_valid) {
     const int lane = threadIdx.x & 63;
@@ -196,6 +197,7 @@ struct MNMajorDirect {
   static constexpr int CPR = ROWS / 8;         // 16-byte chunks per k-row
   static constexpr int RPI = 64 / CPR;         // k-rows per wave instruction
   static constexpr int INSTR = BK / RPI / kLoaders;   // instructions per loading wave
+  static_assert(INSTR * kLoaders * RPI == BK, "the loading waves must cover every k-row of the tile");
   static constexpr int ROWB = ROWS * 2;        // bytes per k-row
   int voff[INSTR];
   __device__ __forceinline__ void init(int64_t ld, int row0, int rows_valid) {

@@ -190,14 +190,22 @@ def split_gemm_problems(shape: BlockShape, tokens: int) -> list[tuple[int, int, 
 
 
 def workspace_bytes(shape: BlockShape, batch: int, seq_len: int,
-                    extra_gemms: tuple[tuple[int, int, int], ...] = ()) -> tuple[int, int]:
+                    extra_gemms: tuple[tuple[int, int, int], ...] = (), split: bool = False) -> tuple[int, int]:
     """Bytes of the GEMM k-split workspace (the largest any of the block's
-    products, or ``extra_gemms``, plans) and of the attention backward's dK/dV
-    partials (its automatic head split) for a block engine."""
-    probs = gemm_problems(shape, batch * seq_len) + list(extra_gemms)
-    gemm = max(K.gemm_workspace_bytes(M, N, Kd) for M, N, Kd in probs)
-    attn = K.attn_bwd_workspace_bytes(batch=batch, seq_len=seq_len, n_heads=shape.n_heads,
-                                      n_kv_heads=shape.n_kv_heads, head_dim=shape.head_dim)
+    products, its split-precision products with ``split``, or the caller's
+    ``extra_gemms`` plans) and of the attention backward's dK/dV partials (its
+    automatic head split) for a block engine of ``batch`` sequences. The
+    engine also runs any smaller number of sequences (the pieces of a step,
+    ``set_sequences``), whose plans can ask for more (a grid that needs no
+    head split at 8 sequences can at 7), so both are the largest over
+    1..``batch`` sequences: a piece never runs short of workspace."""
+    gemm = max([K.gemm_workspace_bytes(M, N, Kd) for M, N, Kd in extra_gemms], default=0)
+    attn = 0
+    for n in range(1, batch + 1):
+        probs = gemm_problems(shape, n * seq_len) + (split_gemm_problems(shape, n * seq_len) if split else [])
+        gemm = max(gemm, max(K.gemm_workspace_bytes(M, N, Kd) for M, N, Kd in probs))
+        attn = max(attn, K.attn_bwd_workspace_bytes(batch=n, seq_len=seq_len, n_heads=shape.n_heads,
+                                                    n_kv_heads=shape.n_kv_heads, head_dim=shape.head_dim))
     return gemm, attn
 
 
@@ -267,8 +275,6 @@ class BlockEngine:
         if not 1 <= self.real_len <= seq_len:
             raise ArchitectureError(f"{self.real_len} tokens do not fit sequences of {seq_len} rows")
         self.split = bool(split)
-        if self.split:
-            extra_gemms = tuple(extra_gemms) + tuple(split_gemm_problems(shape, batch * seq_len))
         self.device = torch.device(device)
         T, h, mlp = batch * seq_len, shape.hidden, shape.intermediate
         self.tokens = T
@@ -311,7 +317,7 @@ class BlockEngine:
         # the library's scratch for the GEMM k-split partials and the attention
         # backward's dK/dV partials, owned here (extra_gemms: products a caller
         # runs with this workspace besides the block's own)
-        gemm_b, attn_b = workspace_bytes(shape, batch, seq_len, extra_gemms)
+        gemm_b, attn_b = workspace_bytes(shape, batch, seq_len, extra_gemms, self.split)
         self.gemm_ws = e(gemm_b, dt=torch.uint8) if gemm_b else None
         self.attn_ws = e(attn_b, dt=torch.uint8) if attn_b else None
         self.x_in: torch.Tensor | None = None  # block input of the last saving forward

@@ -5,6 +5,9 @@ on total storage: a multiple-choice knapsack solved exactly by dynamic
 programming over exact cumulative costs with Pareto pruning. The search runs
 in native code (``mr_allocate_bits`` in ``libmround_hip.so``, host only); this
 module keeps the reference's types, validation and messages.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

@@ -109,13 +109,11 @@ def library_workspace_bytes(m: ModelShape, tokens: int, seq_len: int,
                             extra_gemms: tuple[tuple[int, int, int], ...] = (), split: bool = False) -> int:
     """The GEMM k-split and attention dK/dV workspaces a ``BlockEngine`` at
     ``tokens`` tokens owns (the library's size queries)."""
-    from mround_amd.pipeline.block import BlockShape, split_gemm_problems, workspace_bytes
+    from mround_amd.pipeline.block import BlockShape, workspace_bytes
 
     shape = BlockShape(hidden=m.hidden, n_heads=m.heads, n_kv_heads=m.kv_heads, head_dim=m.head_dim,
                        intermediate=m.intermediate)
-    if split:
-        extra_gemms = tuple(extra_gemms) + tuple(split_gemm_problems(shape, tokens))
-    return sum(workspace_bytes(shape, tokens // seq_len, seq_len, extra_gemms))
+    return sum(workspace_bytes(shape, tokens // seq_len, seq_len, extra_gemms, split))
 
 
 def split_bytes(m: ModelShape, tokens: int) -> int:

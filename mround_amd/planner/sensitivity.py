@@ -5,6 +5,9 @@ with ``g`` the loss gradient at the quantized weights from a calibration
 backward pass. The per-batch term runs on the GPU (``mr_delta_loss``: every
 candidate width in one read of W and g, each term accumulated in fp64); the
 storage cost and the allocator's input are host arithmetic.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations

@@ -35,6 +35,9 @@ backward at each width (``own_width``); it scales with the scoring tokens
 (measured at 128 x 1024).
 
 Every run records the prediction beside what it measured.
+
+Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
+see NOTICE.
 """
 
 from __future__ import annotations
@@ -67,19 +70,15 @@ _SCORING = (9.927e-02, 3.454e-02, 8.859e-10, 1.649e-10)  # fixed, per block, per
 _OWN_WIDTH = 2.79
 _SCORING_TOKENS = SENSITIVITY_SAMPLES * SENSITIVITY_SEQ_LEN
 
-_MINUTE = 60
-_HOUR = 60 * _MINUTE
-
-
 def _duration(seconds: float) -> str:
-    """A span as a person reads it: 4h28m, 7m14s, 45s."""
-    if seconds >= _HOUR - _MINUTE / 2:
-        minutes = round(seconds / _MINUTE)
-        return f"{minutes // _MINUTE}h{minutes % _MINUTE:02d}m"
-    whole = round(seconds)
-    if whole >= _MINUTE:
-        return f"{whole // _MINUTE}m{whole % _MINUTE:02d}s"
-    return f"{whole}s"
+    """``seconds`` spoken the way a progress line says it: whole seconds under a
+    minute ("45s"), minutes and seconds under 59.5 minutes ("7m14s"), hours and
+    minutes from there on ("4h28m")."""
+    if seconds < 3570:
+        mins, secs = divmod(round(seconds), 60)
+        return f"{mins}m{secs:02d}s" if mins else f"{secs}s"
+    hours, mins = divmod(round(seconds / 60), 60)
+    return f"{hours}h{mins:02d}m"
 
 
 @dataclasses.dataclass(frozen=True)

@@ -5,11 +5,13 @@ sequences of any ``seq_len`` (``TuningConfig.seq_len``, mround/schemes.py:266;
 ``calibration.py:442`` asks only for seq_len >= 1), so the padded run must be
 the run on the ``seq_len``-token sequences:
 
-* padding never reaches a token row, the loss or a gradient: whatever the
-  padding rows hold, the loss, the outlier threshold and every dL/dW' are
-  bit-identical (causal attention keeps later rows out of earlier ones, and
-  the padding rows' residuals are zero, so their gradient terms are exact
-  zeros);
+* padding never reaches a token row, the loss or a gradient: whatever
+  finite values the padding rows hold, the loss, the outlier threshold and
+  every dL/dW' are bit-identical (causal attention keeps later rows out of
+  earlier ones, and the padding rows' residuals are zero, so their gradient
+  terms are exact zeros: 0 times a finite activation; an inf or NaN padding
+  row would make them NaN, and the API pads with token 0's embedding, which
+  is finite);
 * the loss and dL/dW' match the float64 oracle run on the unpadded
   ``seq_len``-token sequences, within the bars of the unpadded block tests
   (loss 1e-2 relative, dL/dW' 5e-2 normwise with under 1e-2 of the gradient
@@ -210,8 +212,8 @@ def test_padded_tune_follows_the_oracle_tune():
 def test_a_tune_does_not_see_the_padding():
     """A whole block tune (searched symmetric scales, whose search weighs the
     layers' inputs, 2 bits with the outlier rule, steps replayed as graphs)
-    is bit-identical whatever the padding rows of its inputs and targets
-    hold."""
+    is bit-identical whatever finite values the padding rows of its inputs
+    and targets hold."""
     _case("padded tune invariance")
     iters, real, B = 6, 200, 2
     rows = aligned_length(real)

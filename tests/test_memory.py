@@ -174,3 +174,24 @@ def test_cli_dry_run(tmp_path, capsys):
                                 split_precision=split, memory_budget=1 << 40, device="cpu").prediction.peak
              for split, seq in ((False, 128), (True, 128), (True, 200))]
     assert peaks[0] < peaks[1] < peaks[2], peaks
+
+
+def test_engine_workspaces_cover_every_piece():
+    """An engine of 8 sequences of the 7B geometry also runs pieces of fewer
+    (``set_sequences``): at 7 the dK/dV grid falls under the size that needs
+    no head split and the library plans 117,440,512 bytes of partials, where
+    8 sequences plan none. The engine's workspaces are the largest over
+    every piece size, so no piece's launch falls back to an allocation of
+    the binding's own."""
+    from mround_amd import kernels as K
+    from mround_amd.pipeline.block import BlockShape, gemm_problems, workspace_bytes
+
+    s = BlockShape(hidden=3584, n_heads=28, n_kv_heads=4, head_dim=128, intermediate=18944, attn_bias=True)
+    q = dict(seq_len=2048, n_heads=28, n_kv_heads=4, head_dim=128)
+    assert K.attn_bwd_workspace_bytes(batch=8, **q) == 0
+    assert K.attn_bwd_workspace_bytes(batch=7, **q) == 117_440_512
+    gemm, attn = workspace_bytes(s, 8, 2048)
+    for n in range(1, 9):
+        assert attn >= K.attn_bwd_workspace_bytes(batch=n, **q)
+        assert gemm >= max(K.gemm_workspace_bytes(M, N, Kd) for M, N, Kd in gemm_problems(s, n * 2048))
+    assert attn == max(K.attn_bwd_workspace_bytes(batch=n, **q) for n in range(1, 9))

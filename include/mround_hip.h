@@ -371,6 +371,17 @@ int mr_rope(void* x_bf16, int64_t ld, int64_t T, int S, int n_heads, int head_di
             const float* cos_sin, int backward, void* stream);
 
 /*
+ * Split precision for the attention (the reference's three-product remedy,
+ * DOCUMENTATION.md:885-925, carried through the scaled-dot-product attention
+ * of mround/pipeline/blocks.py:605): fp32 q/k/v rows x [T, ldx] (the split
+ * q/k/v product's output), the first n_rope_heads of the n_heads heads
+ * rotated in fp32 as mr_rope does and the rest passed through, written as
+ * bf16 hi = bf16(y) and lo = bf16(y - hi) rows (leading dimension ld).
+ */
+int mr_rope_split(const float* x, int64_t ldx, int64_t T, int S, int n_rope_heads, int n_heads, int head_dim,
+                  const float* cos_sin, void* hi, void* lo, int64_t ld, void* stream);
+
+/*
  * Causal grouped-query attention on the packed bf16 qkv rows [B*S, ld]
  * (q heads, then k heads, then v heads; query head h uses kv head
  * h / (Hq / Hkv)), head_dim 64 or 128, S a multiple of 128. The forward
@@ -389,6 +400,18 @@ int mr_rope(void* x_bf16, int64_t ld, int64_t T, int S, int n_heads, int head_di
  */
 int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int head_dim,
                 float scale, void* out, int64_t ldo, float* lse, void* stream);
+/*
+ * mr_attn_fwd in split precision: q, k and v as the hi and lo halves of
+ * mr_rope_split (same layout, leading dimension ld), the scores and the
+ * probability-value product each as three bf16 products (hi hi, lo hi,
+ * hi lo). Writes the output's hi half into out (what the backward reads) and
+ * the output split into out_split rows of 3 Hq head_dim values,
+ * [hi | hi | lo] (the activation operand of a split product over
+ * K' = 3 Hq head_dim), and the log-sum-exp.
+ */
+int mr_attn_fwd_split(const void* qkv_hi, const void* qkv_lo, int64_t ld, int B, int S, int Hq, int Hkv,
+                      int head_dim, float scale, void* out, int64_t ldo, void* out_split, int64_t ld_split,
+                      float* lse, void* stream);
 size_t mr_attn_bwd_workspace_bytes(int B, int S, int Hq, int Hkv, int head_dim, int hsplit);
 int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, int64_t ldo,
                 const float* lse, float* dsum_ws, int B, int S, int Hq, int Hkv, int head_dim,

@@ -20,6 +20,7 @@ import dataclasses
 import json
 import math
 import time
+import warnings
 from collections.abc import Mapping, Sequence
 from pathlib import Path
 from typing import Any
@@ -423,6 +424,40 @@ def _run_shape(config, resolved: QuantScheme, tuning: TuningConfig, *, average_b
     return shape, run
 
 
+# Code widths whose block objective one bf16 product cannot resolve: the
+# bf16 rounding of the block's activations is as large as the quantization
+# error itself (the objective reads about a third high against float64), so
+# split precision is on for them unless the caller says otherwise.
+SPLIT_PRECISION_WIDTHS = frozenset({8})
+
+
+def _split_choice(split_precision: bool | None, tuned_widths) -> tuple[bool, str]:
+    """Whether the block forward runs in split precision, and why: the
+    caller's choice, else on when a tuned width is one of
+    ``SPLIT_PRECISION_WIDTHS``. A caller turning it off for such a width is
+    warned that the objective will be imprecise."""
+    wide = sorted(set(int(w) for w in tuned_widths) & SPLIT_PRECISION_WIDTHS)
+    if split_precision is None:
+        if wide:
+            return True, f"automatic: tuned width {wide[0]} needs the split-precision objective"
+        return False, "automatic: no tuned width needs the split-precision objective"
+    if not split_precision and wide:
+        warnings.warn(f"split_precision=False with {wide[0]}-bit codes: the block objective runs on single "
+                      "bf16 products, whose rounding is as large as the quantization error at this width "
+                      "(the loss reads about a third high against float64)", stacklevel=3)
+    return bool(split_precision), "requested"
+
+
+def _tuned_widths(resolved: QuantScheme, average_bits, candidate_bits, plan) -> tuple[int, ...]:
+    """The code widths the block tunes may run at: the scheme's, the plan's,
+    or (a mixed run still to be planned) every candidate."""
+    if average_bits is None:
+        return (resolved.bits,)
+    if plan is not None:
+        return tuple(sorted(set(int(v) for v in plan.values())))
+    return tuple(candidate_bits)
+
+
 def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
                    symmetry: Symmetry = Symmetry.SYMMETRIC, average_bits: float | None = None,
                    candidate_bits: Sequence[int] = (2, 3, 4), sensitivity_gradients: str = "auto",
@@ -432,14 +467,17 @@ def predict_memory(model: str | Path, *, bits: int = 4, group_size: int = 64,
                    tuning: TuningConfig | None = None, scale_init: ScaleInit | str | None = None,
                    quantized_inputs: bool = True, holdout_batches: int = 0,
                    memory_budget: int | None = None, device: str = "cuda",
-                   split_precision: bool = False) -> M.MemoryCheck:
+                   split_precision: bool | None = None) -> M.MemoryCheck:
     """Predict the device memory of the run :func:`quantize` would make, and
     stop (mround/api.py:1088-1192). Reads ``config.json`` and nothing else.
-    ``memory_budget`` defaults to 90 % of the device's memory."""
+    ``memory_budget`` defaults to 90 % of the device's memory;
+    ``split_precision`` follows :func:`quantize`'s rule."""
     config = _read_config(model)
     resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry,
                                        average_bits=average_bits, candidate_bits=candidate_bits,
                                        remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
+    if split_precision is None:
+        split_precision = _split_choice(None, _tuned_widths(resolved, average_bits, candidate_bits, None))[0]
     tuning = tuning or TuningConfig()
     _check_calibration_sizes(tuning)
     shape, run = _run_shape(config, resolved, tuning, average_bits=average_bits, plan=None,
@@ -458,14 +496,18 @@ def predict_time(model: str | Path, *, bits: int = 4, group_size: int = 64,
                  remainder_bits: int | None = None, scoring_samples: int | None = None,
                  scoring_seq_len: int | None = None, scheme: QuantScheme | None = None,
                  tuning: TuningConfig | None = None, scale_init: ScaleInit | str | None = None,
-                 per_layer_recipe: bool = False, holdout_batches: int = 0, split_precision: bool = False):
+                 per_layer_recipe: bool = False, holdout_batches: int = 0,
+                 split_precision: bool | None = None):
     """Predict the seconds the run :func:`quantize` would make takes on one
     MI355X (``mround_amd.planner.timing``), from ``config.json`` alone
-    (mround/cli/main.py:590-624)."""
+    (mround/cli/main.py:590-624); ``split_precision`` follows
+    :func:`quantize`'s rule."""
     config = _read_config(model)
     resolved, widths = _resolve_scheme(bits=bits, group_size=group_size, symmetry=symmetry,
                                        average_bits=average_bits, candidate_bits=candidate_bits,
                                        remainder_bits=remainder_bits, scheme=scheme, scale_init=scale_init)
+    if split_precision is None:
+        split_precision = _split_choice(None, _tuned_widths(resolved, average_bits, candidate_bits, None))[0]
     tuning = tuning or TuningConfig()
     _check_calibration_sizes(tuning)
     shape, run = _run_shape(config, resolved, tuning, average_bits=average_bits, plan=None,
@@ -514,7 +556,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
              per_layer_recipe: bool = False, plan: Mapping[str, int] | None = None,
              scale_init: ScaleInit | str | None = None, seed: int | None = None,
              memory_budget: int | None = None, memory_check: bool = True,
-             min_block_coverage: float = MIN_BLOCK_COVERAGE, split_precision: bool = False,
+             min_block_coverage: float = MIN_BLOCK_COVERAGE, split_precision: bool | None = None,
              device: str = "cuda", progress=None, scoring_progress=None) -> QuantizeResult:
     """Quantize the local checkpoint ``model`` into ``output_dir``.
 
@@ -532,13 +574,18 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     ``min_block_coverage`` of the block stack's linears is refused with
     ``UnsupportedSchemeError`` (``block_coverage``); the layers it cannot
     reach are left dense and reported in ``skipped``. ``split_precision``
-    runs the block forward's products as three bf16 products of hi and lo
-    halves (the reference's documented remedy for the block objective's
-    precision, mround DOCUMENTATION.md:885-925): about 16 significant bits
-    in place of 8 for 1.6-1.8x the block tune time, for wide codes (8 bits),
-    whose residual bf16 products swamp. Raises the reference's exceptions for
-    unrepresentable schemes, bad calibration, unusable plans and unsupported
-    architectures.
+    runs the block forward as three bf16 products of hi and lo halves per
+    product, the attention's included (the reference's documented remedy for
+    the block objective's precision, mround DOCUMENTATION.md:885-925): about
+    16 significant bits in place of 8 for about 1.9x the block tune time.
+    ``None`` (the default) turns it on when a tuned width is 8 bits, whose
+    quantization error single bf16 products cannot resolve, in uniform and
+    mixed runs alike (a mixed run still to be planned counts it on for the
+    memory and time predictions when 8 is a candidate, and runs it when the
+    plan tunes a layer at 8); ``False`` with 8-bit codes warns. The choice
+    and its reason are recorded in the run record. Raises the reference's
+    exceptions for unrepresentable schemes, bad calibration, unusable plans
+    and unsupported architectures.
     """
     started = time.perf_counter()
     if export_format != "mlx":
@@ -554,6 +601,9 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
     tuning = tuning or TuningConfig()
     _check_calibration_sizes(tuning)
     seed = 0 if seed is None else int(seed)
+    requested_split = split_precision
+    split_precision, split_reason = _split_choice(
+        split_precision, _tuned_widths(resolved, average_bits, candidate_bits, plan))
     mshape, rshape = _run_shape(_read_config(model), resolved, tuning, average_bits=average_bits, plan=plan,
                                 widths=candidate_bits if average_bits is not None else (resolved.bits,),
                                 gradient_source=sensitivity_gradients, scoring_samples=scoring_samples,
@@ -604,6 +654,9 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
                 scoring_batch=scoring_batch_size, seed=seed, device=device, progress=scoring_progress)
         remainder_scheme = resolved.with_bits(int(mixed["remainder_bits"]))
         plan_s = time.perf_counter() - tp
+        if requested_split is None:  # the plan decides which widths are tuned
+            split_precision, split_reason = _split_choice(
+                None, {sch.bits for sch in schemes_by_layer.values()} or {resolved.bits})
     runner = QuantizationRunner(resolved, tuning, progress=progress, quantized_inputs=quantized_inputs,
                                 holdout_batches=holdout_batches, per_layer_recipe=per_layer_recipe,
                                 split_precision=split_precision)
@@ -637,6 +690,7 @@ def quantize(model: str | Path, *, output_dir: str | Path, bits: int = 4, group_
         "quantized_inputs": quantized_inputs,
         "holdout_batches": holdout_batches,
         "split_precision": bool(split_precision),
+        "split_precision_reason": split_reason,
         "blocks": [{"index": b.index, "name": b.name, "initial_loss": b.initial_loss,
                     "final_loss": b.final_loss, "reverted": b.reverted, "seconds": b.seconds,
                     "search_seconds": b.search_seconds} for b in summary.blocks],

@@ -54,9 +54,10 @@ def _parser() -> argparse.ArgumentParser:
                    help="run each step's batch in this many pieces, summing their gradients (default: 1)")
     q.add_argument("--allow-dense", action="store_true",
                    help="proceed even when the group size reaches under half of the block stack's layers")
-    q.add_argument("--split-precision", action="store_true",
-                   help="run the block forward's products as three bf16 products of hi and lo halves "
-                        "(about 16-bit operands, 1.6-1.8x the tune time; for 8-bit codes)")
+    q.add_argument("--split-precision", action=argparse.BooleanOptionalAction, default=None,
+                   help="run the block forward as three bf16 products of hi and lo halves per product "
+                        "(about 16-bit operands, about 1.9x the tune time; default: on when a tuned width "
+                        "is 8 bits)")
     q.add_argument("--memory-budget", type=float, default=None,
                    help="GB the run may use on the device (default: 90 %% of its memory)")
     q.add_argument("--skip-memory-check", action="store_true",

@@ -128,6 +128,16 @@ __device__ __forceinline__ bf16x8 cvt8(const f32x16& x, int off) {
   return __builtin_convertvector(v, bf16x8);
 }
 
+// The low bf16 half of 8 accumulator values: bf16(x - bf16(x)), exact in the
+// subtraction (split precision carries x as the two halves).
+__device__ __forceinline__ bf16x8 cvt8_lo(const f32x16& x, int off) {
+  f32x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = x[off + j];
+  const f32x8 hi = __builtin_convertvector(__builtin_convertvector(v, bf16x8), f32x8);
+  return __builtin_convertvector(v - hi, bf16x8);
+}
+
 // Accumulator register r of a 32x32 tile, lane half h: row within the tile.
 __device__ __forceinline__ int acc_row(int r, int h) { return (r >> 2) * 8 + h * 4 + (r & 3); }
 
@@ -135,17 +145,18 @@ __device__ __forceinline__ int acc_row(int r, int h) { return (r >> 2) * 8 + h *
 // acc_row(r, h), query = lane & 31), times `mul`, as bf16 rows [32 queries][D]
 // through LDS: packed 8-byte writes into rows padded to 2 D + 8 bytes (no
 // bank conflicts), then 16-byte row-contiguous global stores.
-template <int D>
-__device__ __forceinline__ void store_qrows(const f32x16 (&acc)[D / 32], float mul, uint8_t* lds,
-                                           uint16_t* dst, int64_t ld, int64_t row0) {
+// (store_qrows_f: the value written is bf16(f(acc)) instead.)
+template <int D, typename F>
+__device__ __forceinline__ void store_qrows_f(const f32x16 (&acc)[D / 32], F f, uint8_t* lds,
+                                             uint16_t* dst, int64_t ld, int64_t row0) {
   constexpr int STAGE_ROW = 2 * D + 8;
   const int lane = threadIdx.x & 63, h = lane >> 5, q = lane & 31;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
-      const uint32_t w0 = pack_bf16(acc[dt][rg * 4 + 0] * mul, acc[dt][rg * 4 + 1] * mul);
-      const uint32_t w1 = pack_bf16(acc[dt][rg * 4 + 2] * mul, acc[dt][rg * 4 + 3] * mul);
+      const uint32_t w0 = pack_bf16(f(acc[dt][rg * 4 + 0]), f(acc[dt][rg * 4 + 1]));
+      const uint32_t w1 = pack_bf16(f(acc[dt][rg * 4 + 2]), f(acc[dt][rg * 4 + 3]));
       const int col = dt * 32 + rg * 8 + h * 4;
       *reinterpret_cast<uint2*>(lds + q * STAGE_ROW + col * 2) = make_uint2(w0, w1);
     }
@@ -158,6 +169,11 @@ __device__ __forceinline__ void store_qrows(const f32x16 (&acc)[D / 32], float m
     const uint2 b = *reinterpret_cast<const uint2*>(lds + row * STAGE_ROW + ch * 16 + 8);
     *reinterpret_cast<uint4*>(dst + (row0 + row) * ld + ch * 8) = make_uint4(a.x, a.y, b.x, b.y);
   }
+}
+template <int D>
+__device__ __forceinline__ void store_qrows(const f32x16 (&acc)[D / 32], float mul, uint8_t* lds,
+                                           uint16_t* dst, int64_t ld, int64_t row0) {
+  store_qrows_f<D>(acc, [mul](float x) { return x * mul; }, lds, dst, ld, row0);
 }
 
 // ---- forward ----------------------------------------------------------------
@@ -189,20 +205,31 @@ __device__ __forceinline__ float xhalf_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int D, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void attn_fwd(const uint16_t* __restrict__ qkv, int64_t ld,
-                                                   int S, int Hq, int Hkv, float scale_log2,
-                                                   uint16_t* __restrict__ out, int64_t ldo,
-                                                   float* __restrict__ lse) {
+// SPLIT: split precision (q, k and v each carried as bf16 hi and lo halves,
+// from qkv and qkv_lo): S^T = K_hi Q_hi^T + K_lo Q_hi^T + K_hi Q_lo^T and
+// O^T += V_hi^T P_hi^T + V_lo^T P_hi^T + V_hi^T P_lo^T with P = P_hi + P_lo,
+// the low-by-low terms left out, so the scores, probabilities and output hold
+// about 16 significant bits. The output is written split as well, row t of
+// out_split holding [hi | hi | lo] of the Hq D outputs (the activation order
+// of a split product over K' = 3 Hq D), and its hi half into out. Twice the
+// LDS and three times the MFMAs; one wave per SIMD (W = 4), whose register
+// file holds the extra fragments.
+template <int D, int W, bool SPLIT = false>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SPLIT ? 1 : 2))) void attn_fwd(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qkv_lo, int64_t ld, int S, int Hq, int Hkv,
+    float scale_log2, uint16_t* __restrict__ out, int64_t ldo, uint16_t* __restrict__ out_split,
+    int64_t ld_split, float* __restrict__ lse) {
   constexpr int NS = D / 16, ND = D / 32;
   constexpr int TILE = KT * D * 2;
+  constexpr int NT = SPLIT ? 8 : 4;     // LDS tiles: K, V of two stages (and their lo halves)
   constexpr int STAGE_ROW = 2 * D + 8;  // staged output row (bytes), 8-byte aligned
-  constexpr int SMEM = 4 * TILE > W * 32 * STAGE_ROW ? 4 * TILE : W * 32 * STAGE_ROW;
+  constexpr int SMEM = NT * TILE > W * 32 * STAGE_ROW ? NT * TILE : W * 32 * STAGE_ROW;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
   uint8_t* const K0 = smem;
   uint8_t* const V0 = smem + TILE;
   uint8_t* const K1 = smem + 2 * TILE;
   uint8_t* const V1 = smem + 3 * TILE;
+  constexpr int LO = 4 * TILE;  // a stage tile's lo half sits this far behind it
   const int qb = gridDim.z - 1 - blockIdx.z;  // the longest blocks start first
   const int hq = blockIdx.x, b = blockIdx.y;
   const int g = hq / (Hq / Hkv);
@@ -213,13 +240,23 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   const int kcol = (Hq + g) * D, vcol = (Hq + Hkv + g) * D;
   const int n_tiles = (qb + 1) * (32 * W) / KT;
 
-  dma_rowtile<D, W>(qkv, ld, tok0, kcol, K0);
-  dma_rowtile<D, W>(qkv, ld, tok0, vcol, V0);
+  auto load_tiles = [&](int64_t r0, uint8_t* Kd, uint8_t* Vd) {
+    dma_rowtile<D, W>(qkv, ld, r0, kcol, Kd);
+    dma_rowtile<D, W>(qkv, ld, r0, vcol, Vd);
+    if constexpr (SPLIT) {
+      dma_rowtile<D, W>(qkv_lo, ld, r0, kcol, Kd + LO);
+      dma_rowtile<D, W>(qkv_lo, ld, r0, vcol, Vd + LO);
+    }
+  };
+  load_tiles(tok0, K0, V0);
 
-  bf16x8 qf[NS];
+  bf16x8 qf[NS], ql[SPLIT ? NS : 1];
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
+  for (int s = 0; s < NS; ++s) {
     qf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + qi) * ld + hq * D + s * 16 + h * 8);
+    if constexpr (SPLIT)
+      ql[s] = *reinterpret_cast<const bf16x8*>(qkv_lo + (tok0 + qi) * ld + hq * D + s * 16 + h * 8);
+  }
   f32x16 o[ND];
 #pragma unroll
   for (int dt = 0; dt < ND; ++dt) o[dt] = f32x16{};
@@ -228,10 +265,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   auto step = [&](int t, const uint8_t* Kc, const uint8_t* Vc, uint8_t* Kn, uint8_t* Vn) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile t have landed
     __syncthreads();                // everyone's have, and nobody still reads the other buffers
-    if (t + 1 < n_tiles) {
-      dma_rowtile<D, W>(qkv, ld, tok0 + (t + 1) * KT, kcol, Kn);
-      dma_rowtile<D, W>(qkv, ld, tok0 + (t + 1) * KT, vcol, Vn);
-    }
+    if (t + 1 < n_tiles) load_tiles(tok0 + (t + 1) * KT, Kn, Vn);
     const int kv0 = t * KT;
     if (kv0 > q0 + 31) return;  // every key of the tile is after every query of the wave
 
@@ -246,8 +280,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
         kfr[(s + 1) & 1][1] = frag_row<D>(Kc, 32 + l32, s + 1, h);
       }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt) {
         st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[s & 1][mt], qf[s], st[mt], 0, 0, 0);
+        if constexpr (SPLIT) {
+          st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_row<D>(Kc + LO, mt * 32 + l32, s, h), qf[s],
+                                                           st[mt], 0, 0, 0);
+          st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[s & 1][mt], ql[s], st[mt], 0, 0, 0);
+        }
+      }
     }
     if (kv0 + KT - 1 > q0) {  // the tile crosses the wave's diagonal
 #pragma unroll
@@ -284,9 +324,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     for (int s = 0; s < KT / 16; ++s) {
       const bf16x8 pb = cvt8(st[s >> 1], 8 * (s & 1));
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(Vc, dt * 32, s, lane), pb, o[dt],
-                                                        0, 0, 0);
+      for (int dt = 0; dt < ND; ++dt) {
+        const bf16x8 vt = frag_tr<D>(Vc, dt * 32, s, lane);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt, pb, o[dt], 0, 0, 0);
+        if constexpr (SPLIT) {
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(Vc + LO, dt * 32, s, lane), pb, o[dt],
+                                                          0, 0, 0);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt, cvt8_lo(st[s >> 1], 8 * (s & 1)), o[dt], 0, 0, 0);
+        }
+      }
     }
   };
 
@@ -299,7 +345,20 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
   __syncthreads();  // all tiles read; the buffers now stage the output
 
   if (h == 0) lse[(static_cast<int64_t>(b) * Hq + hq) * S + qi] = (m + log2f(l)) * kLn2;
-  store_qrows<D>(o, 1.0f / l, smem + wave * 32 * STAGE_ROW, out + hq * D, ldo, tok0 + q0);
+  uint8_t* const stage = smem + wave * 32 * STAGE_ROW;
+  const float inv_l = 1.0f / l;
+  store_qrows<D>(o, inv_l, stage, out + hq * D, ldo, tok0 + q0);
+  if constexpr (SPLIT) {
+    const auto hi = [inv_l](float x) { return x * inv_l; };
+    const auto lo = [inv_l](float x) {
+      const float y = x * inv_l;
+      return y - bf16_to_f32(f32_to_bf16(y));
+    };
+    const int64_t seg = static_cast<int64_t>(Hq) * D;
+    store_qrows_f<D>(o, hi, stage, out_split + hq * D, ld_split, tok0 + q0);
+    store_qrows_f<D>(o, hi, stage, out_split + seg + hq * D, ld_split, tok0 + q0);
+    store_qrows_f<D>(o, lo, stage, out_split + 2 * seg + hq * D, ld_split, tok0 + q0);
+  }
 }
 
 // ---- backward ---------------------------------------------------------------
@@ -935,12 +994,22 @@ template <int D>
 int launch_fwd(const uint16_t* qkv, int64_t ld, int B, int S, int Hq, int Hkv, float scale,
                uint16_t* out, int64_t ldo, float* lse, hipStream_t s) {
   if (S % 256 == 0)
-    hipLaunchKernelGGL((attn_fwd<D, 8>), dim3(Hq, B, S / 256), dim3(512), 0, s, qkv, ld, S, Hq, Hkv,
-                       scale * kLog2e, out, ldo, lse);
+    hipLaunchKernelGGL((attn_fwd<D, 8>), dim3(Hq, B, S / 256), dim3(512), 0, s, qkv, nullptr, ld, S, Hq, Hkv,
+                       scale * kLog2e, out, ldo, nullptr, 0, lse);
   else
-    hipLaunchKernelGGL((attn_fwd<D, 4>), dim3(Hq, B, S / 128), dim3(256), 0, s, qkv, ld, S, Hq, Hkv,
-                       scale * kLog2e, out, ldo, lse);
+    hipLaunchKernelGGL((attn_fwd<D, 4>), dim3(Hq, B, S / 128), dim3(256), 0, s, qkv, nullptr, ld, S, Hq, Hkv,
+                       scale * kLog2e, out, ldo, nullptr, 0, lse);
   MR_LAUNCH_CHECK("mr_attn_fwd");
+  return MR_OK;
+}
+
+template <int D>
+int launch_fwd_split(const uint16_t* qkv, const uint16_t* qkv_lo, int64_t ld, int B, int S, int Hq, int Hkv,
+                     float scale, uint16_t* out, int64_t ldo, uint16_t* out_split, int64_t ld_split, float* lse,
+                     hipStream_t s) {
+  hipLaunchKernelGGL((attn_fwd<D, 4, true>), dim3(Hq, B, S / 128), dim3(256), 0, s, qkv, qkv_lo, ld, S, Hq, Hkv,
+                     scale * kLog2e, out, ldo, out_split, ld_split, lse);
+  MR_LAUNCH_CHECK("mr_attn_fwd_split");
   return MR_OK;
 }
 
@@ -1027,6 +1096,27 @@ int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int 
   uint16_t* o = static_cast<uint16_t*>(out);
   if (head_dim == 128) return launch_fwd<128>(q, ld, B, S, Hq, Hkv, scale, o, ldo, lse, s);
   return launch_fwd<64>(q, ld, B, S, Hq, Hkv, scale, o, ldo, lse, s);
+}
+
+int mr_attn_fwd_split(const void* qkv_hi, const void* qkv_lo, int64_t ld, int B, int S, int Hq, int Hkv,
+                      int head_dim, float scale, void* out, int64_t ldo, void* out_split, int64_t ld_split,
+                      float* lse, void* stream) {
+  using namespace mr;
+  clear_error();
+  int rc = check("mr_attn_fwd_split", qkv_hi, ld, B, S, Hq, Hkv, head_dim, ldo);
+  if (rc) return rc;
+  if (!qkv_lo || !aligned16(qkv_lo)) return fail(MR_EINVAL, "mr_attn_fwd_split: qkv_lo must be 16-byte aligned");
+  if (!out || !lse || !out_split || !aligned16(out) || !aligned16(out_split))
+    return fail(MR_EINVAL, "mr_attn_fwd_split: bad output");
+  if (ld_split < 3ll * Hq * head_dim || ld_split % 8)
+    return fail(MR_EINVAL, "mr_attn_fwd_split: out_split rows must hold 3 Hq head_dim values (ld a multiple of 8)");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* qh = static_cast<const uint16_t*>(qkv_hi);
+  const uint16_t* ql = static_cast<const uint16_t*>(qkv_lo);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  uint16_t* os = static_cast<uint16_t*>(out_split);
+  if (head_dim == 128) return launch_fwd_split<128>(qh, ql, ld, B, S, Hq, Hkv, scale, o, ldo, os, ld_split, lse, s);
+  return launch_fwd_split<64>(qh, ql, ld, B, S, Hq, Hkv, scale, o, ldo, os, ld_split, lse, s);
 }
 
 size_t mr_attn_bwd_workspace_bytes(int B, int S, int Hq, int Hkv, int head_dim, int hsplit) {

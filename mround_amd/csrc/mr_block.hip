@@ -377,6 +377,40 @@ __global__ __launch_bounds__(kBlock) void swiglu_split_rows(const float* __restr
   }
 }
 
+// Split precision for the attention: fp32 q/k/v rows (the split q/k/v
+// product's output) rotated in fp32 (the rotary embedding over the first
+// n_rope heads, q then k, as rope_kernel; the v heads pass through) and
+// written as bf16 hi and lo halves. One block per token row; thread i takes
+// pair i of each head (columns i and i + d/2).
+__global__ __launch_bounds__(kBlock) void rope_split_rows(const float* __restrict__ x, int64_t ldx, int S,
+                                                          int n_rope, int n_heads, int d,
+                                                          const float* __restrict__ cs, uint16_t* __restrict__ hi,
+                                                          uint16_t* __restrict__ lo, int64_t ld) {
+  const int64_t t = blockIdx.x;
+  const int half = d / 2;
+  const int pos = static_cast<int>(t % S);
+  const float* xr = x + t * ldx;
+  uint16_t* hr = hi + t * ld;
+  uint16_t* lr = lo + t * ld;
+  for (int p = threadIdx.x; p < n_heads * half; p += kBlock) {
+    const int hd = p / half, i = p % half;
+    const int64_t ca = static_cast<int64_t>(hd) * d + i, cb = ca + half;
+    float ya = xr[ca], yb = xr[cb];
+    if (hd < n_rope) {
+      const float c = cs[(static_cast<int64_t>(pos) * half + i) * 2];
+      const float sn = cs[(static_cast<int64_t>(pos) * half + i) * 2 + 1];
+      const float a = ya, b = yb;
+      ya = a * c - b * sn;
+      yb = b * c + a * sn;
+    }
+    const uint16_t ha = f32_to_bf16(ya), hb = f32_to_bf16(yb);
+    hr[ca] = ha;
+    hr[cb] = hb;
+    lr[ca] = f32_to_bf16(ya - bf16_to_f32(ha));
+    lr[cb] = f32_to_bf16(yb - bf16_to_f32(hb));
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
@@ -535,6 +569,23 @@ int mr_rmsnorm_bwd(const float* dy, const float* h, const float* w, const float*
   hipLaunchKernelGGL(rmsnorm_bwd, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0, s, dy, h, w,
                      rstd, dres, H, db, dh_f32);
   MR_LAUNCH_CHECK("mr_rmsnorm_bwd");
+  return MR_OK;
+}
+
+int mr_rope_split(const float* x, int64_t ldx, int64_t T, int S, int n_rope_heads, int n_heads, int head_dim,
+                  const float* cos_sin, void* hi, void* lo, int64_t ld, void* stream) {
+  using namespace mr;
+  clear_error();
+  if (T <= 0 || n_heads <= 0) return MR_OK;
+  if (!x || !cos_sin || !hi || !lo) return fail(MR_EINVAL, "mr_rope_split: null pointer");
+  if (head_dim <= 0 || head_dim % 2 || S <= 0 || n_rope_heads < 0 || n_rope_heads > n_heads ||
+      ldx < static_cast<int64_t>(n_heads) * head_dim || ld < static_cast<int64_t>(n_heads) * head_dim)
+    return fail(MR_EINVAL, "mr_rope_split: bad shape");
+  if (T > 0x7fffffff) return fail(MR_EINVAL, "mr_rope_split: too many rows");
+  hipLaunchKernelGGL(rope_split_rows, dim3(static_cast<unsigned>(T)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), x, ldx, S, n_rope_heads, n_heads, head_dim, cos_sin,
+                     static_cast<uint16_t*>(hi), static_cast<uint16_t*>(lo), ld);
+  MR_LAUNCH_CHECK("mr_rope_split");
   return MR_OK;
 }
 

@@ -88,6 +88,8 @@ _SIGNATURES = {
     "mr_swiglu_split": (_I, [_P, _L, _L, _P, _P, _P, _P]),
     "mr_rope": (_I, [_P, _L, _L, _I, _I, _I, _P, _I, _P]),
     "mr_attn_fwd": (_I, [_P, _L, _I, _I, _I, _I, _I, _F, _P, _L, _P, _P]),
+    "mr_attn_fwd_split": (_I, [_P, _P, _L, _I, _I, _I, _I, _I, _F, _P, _L, _P, _L, _P, _P]),
+    "mr_rope_split": (_I, [_P, _L, _L, _I, _I, _I, _I, _P, _P, _P, _L, _P]),
     "mr_attn_bwd_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I, _I, _I, _I]),
     "mr_attn_bwd": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _I, _I, _I, _I, _F, _P, _I, _P, ctypes.c_size_t,
                          _P]),
@@ -514,6 +516,32 @@ def attn_fwd(qkv, *, batch, seq_len, n_heads, n_kv_heads, head_dim, scale, out, 
     rc = lib().mr_attn_fwd(_ptr(qkv), qkv.stride(0), batch, seq_len, n_heads, n_kv_heads, head_dim,
                            scale, _ptr(out), out.stride(0), _ptr(_f32(lse, "lse")), _stream(qkv))
     _check(rc, "mr_attn_fwd")
+
+
+def attn_fwd_split(qkv_hi, qkv_lo, *, batch, seq_len, n_heads, n_kv_heads, head_dim, scale, out, out_split,
+                   lse) -> None:
+    """``mr_attn_fwd_split``: the attention with q/k/v, probabilities and
+    output carried as bf16 hi/lo halves; ``out`` gets the output's hi half,
+    ``out_split`` [T, 3 Hq d] its [hi | hi | lo] rows."""
+    if qkv_lo.stride(0) != qkv_hi.stride(0) or qkv_lo.shape != qkv_hi.shape:
+        raise KernelError("attn_fwd_split: qkv_hi and qkv_lo must share a layout")
+    if out_split.shape[0] != out.shape[0] or out_split.shape[1] < 3 * n_heads * head_dim:
+        raise KernelError(f"attn_fwd_split: out_split must be [{out.shape[0]}, {3 * n_heads * head_dim}]")
+    rc = lib().mr_attn_fwd_split(_ptr(qkv_hi), _ptr(qkv_lo), qkv_hi.stride(0), batch, seq_len, n_heads, n_kv_heads,
+                                 head_dim, scale, _ptr(out), out.stride(0), _ptr(out_split), out_split.stride(0),
+                                 _ptr(_f32(lse, "lse")), _stream(qkv_hi))
+    _check(rc, "mr_attn_fwd_split")
+
+
+def rope_split(x, hi, lo, *, seq_len, n_rope_heads, head_dim, cos_sin) -> None:
+    """``mr_rope_split``: fp32 q/k/v rows ``x`` rotated (the first
+    ``n_rope_heads`` heads) and written as bf16 ``hi`` and ``lo`` halves."""
+    T, cols = x.shape
+    if hi.shape != (T, cols) or lo.shape != (T, cols) or hi.stride(0) != lo.stride(0):
+        raise KernelError(f"rope_split: hi and lo must be [{T}, {cols}] with one layout")
+    rc = lib().mr_rope_split(_ptr(_f32(x, "x")), x.stride(0), T, seq_len, n_rope_heads, cols // head_dim, head_dim,
+                             _ptr(_f32(cos_sin, "cos_sin")), _ptr(hi), _ptr(lo), hi.stride(0), _stream(x))
+    _check(rc, "mr_rope_split")
 
 
 def attn_bwd_workspace_bytes(*, batch, seq_len, n_heads, n_kv_heads, head_dim, hsplit=0) -> int:

@@ -183,10 +183,11 @@ def gemm_problems(shape: BlockShape, tokens: int) -> list[tuple[int, int, int]]:
 
 def split_gemm_problems(shape: BlockShape, tokens: int) -> list[tuple[int, int, int]]:
     """(M, N, K) of the forward products that split precision runs over K' = 3K
-    (the q/k/v projection, the gate/up pair and down; the attention output
-    projection runs as two products of its own K)."""
+    (the q/k/v projection, the attention output projection, the gate/up pair
+    and down)."""
     T, h, mlp, q = tokens, shape.hidden, shape.intermediate, shape.qkv_rows
-    return [(T, q, 3 * h), (T, 2 * mlp, 3 * h), (T, h, 3 * mlp)]
+    hq_d = shape.n_heads * shape.head_dim
+    return [(T, q, 3 * h), (T, h, 3 * hq_d), (T, 2 * mlp, 3 * h), (T, h, 3 * mlp)]
 
 
 def workspace_bytes(shape: BlockShape, batch: int, seq_len: int,
@@ -257,14 +258,14 @@ class BlockEngine:
     token rows only, so the loss and every gradient are those of the
     ``real_len``-token sequences.
 
-    ``split`` runs the forward's products in split precision (the reference's
+    ``split`` runs the forward in split precision (the reference's
     three-product remedy for the block objective, mround DOCUMENTATION.md:
-    885-925): the normalized inputs, the SwiGLU output and every W' are
-    carried as bf16 hi and lo halves, and each product is one bf16 GEMM over
-    K' = 3K of [A_hi | A_hi | A_lo] and [B_hi | B_lo | B_hi] (the attention
-    output projection as A (B_hi + B_lo), two products). The attention itself,
-    the stored q/k/v and the backward stay in bf16. Weights are written
-    through ``w32`` (fp32) and ``split_weights``."""
+    885-925): the normalized inputs, q/k/v (rotated in fp32), the attention's
+    probabilities and output, the SwiGLU output and every W' are carried as
+    bf16 hi and lo halves, and each product is three bf16 products (one GEMM
+    over K' = 3K of [A_hi | A_hi | A_lo] and [B_hi | B_lo | B_hi]; inside the
+    attention, hi hi + lo hi + hi lo). The backward stays in bf16 on the hi
+    halves. Weights are written through ``w32`` (fp32) and ``split_weights``."""
 
     def __init__(self, shape: BlockShape, *, batch: int, seq_len: int, device,
                  extra_gemms: tuple[tuple[int, int, int], ...] = (), real_len: int | None = None,
@@ -304,12 +305,14 @@ class BlockEngine:
         self.threshold = e(1, dt=f32)
         # split precision: fp32 W' and the split operands
         self.w32 = self.wqs = None
-        self.x1s = self.x2s = self.acts = self.gu32 = None
+        self.x1s = self.x2s = self.acts = self.gu32 = self.qkv32 = self.qkv_lo = self.attns = None
         if self.split:
             self.w32 = {k: torch.empty(v.shape, dtype=f32, device=self.device) for k, v in self.wq.items()}
             self.wqs = {k: e(v.shape[0], 3 * v.shape[1]) for k, v in self.wq.items()}
             self.x1s, self.x2s = e(T, 3 * h), e(T, 3 * h)
             self.acts, self.gu32 = e(T, 3 * mlp), e(T, 2 * mlp, dt=f32)
+            self.qkv32, self.qkv_lo = e(T, shape.qkv_rows, dt=f32), e(T, shape.qkv_rows)
+            self.attns = e(T, 3 * hq_d)
         self.cos_sin = rope_table(seq_len, shape.head_dim, shape.rope_theta, self.device, shape.rope_scaling)
         self.scale = 1.0 / math.sqrt(shape.head_dim)
         self.place = placements(shape)
@@ -334,7 +337,7 @@ class BlockEngine:
     PER_TOKEN = ("x1", "rstd1", "qkv", "attn", "h2", "x2", "rstd2", "act", "gu", "grad_out",
                  "grad_out16", "dgu", "dx2", "dh2", "dattn", "dqkv")
     PER_SEQUENCE = ("lse", "dsum")
-    SPLIT_PER_TOKEN = ("x1s", "x2s", "acts", "gu32")
+    SPLIT_PER_TOKEN = ("x1s", "x2s", "acts", "gu32", "qkv32", "qkv_lo", "attns")
 
     def set_sequences(self, n: int) -> None:
         """Run the next passes over ``n`` sequences (at most the capacity the
@@ -472,20 +475,17 @@ class BlockEngine:
         h, hq_d, mlp = s.hidden, s.n_heads * s.head_dim, s.intermediate
         ws = self.gemm_ws
         K.rmsnorm_fwd_split(x, self.norm_in, s.norm_eps, self.x1s, self.x1, self.rstd1)
-        self._run("gemm_qkv", lambda: K.gemm("nt", self.x1s, self.wqs["qkv"], self.qkv, M=T, N=s.qkv_rows,
+        self._run("gemm_qkv", lambda: K.gemm("nt", self.x1s, self.wqs["qkv"], self.qkv32, M=T, N=s.qkv_rows,
                                              K=3 * h, bias=self.bias_qkv, workspace=ws))
-        K.rope(self.qkv, seq_len=self.seq_len, n_heads=s.n_heads + s.n_kv_heads, head_dim=s.head_dim,
-               cos_sin=self.cos_sin)
-        self._run("attn_fwd", lambda: K.attn_fwd(
-            self.qkv, batch=self.batch, seq_len=self.seq_len, n_heads=s.n_heads,
-            n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, scale=self.scale, out=self.attn, lse=self.lse))
-        wo = self.wqs["o"]
-
-        def o_proj():
-            K.gemm("nt", self.attn, wo[:, :hq_d], self.h2, M=T, N=h, K=hq_d, resid=x, workspace=ws)
-            K.gemm("nt", self.attn, wo[:, hq_d:2 * hq_d], self.h2, M=T, N=h, K=hq_d, resid=self.h2,
-                   workspace=ws)
-        self._run("gemm_o", o_proj)
+        # rotated in fp32, then hi (the backward's q/k/v) and lo halves
+        K.rope_split(self.qkv32, self.qkv, self.qkv_lo, seq_len=self.seq_len,
+                     n_rope_heads=s.n_heads + s.n_kv_heads, head_dim=s.head_dim, cos_sin=self.cos_sin)
+        self._run("attn_fwd", lambda: K.attn_fwd_split(
+            self.qkv, self.qkv_lo, batch=self.batch, seq_len=self.seq_len, n_heads=s.n_heads,
+            n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, scale=self.scale, out=self.attn,
+            out_split=self.attns, lse=self.lse))
+        self._run("gemm_o", lambda: K.gemm("nt", self.attns, self.wqs["o"], self.h2, M=T, N=h, K=3 * hq_d,
+                                           resid=x, workspace=ws))
         K.rmsnorm_fwd_split(self.h2, self.norm_post, s.norm_eps, self.x2s, self.x2, self.rstd2)
 
         def gate_up():

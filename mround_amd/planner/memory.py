@@ -118,10 +118,13 @@ def library_workspace_bytes(m: ModelShape, tokens: int, seq_len: int,
 
 def split_bytes(m: ModelShape, tokens: int) -> int:
     """What split precision adds to a ``BlockEngine``: fp32 W' and the split
-    W' operands, the split normalized inputs and SwiGLU output, and the fp32
-    gate/up pair."""
-    T, h, mlp = tokens, m.hidden, m.intermediate
-    return m.block_weights * (4 + 6) + 2 * T * 3 * h * 2 + T * 3 * mlp * 2 + T * 2 * mlp * 4
+    W' operands, the split normalized inputs and SwiGLU output, the fp32
+    gate/up pair, the fp32 q/k/v and their lo halves, and the split attention
+    output."""
+    T, h, mlp, q = tokens, m.hidden, m.intermediate, m.qkv_rows
+    hq_d = m.heads * m.head_dim
+    return (m.block_weights * (4 + 6) + 2 * T * 3 * h * 2 + T * 3 * mlp * 2 + T * 2 * mlp * 4
+            + T * q * (4 + 2) + T * 3 * hq_d * 2)
 
 
 def engine_bytes(m: ModelShape, tokens: int, seq_len: int, *, input_grads: bool = False,

@@ -195,3 +195,35 @@ def test_engine_workspaces_cover_every_piece():
         assert attn >= K.attn_bwd_workspace_bytes(batch=n, **q)
         assert gemm >= max(K.gemm_workspace_bytes(M, N, Kd) for M, N, Kd in gemm_problems(s, n * 2048))
     assert attn == max(K.attn_bwd_workspace_bytes(batch=n, **q) for n in range(1, 9))
+
+
+def test_split_precision_follows_the_tuned_widths(tmp_path):
+    """Split precision defaults on when a tuned width is 8 bits, in uniform
+    runs and in mixed runs whose candidates (or given plan) include 8, and
+    off otherwise; the predictions count it the same way; turning it off for
+    8-bit codes warns."""
+    import warnings
+
+    write_random_checkpoint(tmp_path / "m", TINY)
+    t = TuningConfig(n_samples=8, batch_size=4, seq_len=128)
+    peak = lambda **kw: api.predict_memory(tmp_path / "m", tuning=t, memory_budget=1 << 40, device="cpu",
+                                           **kw).prediction.peak
+    assert peak(bits=8) == peak(bits=8, split_precision=True) > peak(bits=8, split_precision=False)
+    assert peak(bits=4) == peak(bits=4, split_precision=False) < peak(bits=4, split_precision=True)
+    assert (peak(average_bits=5, candidate_bits=(4, 8)) ==
+            peak(average_bits=5, candidate_bits=(4, 8), split_precision=True))
+    assert (peak(average_bits=3, candidate_bits=(2, 4)) ==
+            peak(average_bits=3, candidate_bits=(2, 4), split_precision=False))
+    secs = lambda **kw: api.predict_time(tmp_path / "m", tuning=t, **kw).total
+    assert secs(bits=8) == secs(bits=8, split_precision=True) > secs(bits=8, split_precision=False)
+    assert api._split_choice(None, (8,))[0] and not api._split_choice(None, (2, 3, 4))[0]
+    assert api._split_choice(True, (4,)) == (True, "requested")
+    with pytest.warns(UserWarning, match="8-bit codes"):
+        assert api._split_choice(False, (4, 8)) == (False, "requested")
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        api._split_choice(False, (2, 4))
+    scheme = api.QuantScheme(bits=4, group_size=64)
+    assert api._tuned_widths(scheme, None, (2, 3, 4), None) == (4,)
+    assert api._tuned_widths(scheme, 3.0, (2, 3, 4), None) == (2, 3, 4)
+    assert api._tuned_widths(scheme, 3.0, (2, 3, 4, 8), {"a": 2, "b": 8}) == (2, 8)

@@ -295,6 +295,17 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
             void* stream);
 
 /*
+ * fp32 GEMM on the MFMA cores (fp32 products and accumulation), any sizes:
+ *   C[m, n] = sum_k A(m, k) (B(n, k) - B2(n, k))   (B2 may be NULL)
+ * in the layouts of mr_gemm (B2 shares B's layout and ldb); C fp32 [M, N]
+ * row-major. Replaces the float32 products of the reference's single-layer
+ * loop, the layer residual x (W' - W)^T and the weight gradient
+ * (dL/dr)^T x (mround/core/tuning.py:140-190).
+ */
+int mr_gemm_f32(int layout, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+                const float* B2, int64_t ldb, float* C, int64_t ldc, void* stream);
+
+/*
  * SwiGLU projection pair in one product: act = silu(x Wg^T) * (x Wu^T), bf16
  * [M, N], from the row-interleaved weight Wgu [2N, K] (rows 64b .. 64b+31 are
  * gate rows 32b .. 32b+31, rows 64b+32 .. 64b+63 the matching up rows; the

@@ -10,11 +10,12 @@ it: the residual then carries only its own rounding, not that of two large
 products subtracted.
 
 Per step: W' by the fake-quant kernel (fp32), the residual and dL/dW' as two
-fp32 library GEMMs (``x (W' - W)^T`` and ``(dL/dr)^T x``, any shape), the
-loss and dL/dr by the loss kernels (the outlier rule's threshold on the
-device), and the straight-through gradient, sign step and projection in one
-fused kernel on ``v``, ``alpha`` and ``beta`` in place. The loss is read
-back once per step, as the reference evaluates once per step.
+fp32 MFMA GEMMs (``mr_gemm_f32``: ``x (W' - W)^T``, the difference formed as
+the operand is loaded, and ``(dL/dr)^T x``, any shape), the loss and dL/dr
+by the loss kernels (the outlier rule's threshold on the device), and the
+straight-through gradient, sign step and projection in one fused kernel on
+``v``, ``alpha`` and ``beta`` in place. The loss is read back once per step,
+as the reference evaluates once per step.
 
 Portions follow MRound (Copyright 2026 The MRound Authors, Apache License 2.0);
 see NOTICE.
@@ -92,7 +93,7 @@ def tune_layer(weight: torch.Tensor, activations: torch.Tensor, scheme: QuantSch
     suppress = config.resolved_suppress_outliers(scheme.bits)
     dev = weight.device
     x = activations.to(device=dev, dtype=torch.float32).contiguous()
-    w32 = weight.to(torch.float32)
+    w32 = weight.to(torch.float32).contiguous()
     rows, cols = weight.shape
     n = x.shape[0]
     elements = n * rows
@@ -112,13 +113,13 @@ def tune_layer(weight: torch.Tensor, activations: torch.Tensor, scheme: QuantSch
     losses: list[float] = []
     for step in range(config.iters):
         fake_quantize(weight, params, scheme, eps=eps, init_scale=init_scale, out=qdq)
-        torch.matmul(x, (qdq - w32).T, out=residual)
+        K.gemm_f32("nt", x, qdq, residual, M=n, N=rows, K=cols, b_minus=w32)
         if suppress:
             K.loss_outlier(residual, zero, k=k, denom=elements, loss_out=loss_val, threshold_out=threshold,
                            grad_out=grad_r, workspace=ws)
         else:
             K.loss_mse(residual, zero, denom=elements, loss_out=loss_val, grad_out=grad_r, workspace=ws)
-        torch.matmul(grad_r.T, x, out=grad_w)
+        K.gemm_f32("tn", grad_r, x, grad_w, M=rows, N=cols, K=n)
         value = float(loss_val)
         losses.append(value)
         if value < best_loss:

@@ -86,6 +86,18 @@ __device__ __forceinline__ void store_elem(void* p, int64_t i, float x) {
   }
 }
 
+// x narrowed to DT and widened back: the value store_elem<DT> would store.
+template <int DT>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (DT == MR_F32) {
+    return x;
+  } else if constexpr (DT == MR_BF16) {
+    return bf16_to_f32(f32_to_bf16(x));
+  } else {
+    return f16_to_f32(f32_to_f16(x));
+  }
+}
+
 // 16-byte streaming accesses. Data read or written exactly once per pass goes
 // through these nontemporal forms, which keep it from displacing reused lines
 // in the caches; measured faster than plain accesses on the fake-quant passes.

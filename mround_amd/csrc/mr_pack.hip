@@ -142,15 +142,9 @@ __global__ __launch_bounds__(kBlock) void affine_kernel(const float* __restrict_
   // Round the scale to the stored dtype first; the bias is formed from the
   // stored value (mround/formats/mlx_export.py:186-195). A bf16/fp16 scale times
   // an integer zero point below 2^8 is exact in fp32, so one rounding remains.
-  store_elem<OT>(scales, i, scale[i]);
-  const float s = load_elem<OT>(scales, i);
-  float z;
-  if (zp) {
-    store_elem<OT>(biases, i, zp[i]);
-    z = load_elem<OT>(biases, i);
-  } else {
-    z = sym_offset;
-  }
+  const float s = round_to<OT>(scale[i]);
+  const float z = zp ? round_to<OT>(zp[i]) : sym_offset;
+  store_elem<OT>(scales, i, s);
   store_elem<OT>(biases, i, -s * z);
 }
 

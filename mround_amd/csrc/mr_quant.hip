@@ -362,7 +362,23 @@ __global__ __launch_bounds__(kBlock) void fq_fwd_fast(
 // into place in every word they touch, the four lanes OR their words together
 // by two xor-shuffles, and lane r of the four stores words r and r + 4.
 // Needs cols % 32 == 0 (every 32-code run lies in one row and one group).
-template <int WT, int OT, int MODE, bool HAS_V, int TPG>
+// Lane exchanges within each quad of lanes by DPP quad permutations (VALU,
+// no LDS): the value of lane l ^ 1 and of lane l ^ 2.
+__device__ __forceinline__ uint32_t quad_xor1(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t quad_xor2(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xF, 0xF, false));
+}
+// The value of the next lane of the quad (the last lane keeps its own).
+__device__ __forceinline__ uint32_t quad_next(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xF9, 0xF, 0xF, false));
+}
+
+// PB: the code width when it is 2, 3, 4 or 8 (a lane's 8 codes then fill half a
+// word, three quarters of one, one word or two words, in its quad's word
+// order), 0 for any width (5, 6, 7: codes straddle words).
+template <int WT, int OT, int MODE, bool HAS_V, int TPG, int PB>
 __global__ __launch_bounds__(kBlock) void fq_pack_fast(
     const void* __restrict__ w, const float* __restrict__ v, const float* __restrict__ alpha,
     const float* __restrict__ beta, const float* __restrict__ init_scale, uint32_t* __restrict__ packed,
@@ -395,7 +411,7 @@ __global__ __launch_bounds__(kBlock) void fq_pack_fast(
   const Group p = group_params<MODE>(mx, mn, a, b, base, maxq, inv_maxq, eps);
   float vv[8];
   if constexpr (HAS_V) {
-    load8_f32(v, e, vv);
+    load8_f32_cached(v, e, vv);
   } else {
 #pragma unroll
     for (int k = 0; k < 8; ++k) vv[k] = 0.0f;
@@ -404,41 +420,78 @@ __global__ __launch_bounds__(kBlock) void fq_pack_fast(
   const uint32_t off = MODE == MR_ASYM ? 0u : static_cast<uint32_t>(maxq);
   float t[8];
   quotients<WT, MODE>(x, p.s, lane_quotients_fast<WT>(x, mx, mn), t);
-  uint64_t stream = 0;
+  uint32_t u[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     float c, in;
     quant_t<MODE, HAS_V>(t[k], vv[k], p, qmin, qmax, c, in);
-    const uint32_t u = static_cast<uint32_t>(static_cast<int>(c) + static_cast<int>(off));
-    stream |= static_cast<uint64_t>(u) << (k * bits);
+    u[k] = static_cast<uint32_t>(static_cast<int>(c) + static_cast<int>(off));
   }
+  // Four consecutive lanes hold the 32 codes of a `bits`-word run; lane r's
+  // codes are stream bits [8 r bits, 8 (r + 1) bits).
   const int r = static_cast<int>(chunk & 3);
-  const int start = 8 * r * bits;  // this lane's first bit in the 32-code run
-  uint32_t word[8];
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int sh = start - 32 * q;  // where the lane's bits start relative to word q
-    uint32_t part = 0;
-    if (q < bits) {
-      if (sh >= 0) part = sh < 32 ? static_cast<uint32_t>(stream << sh) : 0u;
-      else part = -sh < 64 ? static_cast<uint32_t>(stream >> (-sh)) : 0u;
-    }
-    part |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(part), 1, 64));
-    part |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(part), 2, 64));
-    word[q] = part;
-  }
-  if (!active) return;
   uint32_t* dst = packed + (e >> 5) * bits;
-  if (r < bits) dst[r] = word[r];
-  if (r + 4 < bits) dst[r + 4] = word[r + 4];
-  if ((chunk & (tpg - 1)) == 0) {
-    store_elem<OT>(scales, grp, p.s);
-    const float sq = load_elem<OT>(scales, grp);
-    float z = maxq;  // symmetric: the stored code offset
-    if constexpr (MODE == MR_ASYM) {
-      store_elem<OT>(biases, grp, p.zp);
-      z = load_elem<OT>(biases, grp);
+  if constexpr (PB == 2 || PB == 4) {
+    uint32_t st = 0;  // the lane's 8 codes: 16 or 32 bits
+#pragma unroll
+    for (int k = 0; k < 8; ++k) st |= u[k] << (k * PB);
+    if constexpr (PB == 2) {
+      const uint32_t odd = quad_xor1(st);  // lanes 2j and 2j + 1 make word j
+      if (!active) return;
+      if (!(r & 1)) dst[r >> 1] = st | (odd << 16);
+    } else {
+      if (!active) return;
+      dst[r] = st;
     }
+  } else if constexpr (PB == 3) {
+    // 24 stream bits per lane: word r (r < 3) is bits 32 r .. 32 r + 31 of the
+    // run, the top 24 - 8 r bits of lane r's codes and the low 8 + 8 r bits
+    // of lane r + 1's.
+    uint32_t st = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) st |= u[k] << (3 * k);
+    const uint32_t nx = quad_next(st);
+    if (!active) return;
+    if (r < 3) dst[r] = (st >> (8 * r)) | (nx << (24 - 8 * r));
+  } else if constexpr (PB == 8) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo |= u[k] << (8 * k);
+      hi |= u[k + 4] << (8 * k);
+    }
+    if (!active) return;
+    dst[2 * r] = lo;  // (the words are only 4-byte aligned)
+    dst[2 * r + 1] = hi;
+  } else {
+    uint64_t stream = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) stream |= static_cast<uint64_t>(u[k]) << (k * bits);
+    const int start = 8 * r * bits;  // this lane's first bit in the 32-code run
+    uint32_t word[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int sh = start - 32 * q;  // where the lane's bits start relative to word q
+      uint32_t part = 0;
+      if (q < bits) {
+        if (sh >= 0) part = sh < 32 ? static_cast<uint32_t>(stream << sh) : 0u;
+        else part = -sh < 64 ? static_cast<uint32_t>(stream >> (-sh)) : 0u;
+      }
+      part |= quad_xor1(part);
+      part |= quad_xor2(part);
+      word[q] = part;
+    }
+    if (!active) return;
+    if (r < bits) dst[r] = word[r];
+    if (r + 4 < bits) dst[r + 4] = word[r + 4];
+  }
+  if ((chunk & (tpg - 1)) == 0) {
+    // scales = out(s), biases = out(-scales * out(zp)): the narrowed values
+    // are formed in registers, not read back from memory.
+    const float sq = round_to<OT>(p.s);
+    float z = maxq;  // symmetric: the stored code offset
+    if constexpr (MODE == MR_ASYM) z = round_to<OT>(p.zp);
+    store_elem<OT>(scales, grp, sq);
     store_elem<OT>(biases, grp, -sq * z);
   }
 }
@@ -883,10 +936,18 @@ int launch_pack(const Shape& sh, const void* w, int wt, const float* v, const fl
   const int64_t n_chunks = sh.rows * sh.cols / 8;
   const int64_t blocks = (n_chunks + kBlock - 1) / kBlock;
   if (blocks > 0x7fffffff) return fail(MR_EINVAL, "mr_quantize_pack: tensor too large");
-#define MR_PACK_T(WT_, OT_, T_)                                                                    \
-  hipLaunchKernelGGL((fq_pack_fast<WT_, OT_, MODE, HAS_V, T_>), dim3(static_cast<unsigned>(blocks)), \
+#define MR_PACK_TB(WT_, OT_, T_, PB_)                                                                    \
+  hipLaunchKernelGGL((fq_pack_fast<WT_, OT_, MODE, HAS_V, T_, PB_>), dim3(static_cast<unsigned>(blocks)), \
                      dim3(kBlock), 0, stream, w, v, alpha, beta, init_scale, packed, scales, biases,   \
                      n_chunks, sh.tpg, sh.tpg_shift, bits, sh.maxq, sh.inv_maxq, sh.qmin, sh.qmax, eps)
+#define MR_PACK_T(WT_, OT_, T_)                         \
+  do {                                                  \
+    if (bits == 2) MR_PACK_TB(WT_, OT_, T_, 2);         \
+    else if (bits == 3) MR_PACK_TB(WT_, OT_, T_, 3);    \
+    else if (bits == 4) MR_PACK_TB(WT_, OT_, T_, 4);    \
+    else if (bits == 8) MR_PACK_TB(WT_, OT_, T_, 8);    \
+    else MR_PACK_TB(WT_, OT_, T_, 0);                   \
+  } while (0)
 #define MR_PACK_W(WT_, OT_)                             \
   do {                                                  \
     if (sh.tpg == 8) MR_PACK_T(WT_, OT_, 8);            \
@@ -905,6 +966,7 @@ int launch_pack(const Shape& sh, const void* w, int wt, const float* v, const fl
 #undef MR_PACK_O
 #undef MR_PACK_W
 #undef MR_PACK_T
+#undef MR_PACK_TB
   MR_LAUNCH_CHECK("mr_quantize_pack");
   return MR_OK;
 }

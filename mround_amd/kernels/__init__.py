@@ -79,6 +79,7 @@ _SIGNATURES = {
     "mr_copy_bytes": (_I, [_P, _P, ctypes.c_size_t, _P]),
     "mr_gemm_workspace_bytes": (ctypes.c_size_t, [_L, _L, _L]),
     "mr_gemm": (_I, [_I, _L, _L, _L, _P, _L, _P, _L, _P, _I, _L, _P, _P, _L, _P, ctypes.c_size_t, _P]),
+    "mr_gemm_f32": (_I, [_I, _L, _L, _L, _P, _L, _P, _P, _L, _P, _L, _P]),
     "mr_gemm_swiglu": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P, ctypes.c_size_t, _P]),
     "mr_gemm_swiglu_bwd": (_I, [_L, _L, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P, ctypes.c_size_t, _P]),
     "mr_rmsnorm_fwd": (_I, [_P, _P, _L, _L, _F, _P, _P, _P]),
@@ -430,6 +431,21 @@ def gemm(layout: str, a, b, c, *, M, N, K, bias=None, resid=None, workspace=None
                        _rows_ptr(_f32(resid, "resid")), resid.stride(0) if resid is not None else 0,
                        ws_ptr, ws_bytes, _stream(a))
     _check(rc, "mr_gemm")
+
+
+def gemm_f32(layout: str, a, b, c, *, M, N, K, b_minus=None) -> None:
+    """``mr_gemm_f32``: C = op(A) (op(B) - op(b_minus)) in fp32 on the MFMA
+    cores, any sizes; leading dimensions from the strides (``b_minus``
+    shares ``b``'s)."""
+    for name, t in (("a", a), ("b", b), ("c", c)) + ((("b_minus", b_minus),) if b_minus is not None else ()):
+        if t.dtype != torch.float32 or t.stride(-1) != 1:
+            raise KernelError(f"gemm_f32: {name} must be float32 with unit column stride")
+    if b_minus is not None and (b_minus.shape != b.shape or b_minus.stride(0) != b.stride(0)):
+        raise KernelError("gemm_f32: b_minus must share b's shape and layout")
+    rc = lib().mr_gemm_f32(GEMM_LAYOUT[layout], M, N, K, _rows_ptr(a), a.stride(0), _rows_ptr(b),
+                           _rows_ptr(b_minus) if b_minus is not None else None, b.stride(0), _rows_ptr(c),
+                           c.stride(0), _stream(a))
+    _check(rc, "mr_gemm_f32")
 
 
 def gemm_swiglu(x, wgu, act, gu=None, *, workspace=None) -> None:

@@ -277,6 +277,10 @@ class QuantizationRunner:
                 if reverted:
                     for name, layer in pending["layers"].items():
                         layer.restore(pending["start"][name])
+                        # the tuned commit's codes and reconstruction go first, so that
+                        # the round-to-nearest commit reuses their memory
+                        layers.pop(f"{block.name}.{name}", None)
+                        block.weights.linears[name] = layer.weight
                         layers[f"{block.name}.{name}"] = self._commit(block, layer)
                     self._advance(eng, block, quantized_stream, spare, None, pending["suppress"])
                 quantized_stream, spare = spare, quantized_stream

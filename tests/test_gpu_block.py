@@ -272,32 +272,41 @@ def _rtn32(w: torch.Tensor, bits: int) -> torch.Tensor:
 
 # Measured on both shapes: loss within 2.8e-4, 6.2e-4, 2.0e-3 of float64 at 2, 3,
 # 4 bits; dL/dW' within 4.2e-2 normwise; flipped gradient mass below 4.4e-4.
-PRECISION_BARS = {2: (1e-3, 3e-2, 2e-4), 3: (2e-3, 4e-2, 5e-4), 4: (5e-3, 6e-2, 1e-3)}
+# At 8 bits the objective runs in split precision (what api.quantize runs for
+# 8-bit codes): measured loss within 4.9e-5, dL/dW' within 6.2e-3 normwise,
+# flipped mass 1.0e-5 (the one-product objective: 0.29-0.34, 0.63-0.65,
+# 7.8e-2), held to 5e-4, 2e-2 and 1e-4.
+PRECISION_BARS = {2: (1e-3, 3e-2, 2e-4), 3: (2e-3, 4e-2, 5e-4), 4: (5e-3, 6e-2, 1e-3), 8: (5e-4, 2e-2, 1e-4)}
 
 
 @pytest.mark.parametrize("key", ["smollm", "d128"])
 def test_objective_precision_by_width(key):
-    """How far the bf16-operand block objective sits from the exact one, by
-    code width, the way the runner forms it: targets from the engine's own
-    forward of the original weights, W' the fp32 round-to-nearest
-    reconstruction (rounded to bf16 by the engine), against float64 with the
-    exact W'. The block residual shrinks about 4x per bit while the bf16
-    rounding of W' and of the activations does not: at 2-4 bits the objective
-    and its gradient are within the bars below; at 8 bits the rounding is as
-    large as the residual (measured: loss 29-34 % high, dL/dW' 63-65 % off
-    normwise, 8 % of its mass of the wrong sign, of which W''s own bf16
-    rounding alone is +13 % of the loss), which the test records and bounds
-    only loosely."""
+    """How far the block objective sits from the exact one, by code width, the
+    way the runner forms it: targets from the engine's own forward of the
+    original weights, W' the fp32 round-to-nearest reconstruction, against
+    float64 with the exact W'. The block residual shrinks about 4x per bit
+    while the bf16 rounding of W' and of the activations does not: at 2-4
+    bits the one-product (bf16 operand) objective and its gradient are within
+    the bars below; at 8 bits that rounding is as large as the residual
+    (measured: loss 29-34 % high, dL/dW' 63-65 % off normwise, 8 % of its mass
+    of the wrong sign), so 8-bit codes run the objective in split precision
+    (every forward product, the attention's included, over bf16 hi/lo
+    halves), which holds the 1e-2 bar; the one-product figure is recorded and
+    bounded only loosely."""
     print("case objective precision", key, flush=True, file=sys.stderr)
     shape, B, S, w, x = _problem(key, seed=1)
     t64 = _oracle_forward(shape, B, S, w, x).reshape(B * S, -1)
-    eng = BlockEngine(shape, batch=B, seq_len=S, device=dev())
-    eng.set_block(_to_dev(w))
-    eng.load_dense({n: t.to(dev()) for n, t in w.linears.items()})
-    target = torch.empty(B * S, shape.hidden, device=dev())
-    eng.forward(x.to(dev()), target, save=False)
+    engines = {}
+    for split in (False, True):
+        eng = BlockEngine(shape, batch=B, seq_len=S, device=dev(), split=split)
+        eng.set_block(_to_dev(w))
+        eng.load_dense({n: t.to(dev()) for n, t in w.linears.items()})
+        target = torch.empty(B * S, shape.hidden, device=dev())
+        eng.forward(x.to(dev()), target, save=False)
+        engines[split] = (eng, target)
     place = placements(shape)
-    for bits in (2, 3, 4, 8):
+    for bits, split in ((2, False), (3, False), (4, False), (8, False), (8, True)):
+        eng, target = engines[split]
         wq = {n: _rtn32(w.linears[n], bits) for n in LAYERS}
         lin = {n: wq[n].double().requires_grad_(True) for n in LAYERS}
         loss = ((_oracle_forward(shape, B, S, w, x, linears=lin).reshape(B * S, -1) - t64) ** 2).mean()
@@ -315,10 +324,10 @@ def test_objective_precision_by_width(key):
             g = unplace(eng.dw[place[n].operand], ref.shape[0], place[n]).double().cpu()
             rels.append(float((g - ref).norm() / ref.norm()))
             flips.append(float(ref.abs()[torch.sign(g) != torch.sign(ref)].sum() / ref.abs().sum()))
-        print(f"  {bits} bits: loss {rel_loss:.2e}, dW' {max(rels):.2e}, flipped {max(flips):.2e}",
-              file=sys.stderr)
-        if bits in PRECISION_BARS:
+        print(f"  {bits} bits{' split' if split else ''}: loss {rel_loss:.2e}, dW' {max(rels):.2e}, "
+              f"flipped {max(flips):.2e}", file=sys.stderr)
+        if bits < 8 or split:
             b_loss, b_dw, b_flip = PRECISION_BARS[bits]
-            assert rel_loss <= b_loss and max(rels) <= b_dw and max(flips) <= b_flip, bits
+            assert rel_loss <= b_loss and max(rels) <= b_dw and max(flips) <= b_flip, (bits, split)
         else:
             assert np.isfinite(got) and rel_loss < 0.6 and max(flips) < 0.2

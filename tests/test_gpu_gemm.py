@@ -307,3 +307,38 @@ def test_gemm_residual_every_layout(layout, mnk, inplace):
         assert K.gemm_workspace_bytes(M, N, Kd) > 0  # the k-split path
     K.gemm(layout, a, b, c, M=M, N=N, K=Kd, resid=resid)
     assert bool(torch.all((c - ref).abs() <= bound + ref.abs() * 2.0**-22))
+
+
+# ------------------------------------------------------------------ fp32 GEMM --
+# mr_gemm_f32, the single-layer loop's products: fp32 products and
+# accumulation, any sizes, B - B2 formed as the operand is loaded. Bound: the
+# float64 product of the same fp32 operands within (K + 4) 2^-23 of the sum of
+# magnitudes (fp32 accumulation, the subtraction's own rounding, a factor 2
+# of margin); columns past N and rows past M untouched.
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("mnk", [(128, 16, 64), (300, 77, 130), (1, 1, 1), (513, 257, 1000), (64, 2048, 33)])
+@pytest.mark.parametrize("minus", [False, True])
+def test_gemm_f32(layout, mnk, minus):
+    M, N, Kd = mnk
+    print("case gemm f32", layout, mnk, minus, flush=True, file=sys.stderr)
+    g = torch.Generator().manual_seed(71)
+    a = torch.randn(M, Kd, generator=g)
+    b = torch.randn(N, Kd, generator=g)
+    b2 = torch.randn(N, Kd, generator=g) * 0.5 if minus else None
+    bm = b - b2 if minus else b
+    want = a.double() @ bm.double().T
+    mags = a.double().abs() @ (b.double().abs() + (b2.double().abs() if minus else 0)).T
+    # the operands in the layout's memory order
+    A = a if layout != "tn" else a.T.contiguous()
+    B = b if layout == "nt" else b.T.contiguous()
+    B2 = None if not minus else (b2 if layout == "nt" else b2.T.contiguous())
+    c = torch.full((M + 3, N + 5), 7.0, device=dev())
+    K.gemm_f32(layout, A.to(dev()), B.to(dev()), c[:M, :N], M=M, N=N, K=Kd,
+               b_minus=None if B2 is None else B2.to(dev()))
+    got = c.double().cpu()
+    assert torch.all((got[:M, :N] - want).abs() <= (Kd + 4) * 2.0**-23 * mags + 1e-30)
+    assert torch.all(got[M:] == 7.0) and torch.all(got[:, N:] == 7.0)
+    # deterministic
+    c2 = torch.empty(M, N, device=dev())
+    K.gemm_f32(layout, A.to(dev()), B.to(dev()), c2, M=M, N=N, K=Kd, b_minus=None if B2 is None else B2.to(dev()))
+    assert torch.equal(c2.cpu(), c[:M, :N].cpu())

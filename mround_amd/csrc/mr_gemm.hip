@@ -306,13 +306,16 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
       // The same wave reads back what it wrote (LDS keeps a wave's accesses
       // in order), then the next slice overwrites the region.
       const int row0 = m0 + wm * WM + i * 32;
+      // uniform bases of the slice; lane offsets stay 32-bit (ld < 2^22, 32 rows)
+      uint16_t* const act_s = act + static_cast<int64_t>(row0) * p.ldc;
+      uint16_t* const gu_s = p.gu + static_cast<int64_t>(row0) * p.ldgu;
 #pragma unroll
       for (int it = 0; it < 32 * CA / 64; ++it) {
         const int idx = it * 64 + lane, r = idx / CA, ch = idx % CA;
         const u32x4 v = *(lds_u32x4*)(sa + r * PA + ch * 16);
         const int col = (n0 + wn * WN) / 2 + ch * 8;
         if (row0 + r < p.M && col < p.n_out)
-          *reinterpret_cast<u32x4*>(act + static_cast<int64_t>(row0 + r) * p.ldc + col) = v;
+          *reinterpret_cast<u32x4*>(act_s + static_cast<uint32_t>(r * static_cast<int>(p.ldc) + col)) = v;
       }
       if (p.gu) {
 #pragma unroll
@@ -321,7 +324,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
           const u32x4 v = *(lds_u32x4*)(sg + r * PG + ch * 16);
           const int col = n0 + wn * WN + ch * 8;
           if (row0 + r < p.M && col < 2 * p.n_out)
-            *reinterpret_cast<u32x4*>(p.gu + static_cast<int64_t>(row0 + r) * p.ldgu + col) = v;
+            *reinterpret_cast<u32x4*>(gu_s + static_cast<uint32_t>(r * static_cast<int>(p.ldgu) + col)) = v;
         }
       }
     }
@@ -362,14 +365,17 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
         // stores are guarded.
         const int row0 = m0 + wm * WM + i * 32;
         const int col0 = n0 + wn * WN + jb * JH * 32;
+        const uint16_t* const gu_s = p.gu + static_cast<int64_t>(row0) * p.ldgu;
+        uint16_t* const dgu_s = dgu + static_cast<int64_t>(row0) * p.ldc;
         u32x4 gv[NIT], uv[NIT];
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
           const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
           const int row = min(row0 + r, p.M - 1), col = min(col0 + ch * 8, p.N - 8);
-          const int64_t o = static_cast<int64_t>(row) * p.ldgu + (col >> 5) * 64 + (col & 31);
-          gv[it] = *reinterpret_cast<const u32x4*>(p.gu + o);
-          uv[it] = *reinterpret_cast<const u32x4*>(p.gu + o + 32);
+          // signed: a slice wholly past the edge clamps to row M - 1, below row0
+          const int o = (row - row0) * static_cast<int>(p.ldgu) + (col >> 5) * 64 + (col & 31);
+          gv[it] = *reinterpret_cast<const u32x4*>(gu_s + o);
+          uv[it] = *reinterpret_cast<const u32x4*>(gu_s + o + 32);
         }
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
@@ -390,10 +396,10 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
             du[e] = da[e] * g * sg;
           }
           if (row < p.M && col < p.N) {
-            const int64_t od = static_cast<int64_t>(row) * p.ldc + (col >> 5) * 64 + (col & 31);
-            *reinterpret_cast<u32x4*>(dgu + od) = u32x4{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]),
+            const uint32_t od = static_cast<uint32_t>(r * static_cast<int>(p.ldc) + (col >> 5) * 64 + (col & 31));
+            *reinterpret_cast<u32x4*>(dgu_s + od) = u32x4{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]),
                                                         pack_bf16x2(dg[4], dg[5]), pack_bf16x2(dg[6], dg[7])};
-            *reinterpret_cast<u32x4*>(dgu + od + 32) = u32x4{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]),
+            *reinterpret_cast<u32x4*>(dgu_s + od + 32) = u32x4{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]),
                                                              pack_bf16x2(du[4], du[5]), pack_bf16x2(du[6], du[7])};
           }
         }
@@ -415,57 +421,76 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
     constexpr int CH = JH * 32 * OBY / 16;  // 16-byte pieces per staged row
     static_assert(32 * PITCH <= REGION && TN % JH == 0, "staging does not fit");
     lds_u8* st = (lds_u8*)region;
+    const bool has_bias = p.bias != nullptr;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int jb = 0; jb < TN / JH; ++jb) {
+        // the slice's accumulators (plus the bias: one uniform branch, two copies) into LDS
+        auto stage = [&](auto biasc) __attribute__((always_inline)) {
+          constexpr bool BIAS = decltype(biasc)::value;
 #pragma unroll
-        for (int jj = 0; jj < JH; ++jj) {
-          const int j = jb * JH + jj;
+          for (int jj = 0; jj < JH; ++jj) {
+            const int j = jb * JH + jj;
 #pragma unroll
-          for (int gi = 0; gi < 4; ++gi) {
-            const int col = n0 + wn * WN + j * 32 + gi * 8 + lrow;
-            float v[4];
+            for (int gi = 0; gi < 4; ++gi) {
+              float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * gi + e] + ((p.bias && col + e < p.N) ? p.bias[col + e] : 0.0f);
-            lds_u8* at = st + lcol * PITCH + (jj * 32 + gi * 8 + lrow) * OBY;
-            if constexpr (OUT_BF16) {
-              u32x2 w;
-              w.x = pack_bf16x2(v[0], v[1]);
-              w.y = pack_bf16x2(v[2], v[3]);
-              *(__attribute__((address_space(3))) u32x2*)at = w;
-            } else {
-              *(__attribute__((address_space(3))) f32x4*)at = f32x4{v[0], v[1], v[2], v[3]};
+              for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * gi + e];
+              if constexpr (BIAS) {
+                // N is a multiple of 8: a group of 4 columns lies wholly inside or past the edge
+                const int col = min(n0 + wn * WN + j * 32 + gi * 8 + lrow, p.N - 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] += p.bias[col + e];
+              }
+              lds_u8* at = st + lcol * PITCH + (jj * 32 + gi * 8 + lrow) * OBY;
+              if constexpr (OUT_BF16) {
+                u32x2 w;
+                w.x = pack_bf16x2(v[0], v[1]);
+                w.y = pack_bf16x2(v[2], v[3]);
+                *(__attribute__((address_space(3))) u32x2*)at = w;
+              } else {
+                *(__attribute__((address_space(3))) f32x4*)at = f32x4{v[0], v[1], v[2], v[3]};
+              }
             }
           }
-        }
+        };
+        if (has_bias) stage(std::true_type{});
+        else stage(std::false_type{});
         const int row0 = m0 + wm * WM + i * 32;
         const int col0 = n0 + wn * WN + jb * JH * 32;
+        // uniform bases of the slice; lane offsets stay 32-bit (ld < 2^22, 32 rows)
+        const int64_t cbase = static_cast<int64_t>(row0) * p.ldc + col0;
+        uint16_t* const cb16 = static_cast<uint16_t*>(p.C) + cbase;
+        float* const cb32 = static_cast<float*>(p.C) + cbase;
         constexpr int NIT = 32 * CH / 64;
         f32x4 res[EPI == EPI_RESID ? NIT : 1];
         if constexpr (EPI == EPI_RESID) {
           // every residual piece of the slice in flight before any store
           // (the output may be the residual itself, so stores cannot move ahead)
+          const float* const rs = p.resid + static_cast<int64_t>(row0) * p.ldr;
 #pragma unroll
           for (int it = 0; it < NIT; ++it) {
             const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
             const int row = min(row0 + r, p.M - 1), col = min(col0 + ch * 4, p.N - 4);
-            res[it] = *reinterpret_cast<const f32x4*>(p.resid + static_cast<int64_t>(row) * p.ldr + col);
+            // signed: a slice wholly past the edge clamps to row M - 1, below row0
+            res[it] = *reinterpret_cast<const f32x4*>(rs + ((row - row0) * static_cast<int>(p.ldr) + col));
           }
         }
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
           const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
           const int row = row0 + r, col = col0 + ch * (16 / OBY);
+          const uint32_t oc = static_cast<uint32_t>(r * static_cast<int>(p.ldc) + ch * (16 / OBY));
           if (row < p.M && col < p.N) {
             if constexpr (OUT_BF16) {
               typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
               const u32x4 w = *(__attribute__((address_space(3))) u32x4*)(st + r * PITCH + ch * 16);
-              *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = w;
+              *reinterpret_cast<u32x4*>(cb16 + oc) = w;
             } else {
               f32x4 w = *(__attribute__((address_space(3))) f32x4*)(st + r * PITCH + ch * 16);
               if constexpr (EPI == EPI_RESID) w = res[it] + w;
-              *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + static_cast<int64_t>(row) * p.ldc + col) = w;
+              *reinterpret_cast<f32x4*>(cb32 + oc) = w;
             }
           }
         }
@@ -1140,7 +1165,8 @@ int dispatch(GemmParams p, hipStream_t s) {
   return launch<256, 256, AK, BKM, EPI, OB>(p, s);
 }
 
-// Load offsets are 32-bit: 256 rows of a K-major tile span 256 * ld * 2 bytes.
+// Load offsets are 32-bit: 256 rows of a K-major tile span 256 * ld * 2 bytes;
+// the epilogues' lane offsets within a 32-row slice of an output are 32-bit too.
 constexpr int kMaxLd = 1 << 22;
 
 bool ok16(const void* p, int64_t ld) {
@@ -1182,7 +1208,7 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
     return fail(MR_EINVAL, "mr_gemm: M and N must be multiples of 8 and K a positive multiple of %d "
                 "(M=%lld N=%lld K=%lld)", BK, (long long)M, (long long)N, (long long)K);
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return fail(MR_EINVAL, "mr_gemm: too large");
-  if (lda > kMaxLd || ldb > kMaxLd)
+  if (lda > kMaxLd || ldb > kMaxLd || ldc > kMaxLd || (resid && ldr > kMaxLd))
     return fail(MR_EINVAL, "mr_gemm: leading dimensions above %d are not supported", kMaxLd);
   if (!ok16(A, lda) || !ok16(B, ldb))
     return fail(MR_EINVAL, "mr_gemm: operands must be 16-byte aligned with ld a multiple of 8");
@@ -1238,7 +1264,8 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
   if (!ok16(X, ldx) || !ok16(Wgu, ldw) || !ok16(act, ldact) || (gu && !ok16(gu, ldgu)))
     return fail(MR_EINVAL, "mr_gemm_swiglu: operands and outputs must be 16-byte aligned with leading "
                 "dimensions multiples of 8");
-  if (ldx < K || ldw < K || ldact < N || (gu && ldgu < 2 * N) || ldx > kMaxLd || ldw > kMaxLd)
+  if (ldx < K || ldw < K || ldact < N || (gu && ldgu < 2 * N) || ldx > kMaxLd || ldw > kMaxLd ||
+      ldact > kMaxLd || (gu && ldgu > kMaxLd))
     return fail(MR_EINVAL, "mr_gemm_swiglu: bad leading dimension");
   GemmParams p{};
   p.M = static_cast<int>(M);
@@ -1270,7 +1297,7 @@ int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t 
   if (!ok16(dd, ldd) || !ok16(Wd, ldw) || !ok16(gu, ldgu) || !ok16(dgu, lddgu))
     return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: operands and gu/dgu must be 16-byte aligned with leading "
                 "dimensions multiples of 8");
-  if (ldd < K || ldw < N || lddgu < 2 * N || ldd > kMaxLd || ldw > kMaxLd)
+  if (ldd < K || ldw < N || lddgu < 2 * N || ldd > kMaxLd || ldw > kMaxLd || lddgu > kMaxLd)
     return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: bad leading dimension");
   if (ldgu != lddgu) return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: gu and dgu must share a layout");
   GemmParams p{};

@@ -719,7 +719,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 }
 
 
-// ---- 4-wave kernel for whole 256 x 256 tiles --------------------------------
+// ---- 4-wave kernel for 256 x 256 tiles ---------------------------------------
 //
 // One wave per SIMD, each owning 128 x 128 of the tile (256 accumulator
 // registers, held in AGPRs): half the LDS operand reads per MFMA of the 8-wave
@@ -750,8 +750,15 @@ __global__ __launch_bounds__(64 * kWaves4) __attribute__((amdgpu_waves_per_eu(1,
   __shared__ __attribute__((aligned(1024))) uint8_t Bs0[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t Bs1[STAGE];
 
-  int bid = blockIdx.x;
-  if ((p.n_tiles & 7) == 0) bid = (bid & 7) * (p.n_tiles >> 3) + (bid >> 3);
+  // A k-split launch takes the splits of one tile as consecutive blocks, each
+  // over kt_per k-tiles (the last over what remains).
+  int bid = blockIdx.x, split = 0;
+  if (p.ksplit > 1) {
+    split = bid % p.ksplit;
+    bid /= p.ksplit;
+  } else if ((p.n_tiles & 7) == 0) {
+    bid = (bid & 7) * (p.n_tiles >> 3) + (bid >> 3);
+  }
   int bm, bn;
   tile_coords(p.tile0 + bid, p.grid_m, p.grid_n, bm, bn);
   const int m0 = bm * BM, n0 = bn * BN;
@@ -763,8 +770,9 @@ __global__ __launch_bounds__(64 * kWaves4) __attribute__((amdgpu_waves_per_eu(1,
   std::conditional_t<B_KMAJOR, KMajorDirect<BN>, MNMajorDirect<BN>> ld_b;
   ld_a.init(p.lda, m0, p.M);
   ld_b.init(p.ldb, n0, p.N);
-  const int KT = p.K / BK;
-  auto tk = [&](int u) { return min(u, KT - 1); };
+  const int kt0 = split * p.kt_per;
+  const int KT = min(p.K / BK - kt0, p.kt_per);  // this block's k-tiles: kt0 .. kt0 + KT - 1
+  auto tk = [&](int u) { return kt0 + min(u, KT - 1); };
   auto ra_at = [&](int kt) { return ld_a.at(p.A, p.lda, m0, A_KMAJOR ? p.M : p.K, kt * BK); };
   auto rb_at = [&](int kt) { return ld_b.at(p.B, p.ldb, n0, B_KMAJOR ? p.N : p.K, kt * BK); };
 
@@ -852,7 +860,7 @@ __global__ __launch_bounds__(64 * kWaves4) __attribute__((amdgpu_waves_per_eu(1,
     // k-tile 0 whole, then k-tile 1's A and the first half of its B, into the
     // stages of positions phase and phase + 1
     auto pro = [&](uint8_t* a0, uint8_t* b0, uint8_t* a1, uint8_t* b1) __attribute__((always_inline)) {
-      const rsrc_t r_a0 = ra_at(0), r_b0 = rb_at(0);
+      const rsrc_t r_a0 = ra_at(tk(0)), r_b0 = rb_at(tk(0));
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         ld_a.issue_one(r_a0, i, a0);
@@ -937,6 +945,20 @@ __global__ __launch_bounds__(64 * kWaves4) __attribute__((amdgpu_waves_per_eu(1,
   // the repeated last loads land, every wave is past its reads: LDS is free
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (p.ksplit > 1) {  // raw partial tile; the reduce kernel applies the epilogue
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    float* out = p.ws + (static_cast<int64_t>(bid) * p.ksplit + split) * (BM * BN);
+    const int lrow = (lane >> 5) * 4, lcol = lane & 31;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+          *reinterpret_cast<f32x4*>(out + (wm * WM + i * 32 + lcol) * BN + wn * WN + j * 32 + gi * 8 + lrow) =
+              f32x4{acc[i][j][4 * gi], acc[i][j][4 * gi + 1], acc[i][j][4 * gi + 2], acc[i][j][4 * gi + 3]};
+    return;
+  }
   uint8_t* region = wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? As2 : Bs0;
   store_tile<WM, WN, STAGE, EPI, OUT_BF16>(p, acc, m0, n0, wm, wn, lane, region);
 }
@@ -1128,8 +1150,12 @@ int launch(GemmParams p, hipStream_t s) {
   p.n_tiles = static_cast<int>(tail);
   p.kt_per = (KT + split - 1) / split;
   p.ksplit = (KT + p.kt_per - 1) / p.kt_per;  // no empty split
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BKM, EPI, OB>),
-                     dim3(static_cast<unsigned>(tail * p.ksplit)), dim3(kThreads), 0, s, p);
+  if (BM == 256 && use_4wave(p.kt_per))
+    hipLaunchKernelGGL((gemm4_kernel<AK, BKM, EPI, OB>), dim3(static_cast<unsigned>(tail * p.ksplit)),
+                       dim3(64 * kWaves4), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BKM, EPI, OB>),
+                       dim3(static_cast<unsigned>(tail * p.ksplit)), dim3(kThreads), 0, s, p);
   constexpr int CW = EPI == EPI_SWIGLU ? BN / 2 : BN;
   const int64_t threads = tail * BM * (CW / 4);
   hipLaunchKernelGGL((gemm_reduce<BM, BN, EPI, OB>), dim3(static_cast<unsigned>((threads + 255) / 256)),

@@ -7,6 +7,7 @@ in two, a stage pattern that repeats every 6 k-tiles).
   bound 2 K 2^-23 |A||B| (plus the bf16 output rounding).
 * Ragged edges (M and N off the tile) with the bias and residual epilogue.
 * The SwiGLU forward and backward epilogues.
+* K-split tails (raw partial tiles summed in split order by the reduce kernel).
 * Bit-identity with the 8-wave kernel (MR_GEMM_8WAVE=1): both accumulate each
   output over the same k16 steps in the same order with the same MFMA, so every
   layout and epilogue must give the same bits.
@@ -142,3 +143,25 @@ def test_4wave_swiglu_backward(kt):
     with _EightWave():
         K.gemm_swiglu_bwd(dd, wd, gu, dgu8)
     assert torch.equal(dgu, dgu8), "4-wave and 8-wave kernels differ"
+
+
+@pytest.mark.parametrize("layout", ["nt", "nn", "tn"])
+@pytest.mark.parametrize("mnk", [(4096, 4352, 6144), (904, 696, 6400)])
+def test_4wave_k_split(layout, mnk):
+    # 4096 x 4352: one whole wave of 256 tiles and 16 past it, cut along K;
+    # 904 x 696 (12 tiles, under one wave, long K): the whole grid cut along K.
+    # The split blocks run on the 4-wave kernel and write raw partial tiles
+    # that the reduce kernel sums in split order, as the 8-wave kernel's do.
+    M, N, Kd = mnk
+    print("case gemm4 k-split", layout, mnk, flush=True, file=sys.stderr)
+    a, b, a_ref, b_ref = _operands(layout, M, N, Kd, seed=170)
+    ref, bound = _gpu_ref(a_ref, b_ref)
+    ws = torch.empty(max(K.gemm_workspace_bytes(M, N, Kd), 16), dtype=torch.uint8, device=dev())
+    assert K.gemm_workspace_bytes(M, N, Kd) > 0, "this shape is expected to split"
+    c = torch.full((M, N), 7.0, device=dev())
+    K.gemm(layout, a, b, c, M=M, N=N, K=Kd, workspace=ws)
+    assert bool(torch.all((c - ref).abs() <= bound))
+    c8 = torch.full((M, N), 5.0, device=dev())
+    with _EightWave():
+        K.gemm(layout, a, b, c8, M=M, N=N, K=Kd, workspace=ws)
+    assert torch.equal(c, c8), "4-wave and 8-wave kernels differ"

@@ -34,6 +34,14 @@ constexpr int KT = 64;   // keys per LDS tile
 constexpr int kAhead = 1;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+template <int V>
+using Ic = std::integral_constant<int, V>;
+
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(vm) lgkmcnt(0), expcnt not
+// waited on: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8. Through the
+// builtin, unlike inline assembly, the compiler's own wait insertion knows
+// the wait happened and adds none of its own for the loads it covers.
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -78,23 +86,28 @@ typedef __attribute__((address_space(1))) void gbl_void_t;
 // instruction fills 1 KB = 64 / (D / 8) rows; lane l covers row l / (D / 8)
 // of it at physical chunk l % (D / 8), i.e. logical chunk (l % (D/8)) ^ swz_bits(row).
 template <int D, int NW = 4>
-__device__ __forceinline__ void dma_rowtile(const uint16_t* src, int64_t ld, int64_t r0, int col,
-                                            uint8_t* lds, int wave = -1) {
+__device__ __forceinline__ void dma_rowtile_one(const uint16_t* src, int64_t ld, int64_t r0, int col,
+                                                uint8_t* lds, int i, int wave) {
   constexpr int CPR = D / 8;
   constexpr int RPI = 64 / CPR;
+  const int lane = threadIdx.x & 63;
+  const int sub = lane / CPR, pchunk = lane % CPR;
+  const int rb = (i * NW + wave) * RPI;
+  const int row = rb + sub;
+  const int c = pchunk ^ swz_bits<D>(row);
+  const uint16_t* g = src + (r0 + row) * ld + col + c * 8;
+  __builtin_amdgcn_global_load_lds((const gbl_void_t*)g, (lds_void_t*)(lds + rb * (2 * D)), 16, 0, 0);
+}
+// The INSTR instructions of one wave (dma_rowtile_one issues instruction i alone).
+template <int D, int NW = 4>
+__device__ __forceinline__ void dma_rowtile(const uint16_t* src, int64_t ld, int64_t r0, int col,
+                                            uint8_t* lds, int wave = -1) {
+  constexpr int RPI = 64 / (D / 8);
   constexpr int INSTR = 64 / RPI / NW;
   static_assert(INSTR * RPI * NW == 64, "the waves must split the tile evenly");
-  const int lane = threadIdx.x & 63;
   if (wave < 0) wave = threadIdx.x >> 6;  // else: this wave's index among the NW
-  const int sub = lane / CPR, pchunk = lane % CPR;
 #pragma unroll
-  for (int i = 0; i < INSTR; ++i) {
-    const int rb = (i * NW + wave) * RPI;
-    const int row = rb + sub;
-    const int c = pchunk ^ swz_bits<D>(row);
-    const uint16_t* g = src + (r0 + row) * ld + col + c * 8;
-    __builtin_amdgcn_global_load_lds((const gbl_void_t*)g, (lds_void_t*)(lds + rb * (2 * D)), 16, 0, 0);
-  }
+  for (int i = 0; i < INSTR; ++i) dma_rowtile_one<D, NW>(src, ld, r0, col, lds, i, wave);
 }
 
 // Transposed MFMA operand from a rowtile with ds_read_b64_tr_b16. In each
@@ -879,6 +892,397 @@ __global__ __launch_bounds__(2 * kThreads) __attribute__((amdgpu_waves_per_eu(2)
   }
 }
 
+// dK, dV at D = 128 with one wave per SIMD. A block of four waves owns 128
+// keys of one kv head (32 per wave: K and V fragments in registers, dK and dV
+// accumulators) and walks, for every query head of the group, the 32-query
+// tiles at or after its first key ("items"), as a software pipeline over
+// eight LDS stages of Q, dO and the items' lse and rowsum(dO O). Iteration i
+// runs two MFMA phases: A, the dV and dK products of item i - 1; B, the S^T
+// and dP^T products of item i + 1. Between those MFMAs run item i's
+// probabilities, causal mask, dS and bf16 conversions, so that one wave's
+// MFMA and VALU work overlap. (Two waves sharing a SIMD, one computing while
+// the other multiplies, overlap poorly: a SIMD running an MFMA wave beside a
+// VALU wave issued MFMAs at about a third of their rate.)
+// One barrier per iteration, ahead of phase A's last two groups: before it
+// each wave waits for its direct loads of item i + 1's stage; after it, item
+// i - 1's stage is free and takes item i + 7's loads (six iterations to land).
+// With one wave per SIMD every instruction takes an issue slot of about 4
+// cycles, and an MFMA 32: the loop spends about 10 instructions per MFMA
+// (operand reads, the arithmetic, scalar address updates), so it is bound by
+// issue and, at the matrix cores' power draw, by the clock more than by the
+// matrix cores themselves. Measured on the 7B launch: 12 % fewer cycles than
+// attn_bwd_dkdv_pair, at a clock about as much lower, the same time.
+// Edges without branches: item -1's stage is zeroed and its P and dS are
+// zeros (its products add +0.0 to zeroed accumulators); items past the last
+// reload the last one (finite data); the iterations past the last item (one
+// to run its dV, dK products, then padding to a whole round of stages) mask
+// every probability of theirs, so their P and dS are zeros.
+// Every accumulator sums the products of attn_bwd_dkdv in the same order, so
+// the results are the same bits.
+template <int D>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_bwd_dkdv_pipe(
+    const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
+    const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
+    float scale, uint16_t* __restrict__ dqkv, int hsplit, float* __restrict__ part) {
+  static_assert(D == 128, "eight 17 KB stages, one wave per SIMD");
+  constexpr int NS = D / 16, ND = D / 32;
+  constexpr int IQ = 32;               // queries per item
+  constexpr int TILE = IQ * D * 2;     // Q or dO rows of an item
+  constexpr int LDW = 64 * 4;          // one wave's copy of the item's lse (32) and rowsum (32)
+  constexpr int STAGE = 2 * TILE + 4 * LDW;
+  constexpr int NST = 8;               // stages
+  constexpr int AHEAD = NST - 1;       // iteration i loads item i + AHEAD
+  constexpr int NLD = 5;               // direct loads per wave and item: 2 Q, 2 dO, 1 lse / rowsum
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  // One array per stage: reads of a stage wait only for direct loads into it.
+  __shared__ __attribute__((aligned(1024))) uint8_t St0[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t St1[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t St2[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t St3[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t St4[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t St5[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t St6[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t St7[STAGE];
+  const int kb = blockIdx.z, g = blockIdx.x / hsplit, hs = blockIdx.x % hsplit, b = blockIdx.y;
+  const int G = Hq / Hkv;
+  const int h_lo = hs * G / hsplit, h_hi = (hs + 1) * G / hsplit;
+  const int hq0 = g * G + h_lo;
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int k0w = kb * QB + wave * 32;
+  const int kj = k0w + l32;  // this lane's key
+  const int64_t tok0 = static_cast<int64_t>(b) * S;
+  const int kcol = (Hq + g) * D, vcol = (Hq + Hkv + g) * D;
+  const float scale_log2 = scale * kLog2e;
+  const int first_q = kb * QB;
+  const int nqt = (S - first_q) / IQ;  // items per query head
+  const int n_items = (h_hi - h_lo) * nqt;
+
+  auto stage = [&](auto c) -> uint8_t* {
+    constexpr int k = decltype(c)::value % NST;
+    if constexpr (k == 0) return St0;
+    else if constexpr (k == 1) return St1;
+    else if constexpr (k == 2) return St2;
+    else if constexpr (k == 3) return St3;
+    else if constexpr (k == 4) return St4;
+    else if constexpr (k == 5) return St5;
+    else if constexpr (k == 6) return St6;
+    else return St7;
+  };
+
+  // Direct loads of item i (clamped to the last) into a stage. Q and dO rows
+  // as dma_rowtile: instruction k of this wave fills rows 16 k + 4 wave +
+  // (0..3); lane l covers row 4 wave + l / 16 (mod 16) at physical chunk
+  // l % 16, a byte offset within those rows that does not depend on k (the
+  // swizzle repeats every 16 rows), so one register per source and a uniform
+  // base. The lse and rowsum of the item's queries go to this wave's own copy.
+  constexpr int CPR = D / 8;
+  uint32_t dq_off, do_off;
+  {
+    const int sub = lane / CPR, row = 4 * wave + sub;
+    const int c = (lane % CPR) ^ swz_bits<D>(row);
+    dq_off = static_cast<uint32_t>(sub * ld * 2 + c * 16);
+    do_off = static_cast<uint32_t>(sub * ldo * 2 + c * 16);
+  }
+  const float* const ld_src = h ? dsum : lse;
+  // The item whose stage loads next, walked in item order and held at the
+  // last one: its index, its query tile within its head, the byte addresses
+  // of its first Q and dO rows (at the head's column) and the index of its
+  // first lse / rowsum value. Advanced by scalar adds, so that each iteration
+  // spends a few scalar instructions on its loads rather than the divisions
+  // and 64-bit products of computing the addresses afresh.
+  struct Cursor {
+    int i, t;
+    const char* q;
+    const char* o;
+    int64_t at;
+  };
+  const int64_t q_row = 2 * IQ * ld, o_row = 2 * IQ * ldo;                   // next tile
+  const int64_t q_head = 2 * D - (nqt - 1) * q_row, o_head = 2 * D - (nqt - 1) * o_row;  // next head
+  const int64_t at_head = S - (nqt - 1) * static_cast<int64_t>(IQ);
+  Cursor cur{0, 0,
+             reinterpret_cast<const char*>(qkv + (tok0 + first_q) * ld + static_cast<int64_t>(hq0) * D),
+             reinterpret_cast<const char*>(dout + (tok0 + first_q) * ldo + static_cast<int64_t>(hq0) * D),
+             (static_cast<int64_t>(b) * Hq + hq0) * S + first_q};
+  auto advance = [&](Cursor& c) __attribute__((always_inline)) {
+    const bool more = c.i < n_items - 1, wrap = c.t == nqt - 1;
+    c.q += more ? (wrap ? q_head : q_row) : 0;
+    c.o += more ? (wrap ? o_head : o_row) : 0;
+    c.at += more ? (wrap ? at_head : IQ) : 0;
+    c.t = more ? (wrap ? 0 : c.t + 1) : c.t;
+    c.i += more ? 1 : 0;
+  };
+  // Q rows (k = 0, 1: rows 16 k + 4 wave + 0..3), dO rows (k = 2, 3), lse / rowsum (k = 4)
+  const int64_t q_k[2] = {4 * wave * 2 * ld, (16 + 4 * wave) * 2 * ld};
+  const int64_t o_k[2] = {4 * wave * 2 * ldo, (16 + 4 * wave) * 2 * ldo};
+  auto dma = [&](const Cursor& c, uint8_t* st, int k) __attribute__((always_inline)) {
+    if (k < 4) {
+      const int rb = (4 * (k & 1) + wave) * 4;
+      const char* base = k < 2 ? c.q + q_k[k & 1] : c.o + o_k[k & 1];
+      __builtin_amdgcn_global_load_lds((const gbl_void_t*)(base + (k < 2 ? dq_off : do_off)),
+                                       (lds_void_t*)(st + (k >> 1) * TILE + rb * (2 * D)), 16, 0, 0);
+    } else {
+      __builtin_amdgcn_global_load_lds((const gbl_void_t*)(ld_src + c.at + l32),
+                                       (lds_void_t*)(st + 2 * TILE + wave * LDW), 4, 0, 0);
+    }
+  };
+
+  // Lane offsets of the operand reads, as in attn_bwd_dkdv.
+  uint32_t row_off[NS], tr_off[2][ND];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    row_off[s] = rowtile_off<D>(l32, 2 * s + h);
+    asm volatile("" : "+v"(row_off[s]));
+  }
+#pragma unroll
+  for (int hv = 0; hv < 2; ++hv)
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+      const int q = (lane >> 4) & 1, li = lane & 15;
+      tr_off[hv][dt] = rowtile_off<D>(4 * h + (li >> 2) + 8 * hv, (dt * 32 + q * 16) / 8 + ((li & 3) >> 1)) +
+                       (li & 1) * 8;
+      asm volatile("" : "+v"(tr_off[hv][dt]));
+    }
+  auto rd_row = [&](const uint8_t* t, int s) -> bf16x8 {
+    return *(const lds_bf16x8_t*)((lds_cptr)t + row_off[s]);
+  };
+  auto rd_tr = [&](const uint8_t* t, int dt, int s) -> bf16x8 {
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((lds_cptr)t + tr_off[0][dt] + s * 16 * (2 * D)));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((lds_cptr)t + tr_off[1][dt] + s * 16 * (2 * D)));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+
+  // prologue: K, V fragments; items 0 .. AHEAD - 1 to stages 0 .. AHEAD - 1;
+  // item -1's stage (NST - 1) zeroed
+  bf16x8 kf[NS], vf[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    kf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + kj) * ld + kcol + s * 16 + h * 8);
+    vf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + kj) * ld + vcol + s * 16 + h * 8);
+  }
+  // The prologue's loads stay in stage order (the waits below count them).
+  __builtin_amdgcn_sched_barrier(0);
+  // A direct load into the last stage's lse / rowsum copy first (item 0's:
+  // never read), so that the compiler meets every stage's loads before the
+  // loop; its waits for them then stay exact inside it.
+  dma(cur, St7, NLD - 1);
+  __builtin_amdgcn_sched_barrier(0);
+  auto pro_load = [&](auto jc) __attribute__((always_inline)) {
+    constexpr int j = decltype(jc)::value;
+#pragma unroll
+    for (int k = 0; k < NLD; ++k) dma(cur, stage(Ic<j>{}), k);
+    advance(cur);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  StaticFor<0, AHEAD>::run(pro_load);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int c = threadIdx.x; c < 2 * TILE / 16; c += kThreads)
+    reinterpret_cast<u32x4_t*>(St7)[c] = u32x4_t{0u, 0u, 0u, 0u};
+  f32x16 dk[ND], dv[ND];
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt) {
+    dk[dt] = f32x16{};
+    dv[dt] = f32x16{};
+  }
+  f32x16 sf[2], df[2];  // S^T and dP^T of an item: [set]
+  // item 0 landed (the later stages may be in flight), the zeros written
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(NLD * (AHEAD - 1) + 1));
+  __builtin_amdgcn_s_barrier();
+  // S^T, dP^T of item 0 (set 0)
+  sf[0] = f32x16{};
+  df[0] = f32x16{};
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    sf[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rd_row(St0, s), kf[s], sf[0], 0, 0, 0);
+    df[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rd_row(St0 + TILE, s), vf[s], df[0], 0, 0, 0);
+  }
+  // Operand reads run two groups ahead of their MFMAs (a ring of three):
+  // one group (about 64 cycles) is shorter than an LDS read's latency with
+  // four waves reading.
+  bf16x8 ta[3], tb[3];   // dO^T and Q^T operands of phase A
+  bf16x8 qa[3], oa[3];   // Q and dO row operands of phase B
+  f32x4 lq4[2], dq4[2];  // lse (log2 domain) and rowsum of four queries, ahead of use
+  ta[0] = rd_tr(St7 + TILE, 0, 0);
+  tb[0] = rd_tr(St7, 0, 0);
+  ta[1] = rd_tr(St7 + TILE, 1, 0);
+  tb[1] = rd_tr(St7, 1, 0);
+  const int lim0 = kj - 4 * h;
+
+  // Item i's arithmetic as a three-stage pipeline over the iteration's 16
+  // MFMA groups G (phase A: G = 0..7, phase B: G = 8..15): value v goes
+  // through stage 1 (S scaled, minus lse) in group v + 2, stage 2 (exp2, dP
+  // minus rowsum) in v + 3 and stage 3 (causal mask, dS, and with its odd
+  // neighbour the bf16 pair) in v + 4; the last values finish in the next
+  // iteration's first groups, ahead of the phase A products that read them.
+  // Each group then runs three short independent chains (a dependent VALU
+  // step waits about 8 cycles on the one before).
+  // P and dS as bf16 operands, packed pairs: [set][k16 step of the item][pair]
+  uint32_t pw[2][2][4], dw[2][2][4];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pw[1][kk][w] = dw[1][kk][w] = 0u;  // item -1
+  // (zeros before item 0: item -1's values finish in iteration 0 as zeros)
+  float xs[16], es[16], ts[16], ps[16], dss[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) xs[v] = es[v] = ts[v] = ps[v] = dss[v] = 0.0f;
+  int lim_p = 0x7fffffff;  // item -1: every value masked (its P, dS are zeros)
+  int tc = 0;              // item i's query tile within its head
+  sf[1] = f32x16{};
+  df[1] = f32x16{};
+  lq4[0] = lq4[1] = dq4[0] = dq4[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  auto pack = [](float a, float b) -> uint32_t {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(mr_f32x2{a, b}, bf16x2_t));
+  };
+  auto st1 = [&](auto setc, auto vc) __attribute__((always_inline)) {
+    constexpr int set = decltype(setc)::value, v = decltype(vc)::value;
+    xs[v] = __builtin_fmaf(sf[set][v], scale_log2, -lq4[(v >> 2) & 1][v & 3]);
+    asm volatile("" : "+v"(xs[v]));  // computed here, not sunk to its use
+  };
+  auto st2 = [&](auto setc, auto vc) __attribute__((always_inline)) {
+    constexpr int set = decltype(setc)::value, v = decltype(vc)::value;
+    es[v] = __builtin_amdgcn_exp2f(xs[v]);
+    ts[v] = df[set][v] - dq4[(v >> 2) & 1][v & 3];
+    asm volatile("" : "+v"(es[v]), "+v"(ts[v]));
+  };
+  auto st3 = [&](auto setc, auto vc, int lim) __attribute__((always_inline)) {
+    constexpr int set = decltype(setc)::value, v = decltype(vc)::value;
+    ps[v] = lim > 8 * (v >> 2) + (v & 3) ? 0.0f : es[v];
+    dss[v] = ps[v] * ts[v];
+    if constexpr (v & 1) {
+      pw[set][v >> 3][(v & 7) >> 1] = pack(ps[v - 1], ps[v]);
+      dw[set][v >> 3][(v & 7) >> 1] = pack(dss[v - 1], dss[v]);
+      asm volatile("" : "+v"(pw[set][v >> 3][(v & 7) >> 1]), "+v"(dw[set][v >> 3][(v & 7) >> 1]));
+    }
+  };
+  auto opnd = [](const uint32_t (&w)[4]) -> bf16x8 {
+    return __builtin_bit_cast(bf16x8, u32x4_t{w[0], w[1], w[2], w[3]});
+  };
+
+  auto iter = [&](auto pc, int i) __attribute__((always_inline)) {
+    constexpr int P = decltype(pc)::value;
+    constexpr int C = P & 1, N = C ^ 1;  // sets of item i and of items i +- 1
+    uint8_t* const Sp = stage(Ic<P + NST - 1>{});  // item i - 1; after the barrier, item i + AHEAD's loads
+    uint8_t* const Sc = stage(Ic<P>{});             // item i
+    uint8_t* const Sn = stage(Ic<P + 1>{});         // item i + 1
+    const lds_cptr LDc = (lds_cptr)Sc + 2 * TILE + wave * LDW;
+    // Value v of item i is masked iff key kj > query qt0 + acc_row(v, h),
+    // i.e. iff lim > 8 (v / 4) + v % 4; every value of the padding items past
+    // the last, so that their P and dS are zeros.
+    // (branch-free: a branch here splits the loop body, and the compiler then
+    // copies the accumulator sets between register files at the join)
+    const int lim_c = lim0 - first_q - tc * IQ + (((n_items - 1 - i) >> 31) & (1 << 30));
+
+    auto ldrd = [&](auto gqc) __attribute__((always_inline)) {  // queries 8 gq + 4 h + 0..3
+      constexpr int gq = decltype(gqc)::value;
+      typedef __attribute__((address_space(3))) f32x4 lds_f32x4_t;
+      const lds_cptr l4 = LDc + (gq * 8 + 4 * h) * 4;
+      lq4[gq & 1] = *(const lds_f32x4_t*)l4 * kLog2e;
+      dq4[gq & 1] = *(const lds_f32x4_t*)(l4 + 32 * 4);
+      asm volatile("" : "+v"(lq4[gq & 1]));
+    };
+    // the arithmetic of group G (see above)
+    auto arith = [&](auto gc) __attribute__((always_inline)) {
+      constexpr int G = decltype(gc)::value;
+      if constexpr (G % 4 == 0) ldrd(Ic<G / 4>{});
+      if constexpr (G >= 4) st3(Ic<C>{}, Ic<G - 4>{}, lim_c);
+      else st3(Ic<N>{}, Ic<G + 12>{}, lim_p);
+      if constexpr (G >= 3) st2(Ic<C>{}, Ic<G - 3>{});
+      else st2(Ic<N>{}, Ic<G + 13>{});
+      if constexpr (G >= 2) st1(Ic<C>{}, Ic<G - 2>{});
+      else st1(Ic<N>{}, Ic<G + 14>{});
+    };
+    // phase A, group x: k16 step kk = x / ND of item i - 1, d tile dt = x % ND
+    auto ga = [&](auto xc) __attribute__((always_inline)) {
+      constexpr int x = decltype(xc)::value, kk = x / ND, dt = x % ND;
+      if constexpr (x + 2 < 2 * ND) {
+        ta[(x + 2) % 3] = rd_tr(Sp + TILE, (x + 2) % ND, (x + 2) / ND);
+        tb[(x + 2) % 3] = rd_tr(Sp, (x + 2) % ND, (x + 2) / ND);
+      }
+      dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opnd(pw[N][kk]), ta[x % 3], dv[dt], 0, 0, 0);
+      dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(opnd(dw[N][kk]), tb[x % 3], dk[dt], 0, 0, 0);
+      arith(Ic<x>{});
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    StaticFor<0, 2 * ND - 2>::run(ga);
+    // item i + 1's stage landed (this wave's loads, then everyone's); every
+    // wave is past its reads of item i - 1's stage
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(NLD * (AHEAD - 2)));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    qa[0] = rd_row(Sn, 0);
+    oa[0] = rd_row(Sn + TILE, 0);
+    qa[1] = rd_row(Sn, 1);
+    oa[1] = rd_row(Sn + TILE, 1);
+    ga(Ic<2 * ND - 2>{});
+    ga(Ic<2 * ND - 1>{});
+    // phase B, group x: k16 step s = x of item i + 1
+    auto gb = [&](auto xc) __attribute__((always_inline)) {
+      constexpr int x = decltype(xc)::value;
+      if constexpr (x + 2 < NS) {
+        qa[(x + 2) % 3] = rd_row(Sn, x + 2);
+        oa[(x + 2) % 3] = rd_row(Sn + TILE, x + 2);
+      } else {  // the next iteration's first phase A operands: item i's stage
+        ta[x - (NS - 2)] = rd_tr(Sc + TILE, x - (NS - 2), 0);
+        tb[x - (NS - 2)] = rd_tr(Sc, x - (NS - 2), 0);
+      }
+      if constexpr (x == 1) dma(cur, Sp, 0);
+      if constexpr (x == 2) dma(cur, Sp, 2);
+      if constexpr (x == 3) dma(cur, Sp, 1);
+      if constexpr (x == 5) dma(cur, Sp, 3);
+      if constexpr (x == 6) dma(cur, Sp, 4);
+      sf[N] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa[x % 3], kf[x], x == 0 ? f32x16{} : sf[N], 0, 0, 0);
+      df[N] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(oa[x % 3], vf[x], x == 0 ? f32x16{} : df[N], 0, 0, 0);
+      arith(Ic<2 * ND + x>{});
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    StaticFor<0, NS>::run(gb);
+    lim_p = lim_c;
+    advance(cur);
+    tc = tc == nqt - 1 ? 0 : tc + 1;
+  };
+
+  // Whole rounds of NST iterations (compile-time stages): n_items + 1
+  // iterations and up to NST - 1 padding ones, whose items add zeros.
+  const int n_it = (n_items + NST) / NST * NST;
+  for (int i = 0; i < n_it; i += NST) {
+    iter(Ic<0>{}, i);
+    iter(Ic<1>{}, i + 1);
+    iter(Ic<2>{}, i + 2);
+    iter(Ic<3>{}, i + 3);
+    iter(Ic<4>{}, i + 4);
+    iter(Ic<5>{}, i + 5);
+    iter(Ic<6>{}, i + 6);
+    iter(Ic<7>{}, i + 7);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the last (repeated) direct loads
+
+  // dk, dv [dt][r]: key k0w + acc_row(r, h), d = dt * 32 + l32, to the
+  // partials ([split][token][k heads | v heads][d]) or as bf16 into dqkv.
+  if (part) {
+    const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
+    float* pbase = part + static_cast<int64_t>(hs) * gridDim.y * S * W;
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = tok0 + k0w + acc_row(r, h);
+        pbase[row * W + g * D + dt * 32 + l32] = dk[dt][r] * scale;
+        pbase[row * W + (Hkv + g) * D + dt * 32 + l32] = dv[dt][r];
+      }
+    return;
+  }
+#pragma unroll
+  for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = tok0 + k0w + acc_row(r, h);
+      dqkv[row * ld + kcol + dt * 32 + l32] = f32_to_bf16(dk[dt][r] * scale);
+      dqkv[row * ld + vcol + dt * 32 + l32] = f32_to_bf16(dv[dt][r]);
+    }
+}
+
 // dK, dV of head-split blocks: the sum of the partials in split order, as
 // bf16 into the k and v columns of dqkv. One thread per 4 consecutive values.
 __global__ __launch_bounds__(kThreads) void attn_bwd_kv_reduce(const float* __restrict__ part,
@@ -1038,6 +1442,14 @@ int auto_hsplit(int B, int S, int Hq, int Hkv, int D, int64_t cap) {
   return hsplit;
 }
 
+// MR_ATTN_PAIR=1 in the environment runs dK, dV at D = 128 on
+// attn_bwd_dkdv_pair instead of attn_bwd_dkdv_pipe (read at every launch;
+// the two give the same bits, which the tests check).
+bool use_pair_kernel() {
+  const char* e = getenv("MR_ATTN_PAIR");
+  return e && e[0] == '1';
+}
+
 template <int D>
 int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint16_t* dout,
                int64_t ldo, const float* lse, float* dsum, int B, int S, int Hq, int Hkv,
@@ -1048,10 +1460,14 @@ int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint1
                      dim3(kThreads), 0, s, dout, out, ldo, T, S, Hq, dsum);
   const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
   if (hsplit == 1) part = nullptr;
-  if constexpr (D == 128)
-    hipLaunchKernelGGL(attn_bwd_dkdv_pair<D>, dim3(Hkv * hsplit, B, S / QB), dim3(2 * kThreads), 0, s, qkv,
-                       ld, dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
-  else
+  if constexpr (D == 128) {
+    if (use_pair_kernel())
+      hipLaunchKernelGGL(attn_bwd_dkdv_pair<D>, dim3(Hkv * hsplit, B, S / QB), dim3(2 * kThreads), 0, s, qkv,
+                         ld, dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
+    else
+      hipLaunchKernelGGL(attn_bwd_dkdv_pipe<D>, dim3(Hkv * hsplit, B, S / QB), dim3(kThreads), 0, s, qkv,
+                         ld, dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
+  } else
     hipLaunchKernelGGL(attn_bwd_dkdv<D>, dim3(Hkv * hsplit, B, S / QB), dim3(kThreads), 0, s, qkv, ld,
                        dout, ldo, lse, dsum, S, Hq, Hkv, scale, dqkv, hsplit, part);
   if (part) {

@@ -9,6 +9,7 @@ magnitudes. Gradients are checked against float64 autograd.
 from __future__ import annotations
 
 import math
+import os
 import sys
 
 import pytest
@@ -180,6 +181,40 @@ def test_attention_backward_head_split(case):
     got = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=hsplit).double().cpu()
     assert torch.all(got[:, width:] == 3.0), "padding columns were written"
     _check_attention_backward(qkv, dout, got[:, :width], B, S, Hq, Hkv, D, 1.0 / math.sqrt(D))
+
+
+class _PairKernel:
+    """Every dK/dV launch at D = 128 inside the block runs on the two-waves-per-SIMD pair kernel."""
+
+    def __enter__(self):
+        os.environ["MR_ATTN_PAIR"] = "1"
+
+    def __exit__(self, *exc):
+        del os.environ["MR_ATTN_PAIR"]
+
+
+# The pipelined dK/dV kernel (D = 128) against the pair kernel, bit for bit:
+# both sum the same products in the same order. Item counts (32-query tiles
+# times query heads per block) end at both positions of its 8-stage round
+# (n mod 8 = 0, 4), with one and several heads per block, bf16 written
+# directly and fp32 partials (hsplit > 1), and the 7B launch.
+PIPE_CASES = [
+    # B, S, Hq, Hkv, D, hsplit
+    (1, 128, 2, 1, 128, 1), (1, 128, 3, 3, 128, 1), (2, 384, 14, 2, 128, 1), (2, 384, 14, 2, 128, 2),
+    (1, 256, 8, 1, 128, 3), (1, 256, 8, 1, 128, 8), (8, 2048, 28, 4, 128, 0),
+]
+
+
+@pytest.mark.parametrize("case", PIPE_CASES)
+def test_attention_dkdv_pipeline_matches_pair(case):
+    B, S, Hq, Hkv, D, hsplit = case
+    print("case attn bwd pipe vs pair", case, flush=True, file=sys.stderr)
+    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, 1.5, seed=30, pad=16)
+    dout = torch.randn(B * S, Hq * D, generator=_gen(31)).to(torch.bfloat16)
+    got = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=hsplit)
+    with _PairKernel():
+        ref = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=hsplit)
+    assert torch.equal(got, ref), "pipelined and pair dK/dV kernels differ"
 
 
 def test_attention_head_splits_agree():

@@ -309,24 +309,31 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
       // uniform bases of the slice; lane offsets stay 32-bit (ld < 2^22, 32 rows)
       uint16_t* const act_s = act + static_cast<int64_t>(row0) * p.ldc;
       uint16_t* const gu_s = p.gu + static_cast<int64_t>(row0) * p.ldgu;
+      // (a slice wholly inside the outputs stores without per-lane guards,
+      // as in the plain epilogue)
+      auto out = [&](auto guardc) __attribute__((always_inline)) {
+        constexpr bool GUARD = decltype(guardc)::value;
 #pragma unroll
-      for (int it = 0; it < 32 * CA / 64; ++it) {
-        const int idx = it * 64 + lane, r = idx / CA, ch = idx % CA;
-        const u32x4 v = *(lds_u32x4*)(sa + r * PA + ch * 16);
-        const int col = (n0 + wn * WN) / 2 + ch * 8;
-        if (row0 + r < p.M && col < p.n_out)
-          *reinterpret_cast<u32x4*>(act_s + static_cast<uint32_t>(r * static_cast<int>(p.ldc) + col)) = v;
-      }
-      if (p.gu) {
-#pragma unroll
-        for (int it = 0; it < 32 * CG / 64; ++it) {
-          const int idx = it * 64 + lane, r = idx / CG, ch = idx % CG;
-          const u32x4 v = *(lds_u32x4*)(sg + r * PG + ch * 16);
-          const int col = n0 + wn * WN + ch * 8;
-          if (row0 + r < p.M && col < 2 * p.n_out)
-            *reinterpret_cast<u32x4*>(gu_s + static_cast<uint32_t>(r * static_cast<int>(p.ldgu) + col)) = v;
+        for (int it = 0; it < 32 * CA / 64; ++it) {
+          const int idx = it * 64 + lane, r = idx / CA, ch = idx % CA;
+          const u32x4 v = *(lds_u32x4*)(sa + r * PA + ch * 16);
+          const int col = (n0 + wn * WN) / 2 + ch * 8;
+          if (!GUARD || (row0 + r < p.M && col < p.n_out))
+            *reinterpret_cast<u32x4*>(act_s + static_cast<uint32_t>(r * static_cast<int>(p.ldc) + col)) = v;
         }
-      }
+        if (p.gu) {
+#pragma unroll
+          for (int it = 0; it < 32 * CG / 64; ++it) {
+            const int idx = it * 64 + lane, r = idx / CG, ch = idx % CG;
+            const u32x4 v = *(lds_u32x4*)(sg + r * PG + ch * 16);
+            const int col = n0 + wn * WN + ch * 8;
+            if (!GUARD || (row0 + r < p.M && col < 2 * p.n_out))
+              *reinterpret_cast<u32x4*>(gu_s + static_cast<uint32_t>(r * static_cast<int>(p.ldgu) + col)) = v;
+          }
+        }
+      };
+      if (row0 + 32 <= p.M && (n0 + wn * WN) / 2 + WN / 2 <= p.n_out) out(std::false_type{});
+      else out(std::true_type{});
     }
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
     // acc is dact transposed (SWAP): lane l holds row l % 32 of block (i, j)
@@ -377,6 +384,8 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
           gv[it] = *reinterpret_cast<const u32x4*>(gu_s + o);
           uv[it] = *reinterpret_cast<const u32x4*>(gu_s + o + 32);
         }
+        auto out = [&](auto guardc) __attribute__((always_inline)) {  // (guards as in the plain epilogue)
+          constexpr bool GUARD = decltype(guardc)::value;
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
           const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
@@ -395,7 +404,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
             dg[e] = da[e] * u * dsilu;
             du[e] = da[e] * g * sg;
           }
-          if (row < p.M && col < p.N) {
+          if (!GUARD || (row < p.M && col < p.N)) {
             const uint32_t od = static_cast<uint32_t>(r * static_cast<int>(p.ldc) + (col >> 5) * 64 + (col & 31));
             *reinterpret_cast<u32x4*>(dgu_s + od) = u32x4{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]),
                                                         pack_bf16x2(dg[4], dg[5]), pack_bf16x2(dg[6], dg[7])};
@@ -403,6 +412,9 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
                                                              pack_bf16x2(du[4], du[5]), pack_bf16x2(du[6], du[7])};
           }
         }
+        };
+        if (row0 + 32 <= p.M && col0 + JH * 32 <= p.N) out(std::false_type{});
+        else out(std::true_type{});
       }
     }
   } else {  // EPI_STORE, EPI_RESID
@@ -477,23 +489,31 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
             res[it] = *reinterpret_cast<const f32x4*>(rs + ((row - row0) * static_cast<int>(p.ldr) + col));
           }
         }
+        // A slice wholly inside the output stores without per-lane guards:
+        // guarded stores each become a branch region of their own, and the
+        // LDS reads then wait one by one instead of being in flight together.
+        auto out = [&](auto guardc) __attribute__((always_inline)) {
+          constexpr bool GUARD = decltype(guardc)::value;
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-          const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
-          const int row = row0 + r, col = col0 + ch * (16 / OBY);
-          const uint32_t oc = static_cast<uint32_t>(r * static_cast<int>(p.ldc) + ch * (16 / OBY));
-          if (row < p.M && col < p.N) {
-            if constexpr (OUT_BF16) {
-              typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-              const u32x4 w = *(__attribute__((address_space(3))) u32x4*)(st + r * PITCH + ch * 16);
-              *reinterpret_cast<u32x4*>(cb16 + oc) = w;
-            } else {
-              f32x4 w = *(__attribute__((address_space(3))) f32x4*)(st + r * PITCH + ch * 16);
-              if constexpr (EPI == EPI_RESID) w = res[it] + w;
-              *reinterpret_cast<f32x4*>(cb32 + oc) = w;
+          for (int it = 0; it < NIT; ++it) {
+            const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
+            const int row = row0 + r, col = col0 + ch * (16 / OBY);
+            const uint32_t oc = static_cast<uint32_t>(r * static_cast<int>(p.ldc) + ch * (16 / OBY));
+            if (!GUARD || (row < p.M && col < p.N)) {
+              if constexpr (OUT_BF16) {
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 w = *(__attribute__((address_space(3))) u32x4*)(st + r * PITCH + ch * 16);
+                *reinterpret_cast<u32x4*>(cb16 + oc) = w;
+              } else {
+                f32x4 w = *(__attribute__((address_space(3))) f32x4*)(st + r * PITCH + ch * 16);
+                if constexpr (EPI == EPI_RESID) w = res[it] + w;
+                *reinterpret_cast<f32x4*>(cb32 + oc) = w;
+              }
             }
           }
-        }
+        };
+        if (row0 + 32 <= p.M && col0 + JH * 32 <= p.N) out(std::false_type{});
+        else out(std::true_type{});
       }
     }
   }

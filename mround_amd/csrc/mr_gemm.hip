@@ -260,80 +260,89 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
     // B rows interleave 32 gate rows and 32 up rows, and a wave's column
     // range starts on a multiple of 64: block j = 2q holds gate columns and
     // j = 2q + 1 the up columns of the same 32 act columns (accumulators are
-    // transposed, see SWAP). Each 32-row slice of the wave's act and gate/up
-    // outputs is staged in a private LDS region (the k loop's stages are free
-    // after its last barrier) and leaves in whole 16-byte row pieces: the
-    // stores then cover full cache lines instead of 64-byte row pieces.
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    // transposed, see SWAP). Each 32-row slice of the wave's accumulators (JH
+    // column blocks at a time, gate and up pairs whole) is staged as fp32 in
+    // the wave's LDS share; then a lane takes 8 consecutive act columns of one
+    // row, reads their gate and up values, and writes act and the bf16 gate
+    // and up copies as one 16-byte store each: whole cache lines instead of
+    // 64-byte row pieces. (Computing act while staging made the compiler read
+    // the accumulators out of the AGPRs ahead of the silu chains and spill.)
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
-    typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
-    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-    auto pack4 = [](float a, float b, float c, float d) {
-      u32x2 v;
-      v.x = pack_bf16x2(a, b);
-      v.y = pack_bf16x2(c, d);
-      return v;
-    };
-    // Row pitches of the staged act (WN / 2 columns) and gate/up (WN columns)
-    // slices: 16 bytes of padding put the 8-byte writes of rows r and r + 16
-    // in different banks only two ways apart, and keep rows 16-byte aligned.
-    constexpr int PA = WN + 16, PG = 2 * WN + 16;
-    static_assert(32 * (PA + PG) <= REGION, "SwiGLU staging does not fit the wave's LDS share");
-    lds_u8* sa = (lds_u8*)region;
-    lds_u8* sg = sa + 32 * PA;
+    typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+    // Rows are not padded (32 rows of two blocks fill the 8-wave 128 x 128
+    // kernel's 8 KB share); instead the 16-byte chunk c of row r sits at
+    // chunk c ^ (r % 16), which spreads a write's 32 rows over all banks.
+    constexpr int JH = (32 * TN * 32 * 4 <= REGION) ? TN : 2;
+    constexpr int PITCH = JH * 32 * 4;
+    constexpr int CH = JH * 16 / 8;  // 8-column act pieces per staged row
+    constexpr int NIT = 32 * CH / 64;
+    static_assert(32 * PITCH <= REGION && TN % JH == 0 && JH % 2 == 0 && NIT * 64 == 32 * CH,
+                  "SwiGLU staging does not fit the wave's LDS share");
+    auto at = [](int r, int c) __attribute__((always_inline)) { return r * PITCH + ((c ^ (r & 15)) << 4); };
+    lds_u8* st = (lds_u8*)region;
     uint16_t* act = static_cast<uint16_t*>(p.C);
-    constexpr int CA = WN / 16, CG = 2 * WN / 16;  // 16-byte pieces per staged row
+    const bool has_gu = p.gu != nullptr;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
-      for (int q = 0; q < TN / 2; ++q) {
-        const f32x16 gt = acc[i][2 * q];
-        const f32x16 ut = acc[i][2 * q + 1];
+      for (int jb = 0; jb < TN / JH; ++jb) {
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          float a[4];
+        for (int jj = 0; jj < JH; ++jj) {
+          const int j = jb * JH + jj;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) a[e] = silu(gt[gi * 4 + e]) * ut[gi * 4 + e];
-          const int c = gi * 8 + lrow;
-          *(lds_u32x2*)(sa + lcol * PA + (q * 32 + c) * 2) = pack4(a[0], a[1], a[2], a[3]);
-          *(lds_u32x2*)(sg + lcol * PG + (2 * q * 32 + c) * 2) =
-              pack4(gt[gi * 4], gt[gi * 4 + 1], gt[gi * 4 + 2], gt[gi * 4 + 3]);
-          *(lds_u32x2*)(sg + lcol * PG + (2 * q * 32 + 32 + c) * 2) =
-              pack4(ut[gi * 4], ut[gi * 4 + 1], ut[gi * 4 + 2], ut[gi * 4 + 3]);
+          for (int gi = 0; gi < 4; ++gi)
+            *(lds_f32x4*)(st + at(lcol, jj * 8 + gi * 2 + lrow / 4)) =
+                f32x4{acc[i][j][4 * gi], acc[i][j][4 * gi + 1], acc[i][j][4 * gi + 2], acc[i][j][4 * gi + 3]};
+        }
+        // The same wave reads back what it wrote (LDS keeps a wave's accesses
+        // in order), then the next slice overwrites the region.
+        const int row0 = m0 + wm * WM + i * 32;
+        const int col0 = n0 + wn * WN + jb * JH * 32;  // gate/up column, a multiple of 64
+        // uniform bases of the slice; lane offsets stay 32-bit (ld < 2^22, 32 rows)
+        uint16_t* const act_s = act + static_cast<int64_t>(row0) * p.ldc + col0 / 2;
+        uint16_t* const gu_s = p.gu + static_cast<int64_t>(row0) * p.ldgu + col0;
+        // (a slice wholly inside the outputs stores without per-lane guards,
+        // as in the plain epilogue; N is a multiple of 32, so an act piece and
+        // its gate and up pieces lie inside or past the edge together)
+        auto out = [&](auto guardc, auto guc) __attribute__((always_inline)) {
+          constexpr bool GUARD = decltype(guardc)::value, GU = decltype(guc)::value;
+#pragma unroll
+          for (int it = 0; it < NIT; ++it) {
+            const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
+            const int gc = (ch >> 2) * 64 + (ch & 3) * 8;  // staged gate column; up 32 further
+            const f32x4 g0 = *(const lds_f32x4*)(st + at(r, gc / 4)), g1 = *(const lds_f32x4*)(st + at(r, gc / 4 + 1));
+            const f32x4 u0 = *(const lds_f32x4*)(st + at(r, gc / 4 + 8)), u1 = *(const lds_f32x4*)(st + at(r, gc / 4 + 9));
+            if (!GUARD || (row0 + r < p.M && col0 / 2 + ch * 8 < p.n_out)) {
+              float a[8];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                a[e] = silu(g0[e]) * u0[e];
+                a[e + 4] = silu(g1[e]) * u1[e];
+              }
+              *reinterpret_cast<u32x4*>(act_s + static_cast<uint32_t>(r * static_cast<int>(p.ldc) + ch * 8)) =
+                  u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(a[4], a[5]),
+                        pack_bf16x2(a[6], a[7])};
+              if constexpr (GU) {
+                uint16_t* const o = gu_s + static_cast<uint32_t>(r * static_cast<int>(p.ldgu) + gc);
+                *reinterpret_cast<u32x4*>(o) = u32x4{pack_bf16x2(g0[0], g0[1]), pack_bf16x2(g0[2], g0[3]),
+                                                     pack_bf16x2(g1[0], g1[1]), pack_bf16x2(g1[2], g1[3])};
+                *reinterpret_cast<u32x4*>(o + 32) = u32x4{pack_bf16x2(u0[0], u0[1]), pack_bf16x2(u0[2], u0[3]),
+                                                          pack_bf16x2(u1[0], u1[1]), pack_bf16x2(u1[2], u1[3])};
+              }
+            }
+          }
+        };
+        const bool full = row0 + 32 <= p.M && col0 / 2 + JH * 16 <= p.n_out;
+        if (has_gu) {
+          if (full) out(std::false_type{}, std::true_type{});
+          else out(std::true_type{}, std::true_type{});
+        } else {
+          if (full) out(std::false_type{}, std::false_type{});
+          else out(std::true_type{}, std::false_type{});
         }
       }
-      // The same wave reads back what it wrote (LDS keeps a wave's accesses
-      // in order), then the next slice overwrites the region.
-      const int row0 = m0 + wm * WM + i * 32;
-      // uniform bases of the slice; lane offsets stay 32-bit (ld < 2^22, 32 rows)
-      uint16_t* const act_s = act + static_cast<int64_t>(row0) * p.ldc;
-      uint16_t* const gu_s = p.gu + static_cast<int64_t>(row0) * p.ldgu;
-      // (a slice wholly inside the outputs stores without per-lane guards,
-      // as in the plain epilogue)
-      auto out = [&](auto guardc) __attribute__((always_inline)) {
-        constexpr bool GUARD = decltype(guardc)::value;
-#pragma unroll
-        for (int it = 0; it < 32 * CA / 64; ++it) {
-          const int idx = it * 64 + lane, r = idx / CA, ch = idx % CA;
-          const u32x4 v = *(lds_u32x4*)(sa + r * PA + ch * 16);
-          const int col = (n0 + wn * WN) / 2 + ch * 8;
-          if (!GUARD || (row0 + r < p.M && col < p.n_out))
-            *reinterpret_cast<u32x4*>(act_s + static_cast<uint32_t>(r * static_cast<int>(p.ldc) + col)) = v;
-        }
-        if (p.gu) {
-#pragma unroll
-          for (int it = 0; it < 32 * CG / 64; ++it) {
-            const int idx = it * 64 + lane, r = idx / CG, ch = idx % CG;
-            const u32x4 v = *(lds_u32x4*)(sg + r * PG + ch * 16);
-            const int col = n0 + wn * WN + ch * 8;
-            if (!GUARD || (row0 + r < p.M && col < 2 * p.n_out))
-              *reinterpret_cast<u32x4*>(gu_s + static_cast<uint32_t>(r * static_cast<int>(p.ldgu) + col)) = v;
-          }
-        }
-      };
-      if (row0 + 32 <= p.M && (n0 + wn * WN) / 2 + WN / 2 <= p.n_out) out(std::false_type{});
-      else out(std::true_type{});
     }
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
     // acc is dact transposed (SWAP): lane l holds row l % 32 of block (i, j)
@@ -418,64 +427,44 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
       }
     }
   } else {  // EPI_STORE, EPI_RESID
-    // The transposed accumulators (plus bias) are staged per 32-row slice and
-    // JH column blocks in the wave's LDS share, then leave as 16-byte row
-    // pieces (the residual added on the way): whole cache lines instead of
-    // 64-byte (bf16) row pieces, and a quarter of the store instructions.
-    // Measured on the 7B block: q/k/v projection 9 %, attention-output input
-    // gradient 10 %, fp32 outputs 1-4 % faster.
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    // The transposed accumulators are staged in fp32 per 32-row slice and JH
+    // column blocks in the wave's LDS share, then leave as 16-byte row pieces
+    // (bias, residual and the bf16 rounding applied on the way): whole cache
+    // lines instead of 64-byte (bf16) row pieces, and a quarter of the store
+    // instructions. Measured on the 7B block: q/k/v projection 9 %,
+    // attention-output input gradient 10 %, fp32 outputs 1-4 % faster. (With
+    // the bias added while staging, its branch made the compiler read every
+    // accumulator out of the AGPRs ahead of it, 256 values, and spill.)
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
-    constexpr int OBY = OUT_BF16 ? 2 : 4;
-    constexpr int JH = (32 * (TN * 32 * OBY + 16) <= REGION) ? TN : (32 * (2 * 32 * OBY + 16) <= REGION ? 2 : 1);
-    constexpr int PITCH = JH * 32 * OBY + 16;
-    constexpr int CH = JH * 32 * OBY / 16;  // 16-byte pieces per staged row
-    static_assert(32 * PITCH <= REGION && TN % JH == 0, "staging does not fit");
+    typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+    constexpr int JH = (32 * (TN * 32 * 4 + 16) <= REGION) ? TN : (32 * (2 * 32 * 4 + 16) <= REGION ? 2 : 1);
+    constexpr int PITCH = JH * 32 * 4 + 16;
+    constexpr int OPC = OUT_BF16 ? 8 : 4;   // output columns per 16-byte store
+    constexpr int CH = JH * 32 / OPC;       // stores per staged row
+    constexpr int NIT = 32 * CH / 64;
+    static_assert(32 * PITCH <= REGION && TN % JH == 0 && NIT * 64 == 32 * CH, "staging does not fit");
+    static_assert(EPI == EPI_STORE || !OUT_BF16, "the residual epilogue writes fp32");
     lds_u8* st = (lds_u8*)region;
     const bool has_bias = p.bias != nullptr;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int jb = 0; jb < TN / JH; ++jb) {
-        // the slice's accumulators (plus the bias: one uniform branch, two copies) into LDS
-        auto stage = [&](auto biasc) __attribute__((always_inline)) {
-          constexpr bool BIAS = decltype(biasc)::value;
 #pragma unroll
-          for (int jj = 0; jj < JH; ++jj) {
-            const int j = jb * JH + jj;
+        for (int jj = 0; jj < JH; ++jj) {
+          const int j = jb * JH + jj;
 #pragma unroll
-            for (int gi = 0; gi < 4; ++gi) {
-              float v[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * gi + e];
-              if constexpr (BIAS) {
-                // N is a multiple of 8: a group of 4 columns lies wholly inside or past the edge
-                const int col = min(n0 + wn * WN + j * 32 + gi * 8 + lrow, p.N - 4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] += p.bias[col + e];
-              }
-              lds_u8* at = st + lcol * PITCH + (jj * 32 + gi * 8 + lrow) * OBY;
-              if constexpr (OUT_BF16) {
-                u32x2 w;
-                w.x = pack_bf16x2(v[0], v[1]);
-                w.y = pack_bf16x2(v[2], v[3]);
-                *(__attribute__((address_space(3))) u32x2*)at = w;
-              } else {
-                *(__attribute__((address_space(3))) f32x4*)at = f32x4{v[0], v[1], v[2], v[3]};
-              }
-            }
-          }
-        };
-        if (has_bias) stage(std::true_type{});
-        else stage(std::false_type{});
+          for (int gi = 0; gi < 4; ++gi)
+            *(lds_f32x4*)(st + lcol * PITCH + (jj * 32 + gi * 8 + lrow) * 4) =
+                f32x4{acc[i][j][4 * gi], acc[i][j][4 * gi + 1], acc[i][j][4 * gi + 2], acc[i][j][4 * gi + 3]};
+        }
         const int row0 = m0 + wm * WM + i * 32;
         const int col0 = n0 + wn * WN + jb * JH * 32;
         // uniform bases of the slice; lane offsets stay 32-bit (ld < 2^22, 32 rows)
         const int64_t cbase = static_cast<int64_t>(row0) * p.ldc + col0;
         uint16_t* const cb16 = static_cast<uint16_t*>(p.C) + cbase;
         float* const cb32 = static_cast<float*>(p.C) + cbase;
-        constexpr int NIT = 32 * CH / 64;
         f32x4 res[EPI == EPI_RESID ? NIT : 1];
         if constexpr (EPI == EPI_RESID) {
           // every residual piece of the slice in flight before any store
@@ -492,28 +481,41 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, f32x16 (&acc)[TM
         // A slice wholly inside the output stores without per-lane guards:
         // guarded stores each become a branch region of their own, and the
         // LDS reads then wait one by one instead of being in flight together.
-        auto out = [&](auto guardc) __attribute__((always_inline)) {
-          constexpr bool GUARD = decltype(guardc)::value;
+        auto out = [&](auto biasc, auto guardc) __attribute__((always_inline)) {
+          constexpr bool BIAS = decltype(biasc)::value, GUARD = decltype(guardc)::value;
 #pragma unroll
           for (int it = 0; it < NIT; ++it) {
             const int idx = it * 64 + lane, r = idx / CH, ch = idx % CH;
-            const int row = row0 + r, col = col0 + ch * (16 / OBY);
-            const uint32_t oc = static_cast<uint32_t>(r * static_cast<int>(p.ldc) + ch * (16 / OBY));
+            const int row = row0 + r, col = col0 + ch * OPC;
+            const uint32_t oc = static_cast<uint32_t>(r * static_cast<int>(p.ldc) + ch * OPC);
             if (!GUARD || (row < p.M && col < p.N)) {
+              // N is a multiple of 8: a store's columns lie wholly inside or past the edge
+              const int cb = GUARD ? min(col, p.N - OPC) : col;
+              f32x4 w = *(lds_f32x4*)(st + r * PITCH + ch * OPC * 4);
+              if constexpr (BIAS) w += f32x4{p.bias[cb], p.bias[cb + 1], p.bias[cb + 2], p.bias[cb + 3]};
               if constexpr (OUT_BF16) {
                 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-                const u32x4 w = *(__attribute__((address_space(3))) u32x4*)(st + r * PITCH + ch * 16);
-                *reinterpret_cast<u32x4*>(cb16 + oc) = w;
+                f32x4 w2 = *(lds_f32x4*)(st + r * PITCH + ch * OPC * 4 + 16);
+                if constexpr (BIAS)
+                  w2 += f32x4{p.bias[cb + 4], p.bias[cb + 5], p.bias[cb + 6], p.bias[cb + 7]};
+                *reinterpret_cast<u32x4*>(cb16 + oc) =
+                    u32x4{pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]), pack_bf16x2(w2[0], w2[1]),
+                          pack_bf16x2(w2[2], w2[3])};
               } else {
-                f32x4 w = *(__attribute__((address_space(3))) f32x4*)(st + r * PITCH + ch * 16);
                 if constexpr (EPI == EPI_RESID) w = res[it] + w;
                 *reinterpret_cast<f32x4*>(cb32 + oc) = w;
               }
             }
           }
         };
-        if (row0 + 32 <= p.M && col0 + JH * 32 <= p.N) out(std::false_type{});
-        else out(std::true_type{});
+        const bool full = row0 + 32 <= p.M && col0 + JH * 32 <= p.N;
+        if (has_bias) {
+          if (full) out(std::true_type{}, std::false_type{});
+          else out(std::true_type{}, std::true_type{});
+        } else {
+          if (full) out(std::false_type{}, std::false_type{});
+          else out(std::false_type{}, std::true_type{});
+        }
       }
     }
   }

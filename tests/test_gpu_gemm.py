@@ -259,6 +259,33 @@ def test_swiglu(mnk):
     assert torch.all((act.double().cpu() - act_ref).abs() <= tol)
 
 
+@pytest.mark.parametrize("mnk", [(200, 96, 64), (1000, 2400, 576), (4096, 4096, 1152), (4216, 4128, 1216)])
+def test_swiglu_copy_bitwise_and_act_only(mnk):
+    # The gate/up copy is the bf16 rounding of the fp32 product over the
+    # interleaved weight, which the plain fp32 GEMM computes with the same
+    # k16 steps in the same order: equal bits. Without the copy, act is
+    # unchanged. Shapes: the 8-wave 128 x 128 and 256 x 256 kernels, and the
+    # 4-wave kernel with whole and cut edge tiles.
+    M, N, Kd = mnk
+    print("case swiglu copy", mnk, flush=True, file=sys.stderr)
+    x = _rand(M, Kd, seed=61).to(dev())
+    wgu = interleave_gate_up(_rand(N, Kd, seed=62), _rand(N, Kd, seed=63)).to(dev())
+    prod = torch.empty(M, 2 * N, device=dev())
+    K.gemm("nt", x, wgu, prod, M=M, N=2 * N, K=Kd)
+    act = torch.full((M, N), 3.0, dtype=torch.bfloat16, device=dev())
+    gu = torch.full((M, 2 * N), 3.0, dtype=torch.bfloat16, device=dev())
+    K.gemm_swiglu(x, wgu, act, gu)
+    assert torch.equal(gu, prod.to(torch.bfloat16))
+    act2 = torch.full((M, N), 5.0, dtype=torch.bfloat16, device=dev())
+    K.gemm_swiglu(x, wgu, act2)
+    assert torch.equal(act, act2)
+    pc = prod.reshape(M, N // 32, 2, 32)
+    g, u = pc[:, :, 0, :].reshape(M, N), pc[:, :, 1, :].reshape(M, N)
+    act_ref = torch.nn.functional.silu(g) * u
+    # the fast exp and the bf16 rounding of act
+    assert bool(torch.all((act.float() - act_ref).abs() <= act_ref.abs() * 2.0**-7 + 1e-6))
+
+
 def test_nn_over_interleaved_pair_equals_sum():
     """dx = dgu Wgu over the interleaved K = 2N equals dgate Wg + dup Wu."""
     M, N, Kd = 256, 192, 128

@@ -205,8 +205,9 @@ int mr_loss_outlier(const float* pred, const float* target, int64_t n, int64_t k
 
 /*
  * mr_loss_outlier without a workspace argument and without any allocation:
- * its workspace (401,424 bytes: block partials, both radix histograms, the
- * select state) is a static device array of the library, one per GPU, held
+ * its workspace (4,778,016 bytes: block partials, the radix and sample
+ * histograms, the select state and the per-wave candidate lists) is a static
+ * device array of the library, one per GPU, held
  * until the process ends; zero_hist clears what must start at zero on every
  * call. No counterpart in the reference: it is for callers that cannot
  * allocate (code under HIP graph capture, serving loops, harnesses that

@@ -37,7 +37,7 @@ from typing import Any
 from mround_amd.exceptions import ArchitectureError, MemoryBudgetError
 
 GIB = 1 << 30
-LOSS_WORKSPACE = 401_424  # mr_loss_workspace_bytes
+LOSS_WORKSPACE = 4_778_016  # mr_loss_workspace_bytes
 SEQ_ALIGN = 128  # block.SEQ_ALIGN (this module imports no torch at load time)
 _DTYPE_BYTES = {"bfloat16": 2, "float16": 2, "float32": 4}
 

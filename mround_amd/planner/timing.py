@@ -51,23 +51,24 @@ from mround_amd.planner.sensitivity import SENSITIVITY_SAMPLES, SENSITIVITY_SEQ_
 
 __all__ = ["MACHINE", "RULE_VERSION", "SPREAD", "TimePrediction", "predict_run_time", "predict_time"]
 
-RULE_VERSION = "2026-12-02.2"
+RULE_VERSION = "2026-12-02.3"
 MACHINE = "one AMD Instinct MI355X"
 
 # Recorded over predicted seconds of the measurement runs (block loop and
-# scoring pass), lowest and highest.
-SPREAD = (0.83, 1.04)
+# scoring pass), lowest and highest, and of the single-block tunes measured
+# apart in bf16 and split precision (the 0.5B-shaped block: 1.075 and 1.10).
+SPREAD = (0.83, 1.10)
 
 # Fitted constants (seconds), timing_runs.fit.
-_STEP = (4.024e-04, 4.510e-15, 1.540e-14)       # fixed, per token x block weight, per attention flop
-_OUTLIER = 9.044e-13                            # per loss element (tokens x hidden)
-_FORWARD = (8.495e-05, 1.426e-15, 4.737e-15)     # one forward over a batch: the same three terms
-_PIECE = 6.967e-04                               # a step's every piece past the first
-_FORWARD_PIECE = 1.458e-04                       # a forward's every piece past the first
-_SEARCH = (1.355e-02, 4.735e-10)                 # per block: fixed, per block weight
+_STEP = (6.231e-04, 4.364e-15, 1.049e-14)       # fixed, per token x block weight, per attention flop
+_OUTLIER = 0.0                                  # per loss element (tokens x hidden)
+_FORWARD = (1.691e-04, 1.358e-15, 3.585e-15)     # one forward over a batch: the same three terms
+_PIECE = 6.668e-04                               # a step's every piece past the first
+_FORWARD_PIECE = 1.411e-04                       # a forward's every piece past the first
+_SEARCH = (1.433e-02, 4.461e-10)                 # per block: fixed, per block weight
 _COMMIT = 5.0e-4                                # per block
-_SCORING = (9.927e-02, 3.454e-02, 8.859e-10, 1.649e-10)  # fixed, per block, per block weight, per head weight
-_OWN_WIDTH = 2.79
+_SCORING = (9.884e-02, 3.352e-02, 8.995e-10, 1.236e-10)  # fixed, per block, per block weight, per head weight
+_OWN_WIDTH = 2.76
 _SCORING_TOKENS = SENSITIVITY_SAMPLES * SENSITIVITY_SEQ_LEN
 
 def _duration(seconds: float) -> str:
@@ -131,10 +132,11 @@ def _work(model: ModelShape, batch: int, seq_len: int) -> tuple[float, float]:
 
 # Split precision's measured cost over its extra GEMM work: 7B-, 3B- and
 # 0.5B-shaped block tunes (2-bit, 200 steps, 16 batches of 8 x 2048) ran
-# 8.33, 3.13 and 0.83 s against 4.54, 1.75 and 0.53 s in bf16; the extra
-# GEMM work alone predicts 0.55-0.68 of the difference (the rest is the split
+# 7.92, 2.96 and 0.84 s against 4.22, 1.63 and 0.52 s in bf16; the extra
+# GEMM work alone predicts about 0.6 of the difference (the rest is the split
 # operands' writes, the fp32 gate/up pair and W' made in fp32 each step).
-# Scaled by 1.75 the rule puts the three at 0.93, 0.97 and 1.04 of it.
+# Scaled by 1.75 the rule puts the three at 0.93, 0.98 and 1.10 of it (bf16:
+# 1.01, 1.02 and 1.075).
 _SPLIT_EXTRA = 1.75
 
 

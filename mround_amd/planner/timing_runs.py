@@ -170,7 +170,10 @@ def fit(records: list[dict]) -> dict:
     step = np.linalg.lstsq(x, y, rcond=None)[0]
     t_step = lambda f: step[0] + step[1] * f["T"] * f["W"] / 1e12 + step[2] * f["A"] / 1e12
     out = [(st["tune"] / r["iters"] - t_step(f)) / (f["T"] * f["h"]) for r, f, st in std if r["outlier_rule"]]
-    outlier = float(np.median(out))
+    # (a cost, so not below zero: with the one-pass outlier loss the rule's
+    # extra cost is inside the runs' scatter and the median can come out
+    # negative)
+    outlier = max(0.0, float(np.median(out)))
     # one forward pass over a batch (the score, targets and advance passes)
     x = np.array([[1.0, f["T"] * f["W"] / 1e12, f["A"] / 1e12] for r, f, st in std])
     y = np.array([st["score"] / f["nb"] for r, f, st in std])

@@ -47,7 +47,7 @@ def test_every_run_inside_the_spread(r):
 
 
 def test_every_run_but_the_smallest_shape_within_seven_percent():
-    """SmolLM2-135M's small steps run under the rule's fixed part (0.83-0.86):
+    """SmolLM2-135M's small steps run under the rule's fixed part (0.83-0.87):
     the rest of the shapes sit within 7 %."""
     for r in RUNS:
         if r["model"] == "smollm2-135m":
@@ -84,8 +84,8 @@ def test_stages_and_record():
     rec = p.record()
     assert rec["rule"] == TM.RULE_VERSION and rec["spread"] == list(TM.SPREAD)
     assert "MI355X" in p.describe()
-    # a 7B block: about 4.6 s (the bench measures 4.6)
-    assert 4.4 < p.block < 5.0
+    # a 7B block: about 4.2 s (the bench measures 4.15-4.2)
+    assert 3.9 < p.block < 4.5
 
 
 def test_scaling():
@@ -96,10 +96,11 @@ def test_scaling():
     p2 = TM.predict_time(model, base, iters=400, outlier_rule=False)
     p3 = TM.predict_time(model, base, iters=600, outlier_rule=False)
     assert p3.block - p2.block == pytest.approx(p2.block - p.block)
-    # pieces and the outlier rule and the search only add
-    for run, rule in ((RunShape(128, 2048, 8, 64, micro_batches=4), False),
-                      (base, True), (RunShape(128, 2048, 8, 64, searched=True), False)):
-        assert TM.predict_time(model, run, iters=200, outlier_rule=rule).block > p.block
+    # pieces and the search add; the outlier rule never takes away (with the
+    # one-pass outlier loss its fitted extra cost is zero, inside the scatter)
+    for run in (RunShape(128, 2048, 8, 64, micro_batches=4), RunShape(128, 2048, 8, 64, searched=True)):
+        assert TM.predict_time(model, run, iters=200, outlier_rule=False).block > p.block
+    assert TM.predict_time(model, base, iters=200, outlier_rule=True).block >= p.block
     # half the calibration set: the passes halve, the steps do not
     half = TM.predict_time(model, RunShape(64, 2048, 8, 64), iters=200, outlier_rule=False)
     assert half.stages["between_blocks"] == pytest.approx(p.stages["between_blocks"] / 2)
@@ -147,6 +148,6 @@ def test_api_reads_the_config_alone(tmp_path):
     (tmp_path / "config.json").write_text(json.dumps(SHAPES["qwen2.5-7b"]))
     p = api.predict_time(tmp_path, bits=2)
     assert p.blocks == 28 and p.outlier_rule and "scoring" not in p.stages
-    assert 28 * 4.4 < p.stages["blocks"] < 28 * 5.0
+    assert 28 * 3.9 < p.stages["blocks"] < 28 * 4.5
     mixed = api.predict_time(tmp_path, average_bits=2.5)
     assert mixed.scoring_source == "own_width" and mixed.stages["scoring"] > 0

@@ -15,12 +15,12 @@
 //
 // One pass over the data in the common case. A guess comes first: the top
 // bits of the (2 ceil(k / 37) + 64)-th largest key in a sample of a 37th of
-// the elements (every 37th run of 64), from a sample histogram and a select. The first pass then, besides the
-// top-bits histogram, writes the gradient of every element, sums r^2 over the
-// elements whose key lies below the guess (all of them kept whatever the
-// threshold turns out to be, if it is at least the guess) and lists the
-// others, the candidates, per wave (at most kCandCap each, in a fixed order:
-// lanes in order within an iteration). When the guess lies at or below the
+// the elements (every 37th run of 64), from a sample histogram and a select.
+// The first pass then, besides the top-bits histogram, writes the gradient of
+// every element, sums r^2 over the elements whose key lies below the guess
+// (all of them kept whatever the threshold turns out to be, if it is at least
+// the guess) and lists the others, the candidates, per wave (at most
+// kCandCap each, in a fixed order: lanes in order within an iteration). When the guess lies at or below the
 // selected top-bits bin and no wave's list overflowed, every element of that
 // bin and above is a candidate: the low-bits histogram, the exclusion (the
 // candidates at or above the threshold: their gradient set to zero) and the
@@ -32,8 +32,9 @@
 // inputs alone, so equal inputs give equal bits.
 //
 // Sums are deterministic: a fixed grid of blocks, fp64 accumulation per
-// thread (per wave list in list order), a fixed-order block reduction, then
-// one block adding the partials in order.
+// thread (over a candidate list, lane j takes entries j, j + 64, ... in order,
+// then a fixed butterfly), a fixed-order block reduction, then one block
+// adding the partials in order.
 #include <mutex>
 
 #include "mr_common.h"

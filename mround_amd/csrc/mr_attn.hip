@@ -1305,11 +1305,14 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_kv_reduce(const float* __re
 // dQ: queries along lanes; a block owns 128 queries of one query head and
 // walks the key tiles up to its last query, K and V arriving by direct loads,
 // double buffered. dQ^T = K^T dS^T takes K^T from the transposing LDS read.
+// With out non-null it also forms D = rowsum(dO O) of its queries (the bits
+// attn_bwd_dot gives) and writes it to dsum for the dK/dV kernel that follows;
+// else it reads dsum.
 template <int D>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void attn_bwd_dq(
     const uint16_t* __restrict__ qkv, int64_t ld, const uint16_t* __restrict__ dout, int64_t ldo,
-    const float* __restrict__ lse, const float* __restrict__ dsum, int S, int Hq, int Hkv,
-    float scale, uint16_t* __restrict__ dqkv) {
+    const float* __restrict__ lse, float* __restrict__ dsum, int S, int Hq, int Hkv,
+    float scale, uint16_t* __restrict__ dqkv, const uint16_t* __restrict__ out) {
   constexpr int NS = D / 16, ND = D / 32;
   constexpr int TILE = KT * D * 2;
   __shared__ __attribute__((aligned(1024))) uint8_t K0[TILE];
@@ -1330,12 +1333,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   dma_rowtile<D>(qkv, ld, tok0, kcol, K0);
   dma_rowtile<D>(qkv, ld, tok0, vcol, V0);
   const float lse2 = lse[(static_cast<int64_t>(b) * Hq + hq) * S + qi] * kLog2e;
-  const float dq_sum = dsum[(static_cast<int64_t>(b) * Hq + hq) * S + qi];
   bf16x8 qf[NS], of[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     qf[s] = *reinterpret_cast<const bf16x8*>(qkv + (tok0 + qi) * ld + hq * D + s * 16 + h * 8);
     of[s] = *reinterpret_cast<const bf16x8*>(dout + (tok0 + qi) * ldo + hq * D + s * 16 + h * 8);
+  }
+  float dq_sum;
+  if (out) {
+    // attn_bwd_dot's lane `sub` sums the 8 products of dO and O at d = 8 sub
+    // .. 8 sub + 7 in order, then a butterfly over its D / 8 lanes adds the
+    // pieces (sub ^ D/16, ..., sub ^ 1). Here piece sub = 2 s + h is piece s
+    // of this lane: the same sums, the butterfly's steps over s in registers
+    // and its last step (h) across the lane halves. Every lane of a butterfly
+    // ends with the same bits (each pair is added the same way up to order).
+    float pd[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+      const u32x4v a = __builtin_bit_cast(u32x4v, of[s]);
+      const u32x4v o = *reinterpret_cast<const u32x4v*>(out + (tok0 + qi) * ldo + hq * D + s * 16 + h * 8);
+      const uint32_t aw[4] = {a[0], a[1], a[2], a[3]}, ow[4] = {o[0], o[1], o[2], o[3]};
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc += __uint_as_float(aw[k] << 16) * __uint_as_float(ow[k] << 16);
+        acc += __uint_as_float(aw[k] & 0xffff0000u) * __uint_as_float(ow[k] & 0xffff0000u);
+      }
+      pd[s] = acc;
+    }
+#pragma unroll
+    for (int o = NS / 2; o >= 1; o >>= 1)
+#pragma unroll
+      for (int s = 0; s < o; ++s) pd[s] = pd[s] + pd[s + o];
+    dq_sum = pd[0] + __shfl_xor(pd[0], 32, 64);
+    if (h == 0) dsum[(static_cast<int64_t>(b) * Hq + hq) * S + qi] = dq_sum;
+  } else {
+    dq_sum = dsum[(static_cast<int64_t>(b) * Hq + hq) * S + qi];
   }
   f32x16 dq[ND];
 #pragma unroll
@@ -1455,9 +1489,19 @@ int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint1
                int64_t ldo, const float* lse, float* dsum, int B, int S, int Hq, int Hkv,
                float scale, uint16_t* dqkv, int hsplit, float* part, hipStream_t s) {
   const int64_t T = static_cast<int64_t>(B) * S;
-  const int64_t lanes = T * Hq * (D / 8);
-  hipLaunchKernelGGL(attn_bwd_dot<D>, dim3(static_cast<unsigned>((lanes + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, s, dout, out, ldo, T, S, Hq, dsum);
+  // The dQ kernel forms D = rowsum(dO O) and leaves it in dsum for the dK/dV
+  // kernel, which therefore runs second. MR_ATTN_DOT=1: D by attn_bwd_dot
+  // first and dQ last, as before (the same bits, for comparisons).
+  const char* e = getenv("MR_ATTN_DOT");
+  const bool dot_first = e && e[0] == '1';
+  if (dot_first) {
+    const int64_t lanes = T * Hq * (D / 8);
+    hipLaunchKernelGGL(attn_bwd_dot<D>, dim3(static_cast<unsigned>((lanes + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, s, dout, out, ldo, T, S, Hq, dsum);
+  } else {
+    hipLaunchKernelGGL(attn_bwd_dq<D>, dim3(Hq, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
+                       lse, dsum, S, Hq, Hkv, scale, dqkv, out);
+  }
   const int64_t W = 2 * static_cast<int64_t>(Hkv) * D;
   if (hsplit == 1) part = nullptr;
   if constexpr (D == 128) {
@@ -1475,8 +1519,9 @@ int launch_bwd(const uint16_t* qkv, int64_t ld, const uint16_t* out, const uint1
     hipLaunchKernelGGL(attn_bwd_kv_reduce, dim3(static_cast<unsigned>((threads + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, s, part, hsplit, T, W, static_cast<int64_t>(Hq) * D, dqkv, ld);
   }
-  hipLaunchKernelGGL(attn_bwd_dq<D>, dim3(Hq, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
-                     lse, dsum, S, Hq, Hkv, scale, dqkv);
+  if (dot_first)
+    hipLaunchKernelGGL(attn_bwd_dq<D>, dim3(Hq, B, S / QB), dim3(kThreads), 0, s, qkv, ld, dout, ldo,
+                       lse, dsum, S, Hq, Hkv, scale, dqkv, static_cast<const uint16_t*>(nullptr));
   MR_LAUNCH_CHECK("mr_attn_bwd");
   return MR_OK;
 }

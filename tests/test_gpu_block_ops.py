@@ -217,6 +217,33 @@ def test_attention_dkdv_pipeline_matches_pair(case):
     assert torch.equal(got, ref), "pipelined and pair dK/dV kernels differ"
 
 
+class _DotFirst:
+    """Attention backward launches inside the block form D = rowsum(dO O) with
+    the separate attn_bwd_dot kernel first and run dQ last."""
+
+    def __enter__(self):
+        os.environ["MR_ATTN_DOT"] = "1"
+
+    def __exit__(self, *exc):
+        del os.environ["MR_ATTN_DOT"]
+
+
+@pytest.mark.parametrize("case", PIPE_CASES + [(2, 256, 4, 2, 64, 1), (1, 384, 8, 2, 64, 2)])
+def test_attention_dq_forms_the_row_sums(case):
+    # The dQ kernel forms D itself (the dot kernel's products and sums in the
+    # same order), writes it for the dK/dV kernel and runs first: dQ, dK and
+    # dV bit-identical to the separate dot kernel's order, at D = 64 and 128,
+    # with head splits, and the 7B launch.
+    B, S, Hq, Hkv, D, hsplit = case
+    print("case attn bwd row sums in dQ", case, flush=True, file=sys.stderr)
+    qkv, ld = _attn_inputs(B, S, Hq, Hkv, D, 1.5, seed=34, pad=16)
+    dout = torch.randn(B * S, Hq * D, generator=_gen(35)).to(torch.bfloat16)
+    got = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=hsplit)
+    with _DotFirst():
+        ref = _run_attention(qkv, B, S, Hq, Hkv, D, dout, ld, hsplit=hsplit)
+    assert torch.equal(got, ref), "the row sums formed in dQ differ from the dot kernel's"
+
+
 def test_attention_head_splits_agree():
     """The split changes only the order dK/dV partials are summed in: every
     split of one problem agrees within a few bf16 units (dQ is bit-identical)."""

@@ -407,7 +407,9 @@ int mr_rope_split(const float* x, int64_t ldx, int64_t T, int S, int n_rope_head
  * hsplit = 0 picks the split automatically (more blocks when fewer than 512
  * blocks of 128 keys would run, Hkv * B * S / 128, within the workspace
  * given; query the size with hsplit = 0); 1..G forces it and refuses a
- * workspace too small for it. The scaled-dot-product attention of the
+ * workspace too small for it. Outputs that share memory with the inputs
+ * (out with qkv; dqkv or dsum_ws with qkv, out, dout or each other) are
+ * refused with MR_EINVAL. The scaled-dot-product attention of the
  * mlx-lm block (mround/pipeline/blocks.py:605) and its autodiff.
  */
 int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int head_dim,

@@ -1540,6 +1540,15 @@ int check(const char* fn, const void* qkv, int64_t ld, int B, int S, int Hq, int
   return MR_OK;
 }
 
+// Byte span of `rows` rows of `width` bf16 values at leading dimension ld.
+int64_t span(int64_t rows, int64_t ld, int64_t width) { return ((rows - 1) * ld + width) * 2; }
+
+// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte.
+bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + static_cast<uintptr_t>(nb) && y < x + static_cast<uintptr_t>(na);
+}
+
 }  // namespace
 }  // namespace mr
 
@@ -1552,6 +1561,10 @@ int mr_attn_fwd(const void* qkv, int64_t ld, int B, int S, int Hq, int Hkv, int 
   int rc = check("mr_attn_fwd", qkv, ld, B, S, Hq, Hkv, head_dim, ldo);
   if (rc) return rc;
   if (!out || !lse || !aligned16(out)) return fail(MR_EINVAL, "mr_attn_fwd: bad output");
+  const int64_t T = static_cast<int64_t>(B) * S;
+  if (overlap(out, span(T, ldo, static_cast<int64_t>(Hq) * head_dim), qkv,
+              span(T, ld, static_cast<int64_t>(Hq + 2 * Hkv) * head_dim)))
+    return fail(MR_EINVAL, "mr_attn_fwd: out must not overlap qkv");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* q = static_cast<const uint16_t*>(qkv);
   uint16_t* o = static_cast<uint16_t*>(out);
@@ -1571,6 +1584,15 @@ int mr_attn_fwd_split(const void* qkv_hi, const void* qkv_lo, int64_t ld, int B,
     return fail(MR_EINVAL, "mr_attn_fwd_split: bad output");
   if (ld_split < 3ll * Hq * head_dim || ld_split % 8)
     return fail(MR_EINVAL, "mr_attn_fwd_split: out_split rows must hold 3 Hq head_dim values (ld a multiple of 8)");
+  {
+    const int64_t T = static_cast<int64_t>(B) * S;
+    const int64_t n_qkv = span(T, ld, static_cast<int64_t>(Hq + 2 * Hkv) * head_dim);
+    const int64_t n_o = span(T, ldo, static_cast<int64_t>(Hq) * head_dim);
+    const int64_t n_s = span(T, ld_split, 3ll * Hq * head_dim);
+    if (overlap(out, n_o, qkv_hi, n_qkv) || overlap(out, n_o, qkv_lo, n_qkv) || overlap(out_split, n_s, qkv_hi, n_qkv) ||
+        overlap(out_split, n_s, qkv_lo, n_qkv) || overlap(out, n_o, out_split, n_s))
+      return fail(MR_EINVAL, "mr_attn_fwd_split: out and out_split must not overlap qkv or each other");
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* qh = static_cast<const uint16_t*>(qkv_hi);
   const uint16_t* ql = static_cast<const uint16_t*>(qkv_lo);
@@ -1599,6 +1621,19 @@ int mr_attn_bwd(const void* qkv, int64_t ld, const void* out, const void* dout, 
   if (!out || !dout || !lse || !dsum_ws || !dqkv || !aligned16(out) || !aligned16(dout) ||
       !aligned16(dqkv))
     return fail(MR_EINVAL, "mr_attn_bwd: bad argument");
+  {
+    // dQ is written while the dK/dV kernel, launched after it, still reads
+    // q, k, v, O and dO, and the row sums while the dQ kernel reads them:
+    // the outputs must not share memory with the inputs or each other
+    const int64_t T = static_cast<int64_t>(B) * S;
+    const int64_t n_qkv = span(T, ld, static_cast<int64_t>(Hq + 2 * Hkv) * head_dim);
+    const int64_t n_o = span(T, ldo, static_cast<int64_t>(Hq) * head_dim);
+    const int64_t n_sum = T * Hq * static_cast<int64_t>(sizeof(float));
+    if (overlap(dqkv, n_qkv, qkv, n_qkv) || overlap(dqkv, n_qkv, out, n_o) || overlap(dqkv, n_qkv, dout, n_o) ||
+        overlap(dsum_ws, n_sum, qkv, n_qkv) || overlap(dsum_ws, n_sum, out, n_o) ||
+        overlap(dsum_ws, n_sum, dout, n_o) || overlap(dsum_ws, n_sum, dqkv, n_qkv))
+      return fail(MR_EINVAL, "mr_attn_bwd: dqkv and dsum_ws must not overlap qkv, out, dout or each other");
+  }
   const int G = Hq / Hkv;
   if (hsplit < 0 || hsplit > G)
     return fail(MR_EINVAL, "mr_attn_bwd: hsplit %d outside [0, %d] (0 = automatic)", hsplit, G);

@@ -164,10 +164,41 @@ def test_attention_workspace_follows_the_head_split(lib):
 
 def test_attention_backward_refuses_a_bad_split(lib):
     P = ctypes.c_void_p
-    args = (P(256), 2304, P(256), P(256), 1792, P(256), P(256), 1, 256, 14, 2, 128, 0.1, P(256))
+    # (distinct, non-overlapping buffers: qkv, out, dout, lse, dsum, dqkv)
+    args = (P(1 << 30), 2304, P(2 << 30), P(3 << 30), 1792, P(4 << 30), P(5 << 30), 1, 256, 14, 2, 128, 0.1,
+            P(6 << 30))
     # more blocks per kv head than the group has query heads
     assert lib.mr_attn_bwd(*args, 8, None, 0, None) == -22
     assert b"hsplit" in lib.mr_last_error()
     # a forced split without room for its partials
     assert lib.mr_attn_bwd(*args, 2, P(256), 1024, None) == -22
     assert b"workspace" in lib.mr_last_error()
+
+
+def test_attention_refuses_outputs_that_overlap_inputs(lib):
+    P = ctypes.c_void_p
+    T, ld, ldo = 256, 2304, 1792  # one sequence of 256, 14 / 2 heads of 128
+    qkv, out, dout, lse, dsum, dqkv = (P(k << 30) for k in range(1, 7))
+    last_row = (T - 1) * ld * 2  # byte offset of qkv's last row
+
+    def bwd(**kw):
+        a = dict(qkv=qkv, out=out, dout=dout, dsum=dsum, dqkv=dqkv)
+        a.update(kw)
+        return lib.mr_attn_bwd(a["qkv"], ld, a["out"], a["dout"], ldo, lse, a["dsum"], 1, T, 14, 2, 128, 0.1,
+                               a["dqkv"], 1, None, 0, None)
+
+    for kw in (dict(dqkv=qkv), dict(dqkv=P((1 << 30) + last_row)), dict(dqkv=out), dict(dqkv=dout),
+               dict(dsum=qkv), dict(dsum=out), dict(dsum=dout), dict(dsum=dqkv)):
+        assert bwd(**kw) == -22, kw
+        assert b"overlap" in lib.mr_last_error()
+    # the forward's output against qkv: inside it, and starting in its last 16 bytes
+    assert lib.mr_attn_fwd(qkv, ld, 1, T, 14, 2, 128, 0.1, P((1 << 30) + 4096), ldo, lse, None) == -22
+    assert b"overlap" in lib.mr_last_error()
+    end = (1 << 30) + last_row + (14 + 4) * 128 * 2
+    assert lib.mr_attn_fwd(qkv, ld, 1, T, 14, 2, 128, 0.1, P(end - 16), ldo, lse, None) == -22
+    # the split forward: its two outputs against the hi and lo halves and each other
+    hi, lo, o, osp = P(1 << 30), P(2 << 30), P(3 << 30), P(4 << 30)
+    for a in ((hi, lo, hi, osp), (hi, lo, o, lo), (hi, lo, o, o)):
+        assert lib.mr_attn_fwd_split(a[0], a[1], ld, 1, T, 14, 2, 128, 0.1, a[2], ldo, a[3], 3 * 14 * 128,
+                                     lse, None) == -22, a
+        assert b"overlap" in lib.mr_last_error()

@@ -194,7 +194,8 @@ int mr_to_affine(const float* scale, const float* zp, int64_t n_groups, int bits
  * where threshold is the k-th largest |r| over the n elements (exact radix
  * select on the float bit pattern; every element tied at the threshold is
  * excluded), unless threshold_in is non-NULL. loss_out and threshold_out are
- * device scalars; grad_out may be NULL.
+ * device scalars; grad_out may be NULL. When the threshold is computed,
+ * grad_out must not overlap pred or target (refused with MR_EINVAL).
  */
 size_t mr_loss_workspace_bytes(int64_t n);
 int mr_loss_mse(const float* pred, const float* target, int64_t n, int64_t denom,
@@ -283,7 +284,10 @@ int mr_embed_rows(const void* table, int dtype, int64_t V, int64_t H, int64_t ld
  * the caller's workspace: mr_gemm_workspace_bytes(M, N, K) bytes (0 when the
  * shape is not split; N is the product's width, 2N for mr_gemm_swiglu), at
  * most 128 MB, 16-byte aligned. A NULL or smaller workspace narrows or
- * drops the split: the same product, summed in another order. Replaces the
+ * drops the split: the same product, summed in another order. Outputs and
+ * the workspace must not overlap the operands or each other (refused with
+ * MR_EINVAL); C may be resid itself (same pointer and leading dimension), and
+ * mr_gemm_swiglu_bwd's dgu may be its gu. Replaces the
  * matmul of the reference's tunable linear, `x @ weight.T`
  * (mround/pipeline/runner.py:364-368), and the two products MLX autodiff
  * forms for its backward.

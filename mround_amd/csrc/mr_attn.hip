@@ -1543,12 +1543,6 @@ int check(const char* fn, const void* qkv, int64_t ld, int B, int S, int Hq, int
 // Byte span of `rows` rows of `width` bf16 values at leading dimension ld.
 int64_t span(int64_t rows, int64_t ld, int64_t width) { return ((rows - 1) * ld + width) * 2; }
 
-// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte.
-bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
-  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
-  return x < y + static_cast<uintptr_t>(nb) && y < x + static_cast<uintptr_t>(na);
-}
-
 }  // namespace
 }  // namespace mr
 

@@ -198,6 +198,11 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) {
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Whether the byte ranges [a, a + na) and [b, b + nb) share a byte.
+inline bool overlap(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + static_cast<uintptr_t>(nb) && y < x + static_cast<uintptr_t>(na);
+}
 
 // f(integral_constant<int, I>) for I = B .. E-1, unrolled by the front end.
 template <int B, int E>

@@ -1248,6 +1248,38 @@ bool set_workspace(GemmParams& p, void* ws, size_t bytes) {
 }  // namespace
 }  // namespace mr
 
+namespace mr {
+namespace {
+
+// Bytes from the first element of a rows x width matrix (leading dimension
+// ld, esize-byte elements) to one past its last.
+int64_t span_bytes(int64_t rows, int64_t ld, int64_t width, int64_t esize) {
+  return ((rows - 1) * ld + width) * esize;
+}
+
+// A region the launch writes (outputs, k-split partials) against the regions
+// it reads: tiles read operand panels while other tiles write, so any shared
+// byte changes results. Each pair is (pointer, bytes); null pointers are
+// skipped. Returns whether any written region overlaps any other region.
+struct Region {
+  const void* p;
+  int64_t n;
+};
+template <int NW, int NR>
+bool writes_overlap(const Region (&w)[NW], const Region (&r)[NR]) {
+  for (int a = 0; a < NW; ++a) {
+    if (!w[a].p) continue;
+    for (int b = 0; b < NR; ++b)
+      if (r[b].p && overlap(w[a].p, w[a].n, r[b].p, r[b].n)) return true;
+    for (int b = a + 1; b < NW; ++b)
+      if (w[b].p && overlap(w[a].p, w[a].n, w[b].p, w[b].n)) return true;
+  }
+  return false;
+}
+
+}  // namespace
+}  // namespace mr
+
 extern "C" {
 
 size_t mr_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
@@ -1280,6 +1312,16 @@ int mr_gemm(int layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
     const bool a_kmajor = layout != 2, b_kmajor = layout == 0;
     if (lda < (a_kmajor ? K : M) || ldb < (b_kmajor ? K : N) || ldc < N || (resid && ldr < N))
       return fail(MR_EINVAL, "mr_gemm: a leading dimension is smaller than its row");
+    // C may be the residual itself (same place, same rows), nothing else it reads
+    const int64_t nc = span_bytes(M, ldc, N, c_dtype == MR_BF16 ? 2 : 4);
+    const bool in_place = resid == C && ldr == ldc;
+    const Region w[2] = {{C, nc}, {workspace, static_cast<int64_t>(workspace_bytes)}};
+    const Region r[3] = {{A, a_kmajor ? span_bytes(M, lda, K, 2) : span_bytes(K, lda, M, 2)},
+                         {B, b_kmajor ? span_bytes(N, ldb, K, 2) : span_bytes(K, ldb, N, 2)},
+                         {in_place ? nullptr : resid, resid ? span_bytes(M, ldr, N, 4) : 0}};
+    if (writes_overlap(w, r) || (in_place && workspace && overlap(workspace, workspace_bytes, C, nc)))
+      return fail(MR_EINVAL, "mr_gemm: C and the workspace must not overlap A, B, the residual (unless C is "
+                  "the residual itself) or each other");
   }
   GemmParams p{};
   p.M = static_cast<int>(M);
@@ -1326,6 +1368,13 @@ int mr_gemm_swiglu(int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, 
   if (ldx < K || ldw < K || ldact < N || (gu && ldgu < 2 * N) || ldx > kMaxLd || ldw > kMaxLd ||
       ldact > kMaxLd || (gu && ldgu > kMaxLd))
     return fail(MR_EINVAL, "mr_gemm_swiglu: bad leading dimension");
+  {
+    const Region w[3] = {{act, span_bytes(M, ldact, N, 2)}, {gu, gu ? span_bytes(M, ldgu, 2 * N, 2) : 0},
+                         {workspace, static_cast<int64_t>(workspace_bytes)}};
+    const Region r[2] = {{X, span_bytes(M, ldx, K, 2)}, {Wgu, span_bytes(2 * N, ldw, K, 2)}};
+    if (writes_overlap(w, r))
+      return fail(MR_EINVAL, "mr_gemm_swiglu: act, gu and the workspace must not overlap X, Wgu or each other");
+  }
   GemmParams p{};
   p.M = static_cast<int>(M);
   p.N = static_cast<int>(2 * N);
@@ -1359,6 +1408,17 @@ int mr_gemm_swiglu_bwd(int64_t M, int64_t N, int64_t K, const void* dd, int64_t 
   if (ldd < K || ldw < N || lddgu < 2 * N || ldd > kMaxLd || ldw > kMaxLd || lddgu > kMaxLd)
     return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: bad leading dimension");
   if (ldgu != lddgu) return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: gu and dgu must share a layout");
+  {
+    // dgu may be written over gu itself: each piece of gu is read before the
+    // same piece of dgu is written, by the same lane
+    const int64_t ng = span_bytes(M, ldgu, 2 * N, 2);
+    const Region w[2] = {{dgu, ng}, {workspace, static_cast<int64_t>(workspace_bytes)}};
+    const Region r[3] = {{dd, span_bytes(M, ldd, K, 2)}, {Wd, span_bytes(K, ldw, N, 2)},
+                         {dgu == gu ? nullptr : gu, ng}};
+    if (writes_overlap(w, r) || (dgu == gu && workspace && overlap(workspace, workspace_bytes, gu, ng)))
+      return fail(MR_EINVAL, "mr_gemm_swiglu_bwd: dgu and the workspace must not overlap dd, Wd, gu (unless dgu "
+                  "is gu itself) or each other");
+  }
   GemmParams p{};
   p.M = static_cast<int>(M);
   p.N = static_cast<int>(N);

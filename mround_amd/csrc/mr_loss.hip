@@ -459,6 +459,11 @@ int outlier(const char* fn, const float* pred, const float* target, int64_t n, i
                 static_cast<long long>(n), static_cast<long long>(kMaxElements));
   if (grad_out && (n % 4) == 0 && !aligned16(grad_out))
     return fail(MR_EINVAL, "%s: gradient must be 16-byte aligned", fn);
+  // the select's later passes read pred and target again after the first
+  // pass has written the gradient
+  if (!threshold_in && grad_out &&
+      (overlap(grad_out, n * 4, pred, n * 4) || overlap(grad_out, n * 4, target, n * 4)))
+    return fail(MR_EINVAL, "%s: grad_out must not overlap pred or target", fn);
   const int grid = grid_for(n);
   const float gscale = static_cast<float>(2.0 / static_cast<double>(denom));
   if (!threshold_in) {

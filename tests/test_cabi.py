@@ -78,6 +78,11 @@ def test_host_validation_refuses_before_launch(lib):
     # loss with an out-of-range rank
     rc = lib.mr_loss_outlier(P(16), P(16), 100, 0, 100, None, None, P(16), None, P(16), None)
     assert rc == -22 and b"rank" in lib.mr_last_error()
+    # a gradient written over the residual's inputs, which the select reads again
+    for grad in (P(1 << 20), P((2 << 20) + 384)):
+        rc = lib.mr_loss_outlier(P(1 << 20), P(2 << 20), 100, 1, 100, None, None, P(3 << 20), grad, P(4 << 20),
+                                 None)
+        assert rc == -22 and b"overlap" in lib.mr_last_error()
     # DeltaLoss with too many widths
     arr = (ctypes.c_int * 9)(*range(9))
     rc = lib.mr_delta_loss(P(16), 1, P(16), 4, 64, 64, arr, 9, 0, 1e-8, P(16), P(16), None)
@@ -100,10 +105,21 @@ def test_host_validation_refuses_before_launch(lib):
     for gu, ldgu, dgu in ((P(264), 128, P(256)), (P(256), 128, P(264)), (P(256), 132, P(256))):
         rc = lib.mr_gemm_swiglu_bwd(64, 64, 64, P(256), 64, P(256), 64, gu, ldgu, dgu, ldgu, None, 0, None)
         assert rc == -22 and b"16-byte" in lib.mr_last_error()
+    # outputs and the k-split workspace against the operands (64 x 64 x 64, fp32 C: 16 KB)
+    A, B_, C = P(1 << 20), P(2 << 20), P(3 << 20)
+    for c, ws, resid in ((A, None, None), (P((2 << 20) + 8000), None, None), (C, P((3 << 20) + 1024), None),
+                         (C, A, None), (C, None, P((3 << 20) + 256))):
+        rc = lib.mr_gemm(0, 64, 64, 64, A, 64, B_, 64, c, MR_F32, 64, None, resid, 64, ws, 4096 if ws else 0,
+                         None)
+        assert rc == -22 and b"overlap" in lib.mr_last_error(), (c, ws, resid)
+    rc = lib.mr_gemm_swiglu(64, 64, 64, A, 64, B_, 64, P(3 << 20), 64, P((3 << 20) + 4096), 128, None, 0, None)
+    assert rc == -22 and b"overlap" in lib.mr_last_error()
+    rc = lib.mr_gemm_swiglu_bwd(64, 64, 64, A, 64, B_, 64, P(3 << 20), 128, P((3 << 20) + 512), 128, None, 0,
+                                None)
+    assert rc == -22 and b"overlap" in lib.mr_last_error()
     # a misaligned k-split workspace
-    rc = lib.mr_gemm(0, 64, 64, 64, P(256), 64, P(256), 64, P(256), MR_F32, 64, None, None, 0, P(264), 1024,
-                     None)
-    assert rc == -22 and b"workspace" in lib.mr_last_error()
+    rc = lib.mr_gemm(0, 64, 64, 64, A, 64, B_, 64, C, MR_F32, 64, None, None, 0, P((4 << 20) + 8), 1024, None)
+    assert rc == -22 and b"workspace must be 16-byte aligned" in lib.mr_last_error()
 
 
 def test_split_entry_points_refuse_bad_arguments(lib):

@@ -316,7 +316,7 @@ __global__ __launch_bounds__(kHistThreads) void radix_hist_lo(const float* __res
 __global__ __launch_bounds__(kSelThreads) void radix_select(int hi, Workspace* ws,
                                                             float* __restrict__ threshold_out,
                                                             uint32_t ks) {
-  __shared__ uint32_t above[kSelThreads];
+  __shared__ uint32_t wave_total[kSelThreads / 64];
   __shared__ uint32_t win[2];  // owner thread, count strictly above its bins
   const uint32_t* hist = hi == 2 ? ws->hist_s : hi ? ws->hist_hi : ws->hist_lo;
   const int per = (hi ? kHiBins : kLoBins) / kSelThreads;  // 32 or 64
@@ -327,17 +327,19 @@ __global__ __launch_bounds__(kSelThreads) void radix_select(int hi, Workspace* w
     const uint4 v = h4[j];
     mine += v.x + v.y + v.z + v.w;
   }
-  // suffix sums over threads, by doubling
-  above[t] = mine;
-  __syncthreads();
-  for (int off = 1; off < kSelThreads; off <<= 1) {
-    const uint32_t add = t + off < kSelThreads ? above[t + off] : 0u;
-    __syncthreads();
-    above[t] += add;
-    __syncthreads();
+  // suffix sums over threads: within each wave by shuffles, then the totals
+  // of the waves above (integer sums, so the order does not matter)
+  uint32_t above = mine;
+  const int lane_t = t & 63, wave_t = t >> 6;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t v = __shfl_down(above, off, 64);
+    if (lane_t + off < 64) above += v;
   }
+  if (lane_t == 0) wave_total[wave_t] = above;
+  __syncthreads();
+  for (int w = wave_t + 1; w < kSelThreads / 64; ++w) above += wave_total[w];
   const uint32_t k = hi == 2 ? ks : ws->state[1];
-  const uint32_t run0 = above[t] - mine;  // strictly above thread t's bins
+  const uint32_t run0 = above - mine;  // strictly above thread t's bins
   if (run0 < k && k <= run0 + mine) {
     win[0] = static_cast<uint32_t>(t);
     win[1] = run0;
